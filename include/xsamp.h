@@ -1,0 +1,176 @@
+/*
+ * xsamp.h -- C ABI of the MI355X (gfx950) token sampler for xwen.
+ *
+ * One shared library (xwen_amd/libxsamp.so) exports these entry points.  Every
+ * signature uses plain C types and pointers; no exceptions cross the ABI.  The
+ * device buffers are HIP device pointers owned by the caller; the library only
+ * borrows them for the duration of the (asynchronous) call on the context's
+ * stream.
+ *
+ * Reference interface each entry point replaces (0rvar/xwen):
+ *   xs_create / xs_destroy      Sampler::new                   src/sampler.rs:130-149
+ *   xs_sample                   Sampler::sample_controlled     src/sampler.rs:190-232
+ *                               + Sampler::draw                src/sampler.rs:235-243
+ *                               (allow-mask: SampleControl::allowed, src/sampler.rs:87-93,
+ *                                apply_control src/sampler.rs:433-448)
+ *                               + held_row / last_logprobs_for src/generate.rs:1871-1933
+ *   xs_verify                   accept_drafts                  src/generate.rs:4020-4046
+ *                               over the verify block          src/generate.rs:2410-2461
+ *   xs_keep_confident           keep_confident                 src/generate.rs:3898-3905
+ *
+ * Randomness: the reference draws from a seeded StdRng inside the sampler.  Here
+ * the caller supplies one uniform per sampled row, u = j * 2^-23 with j in
+ * [0, 2^23) -- exactly the f32 rand 0.9's UniformFloat derives from 23 random
+ * bits -- so the draw is a pure function of (logits, options, u).  Greedy rows
+ * ignore their uniform, as the reference's greedy path never touches the RNG.
+ *
+ * Threading: a context is owned by one thread at a time and its calls are
+ * serialised on its stream (the reference's Sampler is `&mut self`).  Two
+ * contexts are independent.
+ */
+#ifndef XSAMP_H
+#define XSAMP_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Return codes of the API calls (launch/argument errors, not data errors). */
+#define XS_OK 0
+#define XS_ERR_ARG (-1)      /* null pointer, bad size, misaligned row */
+#define XS_ERR_HIP (-2)      /* a HIP runtime call failed */
+#define XS_ERR_CAPACITY (-3) /* more rows / wider rows / larger k than the context holds */
+
+/* Per-row data status, written to the `status` output.  The numbering matches
+ * the reference's error conditions:
+ *   XS_ROW_NAN         a NaN reached the draw (sampler.rs:268-286, :360-373)
+ *   XS_ROW_NO_FINITE   nothing finite left after the controls (:483-488), or no
+ *                      logit above -inf on the greedy path (:285)
+ *   XS_ROW_MASK_SHORT  allow-mask narrower than the encodable ids (:437-442)
+ *   XS_ROW_FORCE_OOR   forced id outside the vocabulary (:472-477); reserved
+ *   XS_ROW_ZERO_WEIGHT WeightedIndex saw no probability mass (:238-240)
+ *   XS_ROW_NARROW      logit row narrower than the encodable bound (:196-200)
+ *   XS_ROW_BAD_PARAM   top_k larger than the context's k_max (no reference
+ *                      counterpart: the reference has no such limit)        */
+#define XS_ROW_OK 0
+#define XS_ROW_NAN 1
+#define XS_ROW_NO_FINITE 2
+#define XS_ROW_MASK_SHORT 3
+#define XS_ROW_FORCE_OOR 4
+#define XS_ROW_ZERO_WEIGHT 5
+#define XS_ROW_NARROW 6
+#define XS_ROW_BAD_PARAM 7
+
+/* Largest top_k a context supports (the selection keeps top_k + 1 entries). */
+#define XS_K_MAX 127
+/* Largest number of held_row log-probs per row. */
+#define XS_TOP_MAX 128
+
+typedef struct xs_context xs_context;
+
+/* SamplerOptions (sampler.rs:36-41) minus the seed, one per row.
+ * Sampler::new (sampler.rs:133-145): temperature <= 0 or top_k <= 1 is greedy;
+ * otherwise top-k then top-p at this temperature.  top_p is the f32 the
+ * reference stores (`top_p as f32`, sampler.rs:139). */
+typedef struct {
+  double temperature;
+  int32_t top_k;
+  float top_p;
+} xs_row_params;
+
+/* Sampler::new's allocation side: a context on `device` for up to `max_rows`
+ * rows of up to `vocab` encodable ids and top_k <= k_max (<= XS_K_MAX).
+ * Allocates the device workspace once; calls allocate nothing afterwards. */
+int xs_create(int device, int64_t max_rows, int64_t vocab, int32_t k_max, xs_context** out);
+int xs_destroy(xs_context* ctx);
+/* Bind the hipStream_t the context's kernels run on (NULL = the null stream). */
+int xs_set_stream(xs_context* ctx, void* hip_stream);
+
+/* One batched Sampler::sample_controlled + draw over `rows` independent rows.
+ * All pointers are device pointers.  Required: logits, params, uniforms, token,
+ * status.  Everything else may be NULL. */
+typedef struct {
+  const float* logits;   /* [rows, ld] row-major f32; 16-byte aligned, ld % 4 == 0 */
+  int64_t rows;
+  int64_t ld;            /* row stride in floats (>= width) */
+  int64_t width;         /* logit row width; width < enc is XS_ROW_NARROW for every row */
+  int64_t enc;           /* encodable ids: the draw is over ids [0, enc) (sampler.rs:191-201) */
+  const xs_row_params* params; /* [rows] */
+  const float* uniforms;       /* [rows], each j * 2^-23 */
+  /* SampleControl::allowed: packed allow-mask, bit t%32 of word t/32 set means
+   * id t may be drawn (sampler.rs:87-93).  NULL = no control (the reference's
+   * no-op fast path).  allowed_words * 32 < enc is XS_ROW_MASK_SHORT. */
+  const uint32_t* allowed; /* [rows, allowed_ld] */
+  int64_t allowed_words;
+  int64_t allowed_ld;
+  /* outputs */
+  int32_t* token;        /* [rows] sampled id (-1 on a row error) */
+  int32_t* status;       /* [rows] XS_ROW_* */
+  int32_t* cand_id;      /* [rows, cand_ld] the candidate set in draw order, or NULL */
+  float* cand_w;         /* [rows, cand_ld] post-top-p weights (zeros included), or NULL */
+  int32_t* n_cand;       /* [rows] candidates written (0 on greedy rows), or NULL */
+  int64_t cand_ld;       /* >= min(top_k, enc) of every row that writes candidates */
+  float* soft_max;       /* [rows] max of the scaled, controlled row, or NULL */
+  float* soft_sum;       /* [rows] softmax denominator used, or NULL */
+  /* held_row statistics over the raw logits (generate.rs:1905-1933), no
+   * allow-mask allowed with these: row_max, ln-sum-exp in f64, and the n_top
+   * highest logits (ties to the lower id) as log-probs v - lse. */
+  float* row_max;        /* [rows] or NULL */
+  double* row_lse;       /* [rows] or NULL (NaN where held_row errors) */
+  int32_t n_top;         /* 0..XS_TOP_MAX */
+  int32_t* top_id;       /* [rows, top_ld] or NULL */
+  float* top_logprob;    /* [rows, top_ld] or NULL */
+  int64_t top_ld;
+} xs_sample_args;
+
+int xs_sample(xs_context* ctx, const xs_sample_args* args);
+
+/* The speculative verify block: `seqs` sequences of `span` = D + 1 rows each
+ * (D drafts plus the bonus position), laid out [seqs, span, ld].  Every row is
+ * sampled as xs_sample would, with its own uniform; then each sequence runs
+ * accept_drafts (generate.rs:4020-4046): walk i = 0..span-1, stop before a row
+ * once `budget` tokens are committed, commit the sampled token, count it as
+ * accepted while it equals drafts[i] (i < D), stop at the first mismatch or at
+ * an end-of-generation id.  Because every row has its own uniform, sampling
+ * all rows first and walking afterwards is the same walk. */
+typedef struct {
+  const float* logits;   /* [seqs * span, ld] */
+  int64_t seqs;
+  int64_t span;          /* D + 1, >= 1 */
+  int64_t ld, width, enc;
+  const xs_row_params* params;  /* [seqs * span] */
+  const float* uniforms;        /* [seqs * span] */
+  const uint32_t* allowed;      /* [seqs * span, allowed_ld] or NULL (per-position masks) */
+  int64_t allowed_words, allowed_ld;
+  const int32_t* drafts;        /* [seqs, span - 1] */
+  const int32_t* budget;        /* [seqs] max committed tokens, or NULL = unbounded */
+  int32_t n_eog;                /* 0..8 end-of-generation ids (Sampler::is_eog) */
+  int32_t eog[8];
+  /* outputs */
+  int32_t* row_token;    /* [seqs * span] every row's sampled id */
+  int32_t* row_status;   /* [seqs * span] */
+  int32_t* accepted;     /* [seqs] m: matched drafts */
+  int32_t* committed;    /* [seqs, span] committed ids (accepted drafts then the bonus) */
+  int32_t* n_committed;  /* [seqs] */
+  int32_t* seq_status;   /* [seqs] the first row error the walk reached, else XS_ROW_OK */
+} xs_verify_args;
+
+int xs_verify(xs_context* ctx, const xs_verify_args* args);
+
+/* keep_confident (generate.rs:3898-3905), host memory: the length of the
+ * longest prefix whose probabilities are all >= p_min (a NaN ends it). */
+int64_t xs_keep_confident(const float* probs, int64_t n, float p_min);
+
+/* Library version string. */
+const char* xs_version(void);
+
+/* Test hook (no reference counterpart): y[i] = the kernels' correctly rounded
+ * binary32 exp of x[i], device pointers, on `hip_stream`.  The parity tests use
+ * it to compare the device exp with the CPU oracle's over millions of inputs. */
+int xs_test_exp(const float* x, float* y, int64_t n, void* hip_stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -60,6 +60,10 @@ def lib():
         L = C.CDLL(LIB_PATH)
         L.xo_exp.restype = C.c_float
         L.xo_exp.argtypes = [C.c_float]
+        L.xo_exp_array.restype = None
+        L.xo_exp_array.argtypes = [_f32p, _f32p, C.c_int64]
+        L.xo_set_exp_mode.restype = None
+        L.xo_set_exp_mode.argtypes = [C.c_int32]
         L.xo_argmax.restype = C.c_int32
         L.xo_argmax.argtypes = [_f32p, C.c_int64, C.POINTER(C.c_uint32)]
         L.xo_softmax_in_place.restype = None
@@ -112,8 +116,16 @@ def exp(x: float) -> float:
 
 
 def exp_array(x: np.ndarray) -> np.ndarray:
-    f = lib().xo_exp
-    return np.array([f(float(v)) for v in np.asarray(x, np.float32).ravel()], np.float32)
+    """xo_exp_array: the correctly rounded exp of every element."""
+    xx = f32(x).ravel()
+    y = np.empty_like(xx)
+    lib().xo_exp_array(xx, y, xx.size)
+    return y
+
+
+def set_exp_mode(mode: int) -> None:
+    """0: correctly rounded exp (parity, default); 1: libm expf (CPU-baseline timing)."""
+    lib().xo_set_exp_mode(mode)
 
 
 def argmax(values) -> tuple[int, int]:

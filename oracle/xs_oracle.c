@@ -78,7 +78,20 @@ static double xo_widen(float f) { /* inf counts as 2^128 when locating midpoints
   return isinf(f) ? copysign(0x1p128, (double)f) : (double)f;
 }
 
-float xo_exp(float xf) {
+/* 0: correctly rounded exp (parity); 1: the platform libm expf, which is what
+ * the reference's f32::exp calls (sampler.rs:303) -- used only to time the CPU
+ * baseline at the reference's own speed. */
+static int xo_exp_mode = 0;
+void xo_set_exp_mode(int32_t mode) { xo_exp_mode = mode; }
+
+static float xo_exp_cr(float xf);
+float xo_exp(float xf) { return xo_exp_mode ? expf(xf) : xo_exp_cr(xf); }
+
+void xo_exp_array(const float* x, float* y, int64_t n) {
+  for (int64_t i = 0; i < n; i++) y[i] = xo_exp_cr(x[i]);
+}
+
+static float xo_exp_cr(float xf) {
   if (xf != xf) return xf + xf;
   if (xf < -104.0f) return 0.0f;
   if (xf > 89.0f) return INFINITY;

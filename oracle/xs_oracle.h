@@ -91,6 +91,8 @@ typedef struct {
 } xo_result;
 
 float xo_exp(float x);
+void xo_exp_array(const float* x, float* y, int64_t n); /* correctly rounded, always */
+void xo_set_exp_mode(int32_t mode); /* 0 = correctly rounded (default), 1 = libm expf */
 int32_t xo_argmax(const float* v, int64_t n, uint32_t* out);
 void xo_softmax_in_place(float* v, int64_t n, double temperature, int32_t sum_mode,
                          float s_given, float* max_out, float* sum_out);

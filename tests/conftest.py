@@ -42,3 +42,14 @@ def oracle():
     from oracle import oracle as o
     o.build()
     return o
+
+
+def pytest_sessionstart(session):
+    """Build what the tests load if nothing is built yet (the GPU box uses the
+    prebuilt files that travel with the tree)."""
+    from oracle import oracle as o
+    o.build()
+    from xwen_amd import _lib
+    if not os.path.exists(_lib.LIB_PATH):
+        from xwen_amd import build
+        build.build()

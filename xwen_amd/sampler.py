@@ -1,0 +1,326 @@
+"""Host-side mirror of xwen's sampler interface over the HIP C ABI.
+
+Names, argument meaning and error behaviour follow the reference:
+
+  SamplerOptions / recommended      src/sampler.rs:36-71
+  SampleControl (allowed mask)      src/sampler.rs:85-121
+  Sampler.new / sample /
+  sample_masked / sample_controlled src/sampler.rs:123-232
+  Sampler.is_eog / eog_ids /
+  encodable                         src/sampler.rs:127-128, :245-253
+  verify_batch (accept_drafts)      src/generate.rs:4020-4046
+  keep_confident                    src/generate.rs:3898-3905
+  held-row log-probs                src/generate.rs:1871-1933
+
+Differences, all forced by the batched device design:
+  * calls are batched: `logits` is [rows, width] on the GPU and every row is an
+    independent draw with its own options;
+  * the RNG is a seeded stream of host uniforms u = j * 2^-23 (the f32 rand
+    0.9's UniformFloat builds from 23 random bits), one per stochastic row and
+    none for a greedy row -- the reference's one-draw-per-committed-token
+    invariant; the reference's StdRng (ChaCha12) bit stream is not reproduced;
+  * row errors are reported per row (SampleError carries every status) instead
+    of failing the first one.
+
+Device memory and streams come from PyTorch (torch.cuda); the computation is the
+HIP kernels in libxsamp.so.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from . import _lib
+
+ROW_STATUS_NAMES = {
+    _lib.ROW_OK: "ok",
+    _lib.ROW_NAN: "the logit row holds a NaN: the forward pass produced a corrupt row",
+    _lib.ROW_NO_FINITE: "every logit was excluded: there is no token to draw",
+    _lib.ROW_MASK_SHORT: "allow-mask covers fewer ids than the vocabulary holds",
+    _lib.ROW_FORCE_OOR: "forced token id is outside the vocabulary",
+    _lib.ROW_ZERO_WEIGHT: "no candidate carries any probability mass after top-k/top-p filtering",
+    _lib.ROW_NARROW: "logit row is narrower than the encodable ids the sampler draws over",
+    _lib.ROW_BAD_PARAM: "top_k exceeds the sampler context's k_max",
+}
+
+
+class SampleError(RuntimeError):
+    """One or more rows failed; `status` holds every row's XS_ROW_* code."""
+
+    def __init__(self, status):
+        self.status = np.asarray(status)
+        bad = np.nonzero(self.status)[0]
+        first = int(bad[0])
+        super().__init__(f"{len(bad)} of {self.status.size} rows failed; row {first}: "
+                         f"{ROW_STATUS_NAMES.get(int(self.status[first]), 'unknown')}")
+
+
+@dataclass
+class SamplerOptions:
+    """SamplerOptions (sampler.rs:36-71): defaults are the thinking set."""
+
+    temperature: float = 1.0
+    top_k: int = 20
+    top_p: float = 0.95
+    seed: int = 42
+
+    @staticmethod
+    def recommended(thinking: bool) -> "SamplerOptions":
+        return SamplerOptions(temperature=1.0 if thinking else 0.7, top_k=20,
+                              top_p=0.95 if thinking else 0.80, seed=42)
+
+    def is_greedy(self) -> bool:
+        # Sampler::new (sampler.rs:133-145)
+        return self.temperature <= 0.0 or self.top_k <= 1
+
+
+@dataclass
+class SampleControl:
+    """SampleControl (sampler.rs:85-121).  `allowed` is a packed u32 allow-mask per
+    row on the GPU ([rows, words], bit t%32 of word t/32), or None."""
+
+    allowed: object = None
+
+
+def _torch():
+    import torch
+    return torch
+
+
+def _ptr(t):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+class Context:
+    """An xs_context: the device workspace for up to max_rows rows of `vocab` ids."""
+
+    def __init__(self, max_rows: int, vocab: int, k_max: int = _lib.K_MAX, device: int = 0):
+        self.lib = _lib.load()
+        torch = _torch()
+        self.device = device
+        torch.cuda.set_device(device)
+        h = C.c_void_p()
+        _lib.check(self.lib.xs_create(device, max_rows, vocab, k_max, C.byref(h)), "xs_create")
+        self.h = h
+        self.max_rows, self.vocab, self.k_max = max_rows, vocab, k_max
+
+    def bind_current_stream(self):
+        torch = _torch()
+        s = torch.cuda.current_stream(self.device).cuda_stream
+        _lib.check(self.lib.xs_set_stream(self.h, C.c_void_p(s)), "xs_set_stream")
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.lib.xs_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def params_tensor(temperature, top_k, top_p, rows: int, device):
+    """Pack per-row (temperature f64, top_k i32, top_p f32) as xs_row_params [rows]."""
+    torch = _torch()
+    arr = np.zeros(rows, dtype=np.dtype([("t", "<f8"), ("k", "<i4"), ("p", "<f4")]))
+    arr["t"] = np.broadcast_to(np.asarray(temperature, np.float64), (rows,))
+    arr["k"] = np.broadcast_to(np.asarray(top_k, np.int64), (rows,)).astype(np.int32)
+    arr["p"] = np.broadcast_to(np.asarray(top_p, np.float64), (rows,)).astype(np.float32)
+    raw = np.frombuffer(arr.tobytes(), dtype=np.uint8).copy()
+    return torch.from_numpy(raw).to(device)
+
+
+@dataclass
+class Draws:
+    """Device outputs of one batched draw (torch tensors on the GPU)."""
+
+    token: object
+    status: object
+    n_cand: object = None
+    cand_id: object = None
+    cand_w: object = None
+    soft_max: object = None
+    soft_sum: object = None
+    row_max: object = None
+    row_lse: object = None
+    top_id: object = None
+    top_logprob: object = None
+
+
+def sample_batch(ctx: Context, logits, params, uniforms, *, enc: int | None = None,
+                 width: int | None = None, allowed=None, allowed_words: int | None = None,
+                 cand_k: int = 0, stats: bool = False, n_top: int = 0, out: Draws | None = None,
+                 check: bool = True) -> Draws:
+    """One xs_sample call.  logits: float32 [rows, ld] CUDA tensor (ld % 4 == 0);
+    params: the uint8 tensor from params_tensor; uniforms: float32 [rows]."""
+    torch = _torch()
+    rows, ld = logits.shape
+    dev = logits.device
+    enc = ld if enc is None else enc
+    width = ld if width is None else width
+    if out is None:
+        out = Draws(token=torch.empty(rows, dtype=torch.int32, device=dev),
+                    status=torch.empty(rows, dtype=torch.int32, device=dev))
+        if cand_k:
+            out.n_cand = torch.empty(rows, dtype=torch.int32, device=dev)
+            out.cand_id = torch.empty((rows, cand_k), dtype=torch.int32, device=dev)
+            out.cand_w = torch.empty((rows, cand_k), dtype=torch.float32, device=dev)
+        if stats:
+            out.soft_max = torch.empty(rows, dtype=torch.float32, device=dev)
+            out.soft_sum = torch.empty(rows, dtype=torch.float32, device=dev)
+        if n_top:
+            out.row_max = torch.empty(rows, dtype=torch.float32, device=dev)
+            out.row_lse = torch.empty(rows, dtype=torch.float64, device=dev)
+            out.top_id = torch.empty((rows, n_top), dtype=torch.int32, device=dev)
+            out.top_logprob = torch.empty((rows, n_top), dtype=torch.float32, device=dev)
+    a = _lib.SampleArgs()
+    a.logits = logits.data_ptr()
+    a.rows, a.ld, a.width, a.enc = rows, ld, width, enc
+    a.params = params.data_ptr()
+    a.uniforms = uniforms.data_ptr()
+    if allowed is not None:
+        a.allowed = allowed.data_ptr()
+        a.allowed_words = allowed.shape[1] if allowed_words is None else allowed_words
+        a.allowed_ld = allowed.shape[1]
+    a.token = out.token.data_ptr()
+    a.status = out.status.data_ptr()
+    if out.cand_id is not None:
+        a.cand_id = out.cand_id.data_ptr()
+        a.cand_w = out.cand_w.data_ptr()
+        a.n_cand = out.n_cand.data_ptr()
+        a.cand_ld = out.cand_id.shape[1]
+    if out.soft_max is not None:
+        a.soft_max = out.soft_max.data_ptr()
+        a.soft_sum = out.soft_sum.data_ptr()
+    if out.top_id is not None:
+        a.row_max = out.row_max.data_ptr()
+        a.row_lse = out.row_lse.data_ptr()
+        a.n_top = out.top_id.shape[1]
+        a.top_id = out.top_id.data_ptr()
+        a.top_logprob = out.top_logprob.data_ptr()
+        a.top_ld = out.top_id.shape[1]
+    rc = ctx.lib.xs_sample(ctx.h, C.byref(a))
+    if check:
+        _lib.check(rc, "xs_sample")
+    return out
+
+
+@dataclass
+class Verdict:
+    row_token: object
+    row_status: object
+    accepted: object
+    committed: object
+    n_committed: object
+    seq_status: object
+
+
+def verify_batch(ctx: Context, logits, seqs: int, span: int, params, uniforms, drafts, *,
+                 budget=None, eog=(), enc: int | None = None, allowed=None,
+                 out: Verdict | None = None) -> Verdict:
+    """One xs_verify call over logits [seqs*span, ld]; drafts int32 [seqs, span-1]."""
+    torch = _torch()
+    rows, ld = logits.shape
+    assert rows == seqs * span
+    dev = logits.device
+    enc = ld if enc is None else enc
+    if out is None:
+        out = Verdict(row_token=torch.empty(rows, dtype=torch.int32, device=dev),
+                      row_status=torch.empty(rows, dtype=torch.int32, device=dev),
+                      accepted=torch.empty(seqs, dtype=torch.int32, device=dev),
+                      committed=torch.empty((seqs, span), dtype=torch.int32, device=dev),
+                      n_committed=torch.empty(seqs, dtype=torch.int32, device=dev),
+                      seq_status=torch.empty(seqs, dtype=torch.int32, device=dev))
+    a = _lib.VerifyArgs()
+    a.logits = logits.data_ptr()
+    a.seqs, a.span, a.ld, a.width, a.enc = seqs, span, ld, ld, enc
+    a.params = params.data_ptr()
+    a.uniforms = uniforms.data_ptr()
+    if allowed is not None:
+        a.allowed = allowed.data_ptr()
+        a.allowed_words = allowed.shape[1]
+        a.allowed_ld = allowed.shape[1]
+    a.drafts = drafts.data_ptr() if span > 1 else None
+    a.budget = budget.data_ptr() if budget is not None else None
+    a.n_eog = len(eog)
+    for i, e in enumerate(eog):
+        a.eog[i] = int(e)
+    a.row_token = out.row_token.data_ptr()
+    a.row_status = out.row_status.data_ptr()
+    a.accepted = out.accepted.data_ptr()
+    a.committed = out.committed.data_ptr()
+    a.n_committed = out.n_committed.data_ptr()
+    a.seq_status = out.seq_status.data_ptr()
+    _lib.check(ctx.lib.xs_verify(ctx.h, C.byref(a)), "xs_verify")
+    return out
+
+
+class Sampler:
+    """Sampler (sampler.rs:21-29) over the device kernels, batched by row."""
+
+    def __init__(self, opts: SamplerOptions, eog_tokens, encodable: int, *, max_rows: int = 256,
+                 device: int = 0):
+        self.opts = opts
+        self.eog = list(eog_tokens)
+        self.encodable_ = encodable
+        self.rng = np.random.default_rng(opts.seed)
+        self.ctx = Context(max_rows, encodable, device=device)
+        self.device = f"cuda:{device}"
+
+    def encodable(self) -> int:
+        return self.encodable_
+
+    def is_eog(self, token: int) -> bool:
+        return token in self.eog
+
+    def eog_ids(self):
+        return list(self.eog)
+
+    def next_uniforms(self, rows: int):
+        """One uniform per stochastic row; a greedy sampler draws none."""
+        if self.opts.is_greedy():
+            return np.zeros(rows, np.float32)
+        return (self.rng.integers(0, 1 << 23, rows) * 2.0 ** -23).astype(np.float32)
+
+    def sample_controlled(self, logits, ctl: SampleControl | None = None, uniforms=None):
+        """Draw one token per row of `logits` ([rows, width] or [width], f32, CUDA).
+        Returns an int64 numpy array of ids; raises SampleError if any row fails."""
+        torch = _torch()
+        if logits.dim() == 1:
+            logits = logits.unsqueeze(0)
+        logits = logits.to(torch.float32)
+        rows, width = logits.shape
+        ld = (width + 3) // 4 * 4
+        if ld != width or not logits.is_contiguous() or logits.data_ptr() % 16:
+            padded = torch.full((rows, ld), float("-inf"), dtype=torch.float32,
+                                device=logits.device)
+            padded[:, :width] = logits
+            logits = padded
+        if uniforms is None:
+            uniforms = self.next_uniforms(rows)
+        u = torch.as_tensor(np.asarray(uniforms, np.float32), device=logits.device)
+        p = params_tensor(self.opts.temperature, self.opts.top_k, self.opts.top_p, rows,
+                          logits.device)
+        allowed = None if ctl is None else ctl.allowed
+        self.ctx.bind_current_stream()
+        out = sample_batch(self.ctx, logits, p, u, enc=self.encodable_, width=width,
+                           allowed=allowed)
+        st = out.status.cpu().numpy()
+        if st.any():
+            raise SampleError(st)
+        return out.token.cpu().numpy().astype(np.int64)
+
+    def sample(self, logits, uniforms=None):
+        return self.sample_controlled(logits, None, uniforms)
+
+
+def keep_confident(ids, probs, p_min: float):
+    """keep_confident (generate.rs:3898-3905) through the C ABI (host memory)."""
+    lib = _lib.load()
+    p = np.ascontiguousarray(np.asarray(probs, np.float32))
+    n = lib.xs_keep_confident(p.ctypes.data if p.size else None, p.size, C.c_float(p_min))
+    return list(ids[:n])

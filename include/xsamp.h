@@ -52,7 +52,10 @@ extern "C" {
  *   XS_ROW_ZERO_WEIGHT WeightedIndex saw no probability mass (:238-240)
  *   XS_ROW_NARROW      logit row narrower than the encodable bound (:196-200)
  *   XS_ROW_BAD_PARAM   top_k larger than the context's k_max (no reference
- *                      counterpart: the reference has no such limit)        */
+ *                      counterpart: the reference has no such limit)
+ *   XS_ROW_INTERNAL    the device-side hand-off between a row's workgroups
+ *                      read an incomplete record (never expected; reported
+ *                      instead of returning a token computed from it)      */
 #define XS_ROW_OK 0
 #define XS_ROW_NAN 1
 #define XS_ROW_NO_FINITE 2
@@ -61,6 +64,7 @@ extern "C" {
 #define XS_ROW_ZERO_WEIGHT 5
 #define XS_ROW_NARROW 6
 #define XS_ROW_BAD_PARAM 7
+#define XS_ROW_INTERNAL 8
 
 /* Largest top_k a context supports (the selection keeps top_k + 1 entries). */
 #define XS_K_MAX 127
@@ -80,7 +84,8 @@ typedef struct {
 } xs_row_params;
 
 /* Sampler::new's allocation side: a context on `device` for up to `max_rows`
- * rows of up to `vocab` encodable ids and top_k <= k_max (<= XS_K_MAX).
+ * rows of up to `vocab` encodable ids (<= 1,048,576) and top_k <= k_max
+ * (<= XS_K_MAX).
  * Allocates the device workspace once; calls allocate nothing afterwards. */
 int xs_create(int device, int64_t max_rows, int64_t vocab, int32_t k_max, xs_context** out);
 int xs_destroy(xs_context* ctx);

@@ -16,7 +16,7 @@ HEADER = os.path.join(ROOT, "include", "xsamp.h")
 
 XS_OK, XS_ERR_ARG, XS_ERR_HIP, XS_ERR_CAPACITY = 0, -1, -2, -3
 ROW_OK, ROW_NAN, ROW_NO_FINITE, ROW_MASK_SHORT, ROW_FORCE_OOR, ROW_ZERO_WEIGHT, ROW_NARROW, \
-    ROW_BAD_PARAM = range(8)
+    ROW_BAD_PARAM, ROW_INTERNAL = range(9)
 K_MAX = 127
 TOP_MAX = 128
 

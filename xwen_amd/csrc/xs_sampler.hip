@@ -54,9 +54,7 @@ constexpr int NWAVE = BLOCK / 64;   // wave64
 constexpr int SLOT = BLOCK * 4;     // elements per slot: one float4 per lane
 constexpr int SPC = 16;             // slots per chunk (16,384 logits, 64 KiB)
 constexpr int KSEL = 128;           // largest selection size K'
-constexpr int CAP = 1024;           // candidate entries per chunk
-constexpr int QPUB = 32;            // sorted lane maxima a chunk publishes
-constexpr int SURV = 2048;          // survivor entries the finalizer ranks
+constexpr int SURV = 256;           // survivor entries the finalizer sorts
 constexpr float LOG2E = 1.44269504088896340736f;
 
 __constant__ double kExpT[32][2] = XS_EXP_TABLE_INIT;
@@ -266,15 +264,14 @@ XS_DEV Cfg make_cfg(const xs_row_params& p, int64_t enc, int n_top) {
 
 // ---------------------------------------------------------------------------
 // Workspace and launch arguments.
-
-struct Summary {  // one per (row, chunk)
-  float vmax;     // max of the controlled logits (NaN ignored)
-  float ssum;     // sum over the chunk of exp((v - vmax) * inv)   (stochastic rows)
-  double rsum;    // sum over the chunk of exp(v - vmax) in f64    (held_row)
-  uint32_t flags; // bit 0: a NaN was seen; bit 1: a finite value was seen
-  int32_t count;  // candidate entries written
-  int32_t pad0, pad1;
-};
+//
+// Chunks hand their results to the row's finalizing wave through the workspace
+// with agent-scope (sc1) stores and loads, which are coherent across the XCDs'
+// L2 caches without the whole-L2 writeback / invalidate a __threadfence()
+// costs.  A writer waits for its stores to be acknowledged (s_waitcnt) before
+// it bumps the row's arrival ticket; the wave that brings the ticket to its
+// last value reads everything back with sc1 loads.  Every record carries the
+// launch's epoch, so a stale read is detected (and reported) instead of used.
 
 struct Args {
   const float* logits;
@@ -309,26 +306,146 @@ struct Args {
   int32_t* seq_status;
   // geometry + workspace
   int32_t n_chunks, nslots;
-  Summary* summ;
-  uint32_t* pub;     // [rows, n_chunks, QPUB]
-  uint64_t* cand;    // [rows, n_chunks, CAP]
+  uint32_t epoch;
+  uint64_t* rec;     // [rows, n_chunks, RECW]: one record per chunk
   int32_t* row_ticket;
   int32_t* seq_ticket;
 };
 
-struct Lds {
-  uint64_t list[SURV];     // chunk candidates / finalizer survivors
-  uint64_t sel[KSEL];      // survivors in (logit desc, id asc) order
-  uint64_t psel[KSEL];     // the same in (p desc, id asc) order
-  float w[KSEL];           // probabilities / weights in draw order
-  int32_t prefix[257];     // chunk candidate offsets
-  int32_t s4[NWAVE];
-  float f4[NWAVE];
-  double d4[NWAVE];
-  uint32_t u4[NWAVE];
-  int32_t count;
-  int32_t flag;
+XS_DEV void st_agent(uint64_t* p, uint64_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+XS_DEV void st_agent(uint32_t* p, uint32_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+XS_DEV void st_agent(int32_t* p, int32_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+XS_DEV uint64_t ld_agent(const uint64_t* p) { return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+XS_DEV uint32_t ld_agent(const uint32_t* p) { return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+XS_DEV int32_t ld_agent(const int32_t* p) { return __hip_atomic_load(const_cast<int32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+
+// Wait until every memory operation this wave issued has completed.
+XS_DEV void drain() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// Order this wave's LDS writes before its later LDS reads by other lanes.
+XS_DEV void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+}
+
+XS_DEV uint32_t rdl(uint32_t x, int i) { return (uint32_t)__builtin_amdgcn_readlane((int)x, i); }
+XS_DEV float rdlf(float x, int i) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), i)); }
+XS_DEV uint64_t rdl64(uint64_t x, int i) {
+  return ((uint64_t)rdl((uint32_t)(x >> 32), i) << 32) | rdl((uint32_t)x, i);
+}
+XS_DEV uint64_t shfl64(uint64_t x, int src) {
+  const uint32_t lo = (uint32_t)__shfl((int)(uint32_t)x, src);
+  const uint32_t hi = (uint32_t)__shfl((int)(uint32_t)(x >> 32), src);
+  return ((uint64_t)hi << 32) | lo;
+}
+XS_DEV uint64_t shfl_xor64(uint64_t x, int m) {
+  const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)x, m);
+  const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(x >> 32), m);
+  return ((uint64_t)hi << 32) | lo;
+}
+// Lanes below this one whose bit is set in `mask`.
+XS_DEV int lanes_below(uint64_t mask) {
+  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+XS_DEV int wave_incl_scan(int v) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int t = __shfl_up(v, o);
+    if (lane >= o) v += t;
+  }
+  return v;
+}
+XS_DEV int wave_sumi(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+// Bitonic sort, descending, of 64*R u64 keys held R per lane (element r*64+lane).
+template <int R>
+XS_DEV void wave_sort_desc64(uint64_t (&x)[R]) {
+  const int lane = lane_id();
+  constexpr int N = 64 * R;
+#pragma unroll
+  for (int size = 2; size <= N; size <<= 1) {
+#pragma unroll
+    for (int d = size >> 1; d > 0; d >>= 1) {
+      if (d >= 64) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+          const int p = r ^ (d >> 6);
+          if (p > r) {
+            const bool desc = ((r * 64 + lane) & size) == 0;
+            const uint64_t a = x[r], b = x[p];
+            const uint64_t hi = a > b ? a : b, lo = a > b ? b : a;
+            x[r] = desc ? hi : lo;
+            x[p] = desc ? lo : hi;
+          }
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+          const uint64_t b = shfl_xor64(x[r], d);
+          const bool desc = ((r * 64 + lane) & size) == 0;
+          const bool lower = (lane & d) == 0;
+          const uint64_t hi = x[r] > b ? x[r] : b, lo = x[r] > b ? b : x[r];
+          x[r] = (lower == desc) ? hi : lo;
+        }
+      }
+    }
+  }
+}
+
+// Element `i` of a list held R per lane (i uniform).
+template <int R>
+XS_DEV uint64_t pick64(const uint64_t (&x)[R], int i) {
+  uint64_t out = 0;
+#pragma unroll
+  for (int r = 0; r < R; r++)
+    if ((i >> 6) == r) out = rdl64(x[r], i & 63);
+  return out;
+}
+
+// Record of one chunk in the workspace, RECW u64 words:
+//   w0  ssum bits << 32 | vmax bits     (softmax partial sum, chunk max)
+//   w1  rsum bits                       (held_row f64 partial sum)
+//   w2  count << 32 | flags
+//   w3  epoch
+//   w4..w7  the chunk's 8 largest lane maxima (u32 keys, two per word)
+//   w8..    count candidate entries
+constexpr int HDR = 8;
+constexpr int CAPB = 1024;          // candidate entries per chunk
+constexpr int RECW = HDR + CAPB;
+constexpr int CAPH = 256;           // candidate entries per wave before the overflow path
+constexpr int STG = 1024;           // finalizer staging words
+constexpr int NLM = 8;              // lane maxima a chunk publishes
+
+struct ChunkLds {
+  uint32_t lanemax[BLOCK];          // each wave's sorted lane maxima (the chunk bound)
+  uint64_t hits[NWAVE * CAPH];      // candidates, per wave; flat after an overflow
+  int32_t nhit[NWAVE];
   int32_t misc[8];
+  float wm[NWAVE];                  // each wave's max, flags and partial sums
+  uint32_t wf[NWAVE];
+  double ws[NWAVE];
+  double wr[NWAVE];
+};
+struct FinLds {
+  uint64_t stage[STG];              // the row's records as first loaded
+  uint64_t list[SURV];              // gathered survivors
+  uint64_t psel[KSEL];              // the candidate set in draw order: (p bits << 32) | ~id
+  float wbuf[KSEL];                 // weights for the serial draw
+};
+union Lds {
+  ChunkLds c;
+  FinLds f;
 };
 
 // p = rn(e / S) of one controlled logit v (the reference's softmax_in_place:
@@ -346,17 +463,21 @@ XS_DEV float next_below(float f) {
   return __uint_as_float(f > 0.0f ? b - 1u : b + 1u);
 }
 
-// Rare path of the chunk pass: more than CAP elements at or above the bound
-// (ties at the bound: constant or masked stretches).  Keeps the elements
-// strictly above the bound, then the lowest ids equal to it; if even the
-// strict set overflows, finds the exact K'-th largest key by bisection first.
-// Re-reads the chunk from memory so the streaming path keeps no registers for
-// it.  Every lane of the block calls it (it contains barriers).
+// ---------------------------------------------------------------------------
+// Rare path of the chunk pass: more than CAPH of a wave's elements lie at or
+// above the chunk bound (ties at the bound: constant or masked stretches).
+// Writes the chunk's exact K' best (logit desc, id asc) into `out`: everything
+// strictly above a threshold, then the lowest ids equal to it.  When even the
+// strict set would not fit, the threshold first moves to the chunk's exact
+// K'-th largest key by bisection.  Re-reads the chunk from memory so the
+// streaming path keeps no registers for it.  Every lane of the block calls it
+// (it contains barriers); returns the entry count.
 template <bool HAS_MASK>
 __device__ __noinline__ int chunk_overflow(const float* rowp, const uint32_t* mrow, int s0, int ns,
-                                           int enc, uint32_t tau_key, int kp, Lds& L) {
+                                           int enc, uint32_t tau_key, int kp, uint64_t* out,
+                                           int32_t* s4, int32_t* counter) {
   const int tid = threadIdx.x;
-  // Element e of lane tid in slot j; NaN marks an absent element (no compare holds).
+  // element e of this lane in slot j; NaN marks an absent element
   auto load = [&](int j, int e, int* idp) -> float {
     const int id = (s0 + j) * SLOT + 4 * tid + e;
     *idp = id;
@@ -365,54 +486,43 @@ __device__ __noinline__ int chunk_overflow(const float* rowp, const uint32_t* mr
     if (HAS_MASK && !((mrow[id >> 5] >> (id & 31)) & 1u)) x = -INFINITY;
     return x;
   };
+  auto count_ge = [&](uint32_t key, bool strict) -> int {
+    int c = 0;
+    for (int j = 0; j < ns; j++)
+      for (int e = 0; e < 4; e++) {
+        int id;
+        const float x = load(j, e, &id);
+        if (x == x) c += strict ? (fkey(x) > key) : (fkey(x) >= key);
+      }
+    int tot;
+    block_excl_scan(c, s4, &tot);
+    return tot;
+  };
   uint32_t eq_key = tau_key;
-  if (tid == 0) L.count = 0;
+  if (count_ge(tau_key, true) > CAPB - KSEL) {
+    uint32_t ans = 0;
+    for (int bit = 31; bit >= 0; bit--) {
+      const uint32_t cnd = ans | (1u << bit);
+      if (count_ge(cnd, false) >= kp) ans = cnd;
+    }
+    eq_key = ans;
+  }
+  if (tid == 0) *counter = 0;
   __syncthreads();
   for (int j = 0; j < ns; j++)
     for (int e = 0; e < 4; e++) {
       int id;
       const float x = load(j, e, &id);
-      if (x == x && fkey(x) > tau_key) {
-        const int pos = atomicAdd(&L.count, 1);
-        if (pos < CAP) L.list[pos] = pack(fkey(x), (uint32_t)id);
+      if (x == x && fkey(x) > eq_key) {
+        const int pos = atomicAdd(counter, 1);
+        if (pos < CAPB) out[pos] = pack(fkey(x), (uint32_t)id);
       }
     }
   __syncthreads();
-  int gt = L.count;
+  const int gt = min(*counter, CAPB);
   __syncthreads();
-  if (gt > CAP - KSEL) {
-    uint32_t ans = 0;
-    for (int bit = 31; bit >= 0; bit--) {
-      const uint32_t cnd = ans | (1u << bit);
-      int c = 0;
-      for (int j = 0; j < ns; j++)
-        for (int e = 0; e < 4; e++) {
-          int id;
-          const float x = load(j, e, &id);
-          c += (x == x && fkey(x) >= cnd) ? 1 : 0;
-        }
-      int tot;
-      block_excl_scan(c, L.s4, &tot);
-      if (tot >= kp) ans = cnd;
-    }
-    eq_key = ans;
-    if (tid == 0) L.count = 0;
-    __syncthreads();
-    for (int j = 0; j < ns; j++)
-      for (int e = 0; e < 4; e++) {
-        int id;
-        const float x = load(j, e, &id);
-        if (x == x && fkey(x) > eq_key) {
-          const int pos = atomicAdd(&L.count, 1);
-          if (pos < CAP) L.list[pos] = pack(fkey(x), (uint32_t)id);
-        }
-      }
-    __syncthreads();
-    gt = L.count;
-    __syncthreads();
-  }
-  // Ties at eq_key, lowest ids first: slot j covers ids s0*SLOT + j*SLOT +
-  // [0, SLOT) in lane order, so a block prefix count per slot is id order.
+  // ties at eq_key, lowest ids first: slot j covers ids s0*SLOT + j*SLOT +
+  // [0, SLOT) in lane order, so a block prefix count per slot is id order
   int need = kp - gt, have = gt;
   for (int j = 0; j < ns && need > 0; j++) {
     int c = 0;
@@ -423,13 +533,12 @@ __device__ __noinline__ int chunk_overflow(const float* rowp, const uint32_t* mr
       c += (xs[e] == xs[e] && fkey(xs[e]) == eq_key) ? 1 : 0;
     }
     int tot;
-    int pre = block_excl_scan(c, L.s4, &tot);
-    for (int e = 0; e < 4; e++) {
+    int pre = block_excl_scan(c, s4, &tot);
+    for (int e = 0; e < 4; e++)
       if (xs[e] == xs[e] && fkey(xs[e]) == eq_key) {
-        if (pre < need) L.list[have + pre] = pack(eq_key, (uint32_t)ids[e]);
+        if (pre < need) out[have + pre] = pack(eq_key, (uint32_t)ids[e]);
         pre++;
       }
-    }
     have += min(tot, need);
     need -= tot;
     __syncthreads();
@@ -446,8 +555,8 @@ __global__ __launch_bounds__(BLOCK) void sample_kernel(Args a) {
   const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
   const int row = blockIdx.x / a.n_chunks;
   const int chunk = blockIdx.x - row * a.n_chunks;
-  const int64_t enc = a.enc;
-  const Cfg cfg = make_cfg(a.params[row], enc, a.n_top);
+  const int enc = (int)a.enc;
+  const Cfg cfg = make_cfg(a.params[row], a.enc, a.n_top);
   const bool stoch = !cfg.greedy && !cfg.bad;
   const int kp = cfg.kp;
 
@@ -462,7 +571,7 @@ __global__ __launch_bounds__(BLOCK) void sample_kernel(Args a) {
   float v[SPC * 4];
 #pragma unroll
   for (int j = 0; j < SPC; j++) {
-    const int64_t f = (int64_t)(s0 + j) * BLOCK + tid;  // float4 index in the row
+    const int f = (s0 + j) * BLOCK + tid;  // float4 index in the row
     float4 q = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
     if (j < ns && 4 * f < enc) {
       const v4f t = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(rp4 + f));
@@ -490,11 +599,10 @@ __global__ __launch_bounds__(BLOCK) void sample_kernel(Args a) {
     for (int i = 0; i < SPC * 4; i++) rsum += (double)expf(v[i] - off);
   }
 
-  uint32_t flags = 0;
   if (HAS_MASK) {
 #pragma unroll
     for (int j = 0; j < SPC; j++) {
-      const int64_t f = (int64_t)(s0 + j) * BLOCK + tid;
+      const int f = (s0 + j) * BLOCK + tid;
       if (j < ns && 4 * f < enc) {
         const uint32_t bits = mrow[f >> 3] >> ((f & 7) * 4);
 #pragma unroll
@@ -502,483 +610,582 @@ __global__ __launch_bounds__(BLOCK) void sample_kernel(Args a) {
           if (!((bits >> e) & 1u)) v[4 * j + e] = -INFINITY;
       }
     }
-#pragma unroll
-    for (int i = 0; i < SPC * 4; i++) flags |= (__builtin_fabsf(v[i]) < INFINITY) ? 2u : 0u;
   }
   float m = -INFINITY;
 #pragma unroll
-  for (int i = 0; i < SPC * 4; i++) {
-    m = fmaxf(m, v[i]);
-    flags |= (v[i] != v[i]) ? 1u : 0u;
+  for (int i = 0; i < SPC * 4; i++) m = fmaxf(m, v[i]);
+  // flags: bit 0 a NaN (or, on stochastic rows, a +inf) was seen; bit 1 a
+  // finite value was seen (only needed with an allow-mask)
+  uint32_t flags = 0;
+  if (HAS_MASK) {
+    if (__builtin_isfinite(m)) {
+      flags |= 2u;
+    } else if (m == INFINITY) {
+#pragma unroll
+      for (int i = 0; i < SPC * 4; i++) flags |= __builtin_isfinite(v[i]) ? 2u : 0u;
+    }
   }
   // Softmax partial sum in the reference's scaled domain: s = v * inv rounded to
   // f32 exactly as softmax_in_place does, then exp(s - off_s) with off_s the
-  // lane's scaled max, so each term carries the reference's own roundings.
+  // lane's scaled max.  The exponent is one fma, s*log2(e) - rn(off_s*log2(e));
+  // the constant rounding error of rn(off_s*log2(e)) is exact (an fma) and is
+  // taken back out of the lane's sum once.  A NaN, or a +inf max (inf - inf),
+  // makes the sum NaN, which is the stochastic path's NaN test.
   float ssum = 0.0f;
   const float off = (m == -INFINITY) ? 0.0f : m;
   const float off_s = cfg.scale ? off * cfg.inv : off;
   if (stoch) {
+    const float offl = off_s * LOG2E;
+    const float err = __builtin_fmaf(off_s, LOG2E, -offl);  // off_s*log2e - offl, exact
     if (cfg.scale) {
 #pragma unroll
-      for (int i = 0; i < SPC * 4; i++) ssum += __builtin_amdgcn_exp2f((v[i] * cfg.inv - off_s) * LOG2E);
+      for (int i = 0; i < SPC * 4; i++) ssum += __builtin_amdgcn_exp2f(__builtin_fmaf(v[i] * cfg.inv, LOG2E, -offl));
     } else {
 #pragma unroll
-      for (int i = 0; i < SPC * 4; i++) ssum += __builtin_amdgcn_exp2f((v[i] - off_s) * LOG2E);
+      for (int i = 0; i < SPC * 4; i++) ssum += __builtin_amdgcn_exp2f(__builtin_fmaf(v[i], LOG2E, -offl));
     }
+    ssum *= __builtin_amdgcn_exp2f(-err);
+    if (ssum != ssum) flags |= 1u;
+  } else {
+#pragma unroll
+    for (int i = 0; i < SPC * 4; i++) flags |= (v[i] != v[i]) ? 1u : 0u;
   }
+  if (WANT_LSE && rsum != rsum) flags |= 1u;
 
-  // Block reductions: chunk max, flags, then the partial sums rescaled to it.
-  {
-    const float wm = wave_maxf(m);
-    const uint32_t wf = wave_or(flags);
-    if (lane == 0) { L.f4[wave] = wm; L.u4[wave] = wf; }
-  }
-  __syncthreads();
-  float m_c = L.f4[0];
-  uint32_t f_c = L.u4[0];
-#pragma unroll
-  for (int w = 1; w < NWAVE; w++) { m_c = fmaxf(m_c, L.f4[w]); f_c |= L.u4[w]; }
-  const float off_c = (m_c == -INFINITY) ? 0.0f : m_c;
-  const float off_cs = cfg.scale ? off_c * cfg.inv : off_c;
-  __syncthreads();
-  if (stoch) {
-    double t = 0.0;
-    if (ssum != 0.0f) t = (double)ssum * exp((double)off_s - (double)off_cs);
-    t = wave_sumd(t);
-    if (lane == 0) L.d4[wave] = t;
-  }
-  __syncthreads();
-  double ssum_c = 0.0;
-  if (stoch) {
-#pragma unroll
-    for (int w = 0; w < NWAVE; w++) ssum_c += L.d4[w];
-  }
-  __syncthreads();
-  double rsum_c = 0.0;
+  // Wave reductions: max, flags, and the partial sums rescaled to the wave max.
+  const float m_w = wave_maxf(m);
+  const uint32_t f_w = wave_or(flags);
+  const float offw = (m_w == -INFINITY) ? 0.0f : m_w;
+  const float offw_s = cfg.scale ? offw * cfg.inv : offw;
+  double ssum_w = 0.0, rsum_w = 0.0;
+  if (stoch) ssum_w = wave_sumd(ssum != 0.0f ? (double)ssum * exp((double)off_s - (double)offw_s) : 0.0);
   if (WANT_LSE) {
     const float moff = __builtin_isinf(m_raw) ? 0.0f : m_raw;
-    double t = 0.0;
-    if (rsum != 0.0) t = rsum * exp((double)moff - (double)off_c);
-    t = wave_sumd(t);
-    if (lane == 0) L.d4[wave] = t;
-    __syncthreads();
-#pragma unroll
-    for (int w = 0; w < NWAVE; w++) rsum_c += L.d4[w];
-    __syncthreads();
+    rsum_w = wave_sumd(rsum != 0.0 ? rsum * exp((double)moff - (double)offw) : 0.0);
   }
 
   // Candidate bound: the K'-th largest of the block's 256 lane maxima (distinct
   // elements, so at least K' elements of the chunk lie at or above it).  Each
-  // wave sorts its 64 lane maxima; wave 0 merges the four sorted lists with two
-  // bitonic top-64 merges (max(A[i], B[63-i]) is bitonic and holds the top 64
-  // of A u B), or sorts all 256 when K' > 64.  The chunk publishes its 32
-  // largest lane maxima for the row-level bound.
-  uint32_t* lu = reinterpret_cast<uint32_t*>(L.list);
+  // wave sorts its 64 lane maxima, then every wave merges the four sorted lists
+  // with two bitonic top-64 merges (max(A[i], B[63-i]) is bitonic and holds the
+  // top 64 of A u B), or sorts all 256 when K' > 64.
   {
     uint32_t srt[1] = {fkey(m)};
     wave_sort_desc<1>(srt);
-    lu[wave * 64 + lane] = srt[0];
+    L.c.lanemax[wave * 64 + lane] = srt[0];
   }
   __syncthreads();
-  if (wave == 0) {
-    uint32_t top;  // element `lane` of the block's sorted lane maxima
-    uint32_t tk = 0;
-    if (kp <= 64) {
-      uint32_t c1 = max(lu[lane], lu[64 + 63 - lane]);
-      uint32_t c2 = max(lu[128 + lane], lu[192 + 63 - lane]);
+  uint32_t top, tau_key = 0;
+  if (kp <= 64) {
+    uint32_t c1 = max(L.c.lanemax[lane], L.c.lanemax[64 + 63 - lane]);
+    uint32_t c2 = max(L.c.lanemax[128 + lane], L.c.lanemax[192 + 63 - lane]);
 #pragma unroll
-      for (int d = 32; d > 0; d >>= 1) {
-        const uint32_t b1 = (uint32_t)__shfl_xor((int)c1, d);
-        const uint32_t b2 = (uint32_t)__shfl_xor((int)c2, d);
-        const bool lower = (lane & d) == 0;
-        c1 = lower ? max(c1, b1) : min(c1, b1);
-        c2 = lower ? max(c2, b2) : min(c2, b2);
-      }
-      uint32_t c = max(c1, (uint32_t)__shfl((int)c2, 63 - lane));
-#pragma unroll
-      for (int d = 32; d > 0; d >>= 1) {
-        const uint32_t b = (uint32_t)__shfl_xor((int)c, d);
-        c = ((lane & d) == 0) ? max(c, b) : min(c, b);
-      }
-      top = c;
-      tk = (uint32_t)__shfl((int)c, kp - 1);
-    } else {
-      uint32_t all[4];
-#pragma unroll
-      for (int r = 0; r < 4; r++) all[r] = lu[r * 64 + lane];
-      wave_sort_desc<4>(all);
-      top = all[0];
-      const int i = kp - 1;  // < 256
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const uint32_t t = (uint32_t)__shfl((int)all[r], i & 63);
-        if ((i >> 6) == r) tk = t;
-      }
+    for (int d = 32; d > 0; d >>= 1) {
+      const uint32_t b1 = (uint32_t)__shfl_xor((int)c1, d);
+      const uint32_t b2 = (uint32_t)__shfl_xor((int)c2, d);
+      const bool lower = (lane & d) == 0;
+      c1 = lower ? max(c1, b1) : min(c1, b1);
+      c2 = lower ? max(c2, b2) : min(c2, b2);
     }
-    if (lane < QPUB) a.pub[((int64_t)row * a.n_chunks + chunk) * QPUB + lane] = top;
-    if (lane == 0) L.misc[0] = (int32_t)tk;
+    uint32_t c = max(c1, (uint32_t)__shfl((int)c2, 63 - lane));
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1) {
+      const uint32_t b = (uint32_t)__shfl_xor((int)c, d);
+      c = ((lane & d) == 0) ? max(c, b) : min(c, b);
+    }
+    top = c;
+    tau_key = rdl(c, kp - 1);
+  } else {
+    uint32_t all[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) all[r] = L.c.lanemax[r * 64 + lane];
+    wave_sort_desc<4>(all);
+    top = all[0];
+    const int i = kp - 1;  // < 256
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+      if ((i >> 6) == r) tau_key = rdl(all[r], i & 63);
   }
-  if (tid == 0) L.count = 0;
-  __syncthreads();
-  const uint32_t tau_key = (uint32_t)L.misc[0];
   const float tau = keyf(tau_key);
 
-  // Filter: every element at or above the bound (ids < enc).  One compare per
-  // element; the append branch is taken by ~K' lanes of the whole block.
+  // Filter: this wave's elements at or above the bound, compacted with ballots
+  // into the wave's LDS list.  One compare per element; the ballot branch is
+  // taken for the ~K' hits of the whole block.
+  uint64_t* hw = L.c.hits + wave * CAPH;
   const int base_id = s0 * SLOT + 4 * tid;
+  int count = 0;
 #pragma unroll
   for (int j = 0; j < SPC; j++) {
 #pragma unroll
     for (int e = 0; e < 4; e++) {
       const float x = v[4 * j + e];
-      if (x >= tau && j < ns) {
-        const int id = base_id + j * SLOT + e;
-        if (id < enc) {
-          const int pos = atomicAdd(&L.count, 1);
-          if (pos < CAP) L.list[pos] = pack(fkey(x), (uint32_t)id);
-        }
+      const int id = base_id + j * SLOT + e;
+      const bool hit = x >= tau && j < ns && id < enc;
+      const uint64_t b = __ballot(hit);
+      if (b) {
+        const int pos = count + lanes_below(b);
+        if (hit && pos < CAPH) hw[pos] = pack(fkey(x), (uint32_t)id);
+        count += __popcll(b);
       }
     }
   }
+  if (lane == 0) {
+    L.c.nhit[wave] = count;
+    L.c.wm[wave] = m_w;
+    L.c.wf[wave] = f_w;
+    L.c.ws[wave] = ssum_w;
+    L.c.wr[wave] = rsum_w;
+  }
   __syncthreads();
-  int count = L.count;
-  __syncthreads();
-  if (count > CAP) count = chunk_overflow<HAS_MASK>(rowp, mrow, s0, ns, (int)enc, tau_key, kp, L);
-  // Publish the chunk: candidates, then the summary.
+  int cnt[NWAVE], total = 0;
+  bool ovf = false;
+#pragma unroll
+  for (int w = 0; w < NWAVE; w++) {
+    cnt[w] = L.c.nhit[w];
+    total += cnt[w];
+    ovf |= cnt[w] > CAPH;
+  }
+  if (ovf) {
+    __syncthreads();
+    total = chunk_overflow<HAS_MASK>(rowp, mrow, s0, ns, enc, tau_key, kp, L.c.hits, L.c.misc,
+                                     &L.c.misc[NWAVE]);
+    cnt[0] = total;
+    cnt[1] = cnt[2] = cnt[3] = 0;
+  }
+  if (wave != 0) return;
+
+  // Chunk statistics: the four waves' partials rescaled to the chunk max.
+  float m_c = L.c.wm[0];
+  uint32_t f_c = L.c.wf[0];
+#pragma unroll
+  for (int w = 1; w < NWAVE; w++) {
+    m_c = fmaxf(m_c, L.c.wm[w]);
+    f_c |= L.c.wf[w];
+  }
+  double ssum_c = 0.0, rsum_c = 0.0;
   {
-    uint64_t* gl = a.cand + ((int64_t)row * a.n_chunks + chunk) * CAP;
-    for (int i = tid; i < count; i += BLOCK) gl[i] = L.list[i];
-    if (tid == 0) {
-      Summary s;
-      s.vmax = m_c;
-      s.ssum = (float)ssum_c;
-      s.rsum = rsum_c;
-      s.flags = f_c;
-      s.count = count;
-      s.pad0 = s.pad1 = 0;
-      a.summ[(int64_t)row * a.n_chunks + chunk] = s;
+    const float oc = (m_c == -INFINITY) ? 0.0f : m_c;
+    const float oc_s = cfg.scale ? oc * cfg.inv : oc;
+#pragma unroll
+    for (int w = 0; w < NWAVE; w++) {
+      const float ow = (L.c.wm[w] == -INFINITY) ? 0.0f : L.c.wm[w];
+      const float ow_s = cfg.scale ? ow * cfg.inv : ow;
+      if (L.c.ws[w] != 0.0) ssum_c += L.c.ws[w] * exp((double)ow_s - (double)oc_s);
+      if (WANT_LSE && L.c.wr[w] != 0.0) rsum_c += L.c.wr[w] * exp((double)ow - (double)oc);
     }
   }
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    const int t = atomicAdd(&a.row_ticket[row], 1);
-    L.flag = (t == a.n_chunks - 1);
-    if (L.flag) a.row_ticket[row] = 0;
-  }
-  __syncthreads();
-  if (!L.flag) return;
-  __threadfence();
 
-  // ---------------- row finalize (last workgroup of the row) ----------------
-  const int nc = a.n_chunks;
-  const Summary* sm = a.summ + (int64_t)row * nc;
-  float vmax = -INFINITY;
-  uint32_t fl = 0;
-  int cnt = 0;
-  for (int c = tid; c < nc; c += BLOCK) {
-    const Summary s = sm[c];
-    vmax = fmaxf(vmax, s.vmax);
-    fl |= s.flags;
+  // Wave 0 publishes the chunk record, then takes the row's arrival ticket.
+  uint64_t* rec = a.rec + ((int64_t)row * a.n_chunks + chunk) * RECW;
+  for (int i = lane; i < total; i += 64) {
+    int w = 0, j = i;
+    if (!ovf) {
+      while (j >= cnt[w]) { j -= cnt[w]; w++; }
+    }
+    st_agent(rec + HDR + i, L.c.hits[(ovf ? 0 : w * CAPH) + j]);
   }
   {
-    const float wm = wave_maxf(vmax);
-    const uint32_t wf = wave_or(fl);
-    if (lane == 0) { L.f4[wave] = wm; L.u4[wave] = wf; }
+    const uint32_t t0 = (uint32_t)__shfl((int)top, (2 * lane) & 63);
+    const uint32_t t1 = (uint32_t)__shfl((int)top, (2 * lane + 1) & 63);
+    if (lane < NLM / 2) st_agent(rec + 4 + lane, ((uint64_t)t1 << 32) | t0);
   }
-  __syncthreads();
-  float m_v = L.f4[0];
-  fl = L.u4[0];
+  if (lane == 0) {
+    st_agent(rec + 0, ((uint64_t)__float_as_uint((float)ssum_c) << 32) | __float_as_uint(m_c));
+    st_agent(rec + 1, (uint64_t)__double_as_longlong(rsum_c));
+    st_agent(rec + 2, ((uint64_t)(uint32_t)total << 32) | f_c);
+    st_agent(rec + 3, (uint64_t)a.epoch);
+  }
+  drain();
+  int t = 0;
+  if (lane == 0) t = __hip_atomic_fetch_add(&a.row_ticket[row], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  t = __shfl(t, 0);
+  const int nc = a.n_chunks;
+  if (t != nc - 1) return;
+  if (lane == 0) st_agent(&a.row_ticket[row], 0);
+
+  // ---------------- row finalize: wave 0 of the last block ----------------
+  // All of the row's records, STG words at most, in one round of loads.
+  FinLds& F = L.f;
+  const uint64_t* rr = a.rec + (int64_t)row * nc * RECW;
+  const int w1 = min(RECW, STG / nc);  // words of each record staged (>= HDR + 8)
+  {
+    constexpr int NB = STG / 64;
+    uint64_t sv[NB];
 #pragma unroll
-  for (int w = 1; w < NWAVE; w++) { m_v = fmaxf(m_v, L.f4[w]); fl |= L.u4[w]; }
-  __syncthreads();
+    for (int u = 0; u < NB; u++) {
+      const int i = u * 64 + lane;
+      sv[u] = 0ull;
+      if (i < nc * w1) {
+        const int c = i / w1, k = i - c * w1;
+        sv[u] = ld_agent(rr + (int64_t)c * RECW + k);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < NB; u++)
+      if (u * 64 + lane < nc * w1) F.stage[u * 64 + lane] = sv[u];
+  }
+  wave_lds_sync();
+  // Lane c holds chunk c's header (nc <= 64 is enforced by the host).
+  float cv = -INFINITY, cs = 0.0f;
+  double cr = 0.0;
+  uint32_t cf = 0;
+  int cc = 0;
+  bool stale = false;
+  if (lane < nc) {
+    uint64_t h3 = F.stage[lane * w1 + 3];
+    if ((uint32_t)h3 != a.epoch) {
+      // not visible yet: re-read the record (bounded), then restage its words
+      for (int spin = 0; spin < 1000 && (uint32_t)h3 != a.epoch; spin++) h3 = ld_agent(rr + (int64_t)lane * RECW + 3);
+      stale = (uint32_t)h3 != a.epoch;
+      for (int k = 0; k < w1; k++) F.stage[lane * w1 + k] = ld_agent(rr + (int64_t)lane * RECW + k);
+    }
+    const uint64_t h0 = F.stage[lane * w1 + 0];
+    const uint64_t h1 = F.stage[lane * w1 + 1];
+    const uint64_t h2 = F.stage[lane * w1 + 2];
+    cv = __uint_as_float((uint32_t)h0);
+    cs = __uint_as_float((uint32_t)(h0 >> 32));
+    cr = __longlong_as_double((long long)h1);
+    cf = (uint32_t)h2;
+    cc = (int)(h2 >> 32);
+  }
+  wave_lds_sync();
+  const bool any_stale = __ballot(stale) != 0;
+  const float m_v = wave_maxf(cv);
+  const uint32_t fl = wave_or(cf);
   const float moff = (m_v == -INFINITY) ? 0.0f : m_v;
   const float moff_s = cfg.scale ? moff * cfg.inv : moff;
-  // Denominator: chunk partials rescaled to the row max, summed in f64.
   double S_d = 0.0, R_d = 0.0;
-  for (int c = tid; c < nc; c += BLOCK) {
-    const Summary s = sm[c];
-    const float co = (s.vmax == -INFINITY) ? 0.0f : s.vmax;
+  {
+    const float co = (cv == -INFINITY) ? 0.0f : cv;
     const float co_s = cfg.scale ? co * cfg.inv : co;
-    if (s.ssum != 0.0f) S_d += (double)s.ssum * exp((double)co_s - (double)moff_s);
-    if (WANT_LSE && s.rsum != 0.0) R_d += s.rsum * exp((double)co - (double)moff);
+    if (cs != 0.0f) S_d = (double)cs * exp((double)co_s - (double)moff_s);
+    if (WANT_LSE && cr != 0.0) R_d = cr * exp((double)co - (double)moff);
   }
   S_d = wave_sumd(S_d);
-  if (lane == 0) L.d4[wave] = S_d;
-  __syncthreads();
-  S_d = 0.0;
-#pragma unroll
-  for (int w = 0; w < NWAVE; w++) S_d += L.d4[w];
-  __syncthreads();
-  if (WANT_LSE) {
-    R_d = wave_sumd(R_d);
-    if (lane == 0) L.d4[wave] = R_d;
-    __syncthreads();
-    R_d = 0.0;
-#pragma unroll
-    for (int w = 0; w < NWAVE; w++) R_d += L.d4[w];
-    __syncthreads();
-  }
+  if (WANT_LSE) R_d = wave_sumd(R_d);
   const float S = (float)S_d;
   const float m_s = cfg.scale ? m_v * cfg.inv : m_v;
   const bool nan_seen = fl & 1u;
   const bool finite_seen = fl & 2u;
 
   int st = XS_ROW_OK;
-  if (cfg.bad) st = XS_ROW_BAD_PARAM;
+  if (any_stale) st = XS_ROW_INTERNAL;
+  else if (cfg.bad) st = XS_ROW_BAD_PARAM;
   else if (HAS_MASK && !finite_seen) st = XS_ROW_NO_FINITE;
   else if (cfg.greedy) st = nan_seen ? XS_ROW_NAN : (m_v == -INFINITY ? XS_ROW_NO_FINITE : XS_ROW_OK);
   else if (nan_seen || __builtin_isinf(m_s)) st = XS_ROW_NAN;
 
   // Survivor bound: the K'-th largest of the chunks' published lane maxima
-  // (distinct elements), using the top q of every chunk's list, <= 256 values.
-  int q = (kp + nc - 1) / nc + 1;
-  q = min(q, QPUB);
-  while (q > 1 && nc * q > 256) q--;
-  const int nv = min(nc * q, 256);
-  if (wave == 0) {
-    uint32_t x[4];
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const int i = r * 64 + lane;
-      x[r] = 0u;
-      if (i < nv) {
-        const int c = i / q, qi = i - c * q;
-        x[r] = a.pub[((int64_t)row * nc + c) * QPUB + qi];
-      }
-    }
-    wave_sort_desc<4>(x);
-    uint32_t tk = 0;
+  // (distinct elements; NLM per chunk, up to 256 values).
+  uint32_t tau_row = 0;
+  {
+    const int nv = min(nc * NLM, 256);
     if (nv >= kp) {
-      const int i = kp - 1;
+      uint32_t x[4];
 #pragma unroll
       for (int r = 0; r < 4; r++) {
-        const uint32_t t = (uint32_t)__shfl((int)x[r], i & 63);
-        if ((i >> 6) == r) tk = t;
+        const int i = r * 64 + lane;
+        const int c = i / NLM, k = i - c * NLM;
+        x[r] = 0u;
+        if (i < nv) {
+          const uint64_t wv = F.stage[c * w1 + 4 + (k >> 1)];
+          x[r] = (k & 1) ? (uint32_t)(wv >> 32) : (uint32_t)wv;
+        }
+      }
+      if (nv <= 64) {
+        uint32_t y[1] = {x[0]};
+        wave_sort_desc<1>(y);
+        tau_row = rdl(y[0], kp - 1);
+      } else if (nv <= 128) {
+        uint32_t y[2] = {x[0], x[1]};
+        wave_sort_desc<2>(y);
+        tau_row = (kp - 1) < 64 ? rdl(y[0], kp - 1) : rdl(y[1], kp - 65);
+      } else {
+        wave_sort_desc<4>(x);
+        const int i = kp - 1;
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+          if ((i >> 6) == r) tau_row = rdl(x[r], i & 63);
       }
     }
-    if (lane == 0) L.misc[2] = (int32_t)tk;
   }
-  // chunk candidate offsets (nc <= BLOCK is enforced by the host)
-  {
-    const int c0 = tid < nc ? sm[tid].count : 0;
-    int tot;
-    const int pre = block_excl_scan(c0, L.s4, &tot);
-    if (tid < nc) L.prefix[tid] = pre;
-    if (tid == 0) { L.prefix[nc] = tot; L.count = 0; }
-  }
-  __syncthreads();
-  uint64_t floor_e = (uint64_t)(uint32_t)L.misc[2] << 32;  // survivors: entries >= floor_e
-  const int total = L.prefix[nc];
+  // Gather the survivors (entries at or above the bound) into LDS: lane c
+  // reads chunk c's entries eight at a time (staged words first, the rest from
+  // the workspace); a wave prefix sum places them.
+  int maxc = cc;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) maxc = max(maxc, __shfl_xor(maxc, o));
+  uint64_t floor_e = (uint64_t)tau_row << 32;
+  int M = 0;
   for (int pass = 0; pass < 2; pass++) {
-    for (int i = tid; i < total; i += BLOCK) {
-      int lo = 0, hi = nc - 1;  // chunk c with prefix[c] <= i < prefix[c+1]
-      while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (L.prefix[mid] <= i) lo = mid; else hi = mid - 1;
+    M = 0;
+    for (int j0 = 0; j0 < maxc; j0 += 8) {
+      uint64_t e[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        const int j = j0 + u;
+        e[u] = 0ull;
+        if (j < cc) e[u] = (HDR + j < w1) ? F.stage[lane * w1 + HDR + j] : ld_agent(rr + (int64_t)lane * RECW + HDR + j);
       }
-      const uint64_t e = a.cand[((int64_t)row * nc + lo) * CAP + (i - L.prefix[lo])];
-      if (e >= floor_e) {
-        const int pos = atomicAdd(&L.count, 1);
-        if (pos < SURV) L.list[pos] = e;
-      }
+      int h = 0;
+#pragma unroll
+      for (int u = 0; u < 8; u++) h += (j0 + u < cc && e[u] >= floor_e) ? 1 : 0;
+      const int incl = wave_incl_scan(h);
+      int pos = M + incl - h;
+#pragma unroll
+      for (int u = 0; u < 8; u++)
+        if (j0 + u < cc && e[u] >= floor_e) {
+          if (pos < SURV) F.list[pos] = e[u];
+          pos++;
+        }
+      M += __shfl(incl, 63);
     }
-    __syncthreads();
-    if (L.count <= SURV) break;  // block-uniform
-    // Too many survivors (ties at the bound across many chunks): find the exact
-    // K'-th largest entry by bisection over the unique u64 entries, then refilter.
+    if (M <= SURV) break;
+    // More survivors than one wave sorts (ties at the bound across many
+    // chunks): move the floor to the exact K'-th largest entry by bisection.
     uint64_t ans = 0;
     for (int bit = 63; bit >= 0; bit--) {
       const uint64_t cnd = ans | (1ull << bit);
       int c = 0;
-      for (int i = tid; i < total; i += BLOCK) {
-        int lo = 0, hi = nc - 1;
-        while (lo < hi) {
-          const int mid = (lo + hi + 1) >> 1;
-          if (L.prefix[mid] <= i) lo = mid; else hi = mid - 1;
-        }
-        c += a.cand[((int64_t)row * nc + lo) * CAP + (i - L.prefix[lo])] >= cnd ? 1 : 0;
+      for (int j = 0; j < cc; j++) {
+        const uint64_t e = (HDR + j < w1) ? F.stage[lane * w1 + HDR + j] : ld_agent(rr + (int64_t)lane * RECW + HDR + j);
+        c += e >= cnd ? 1 : 0;
       }
-      int tot;
-      block_excl_scan(c, L.s4, &tot);
-      if (tot >= kp) ans = cnd;
+      if (wave_sumi(c) >= kp) ans = cnd;
     }
     floor_e = ans;
-    if (tid == 0) L.count = 0;
-    __syncthreads();
   }
-  const int M = min(L.count, SURV);
-  // Exact selection: rank every survivor against all others (keys are unique).
-  for (int i = tid; i < M; i += BLOCK) {
-    const uint64_t me = L.list[i];
-    int rank = 0;
-    for (int j2 = 0; j2 < M; j2++) rank += (L.list[j2] > me) ? 1 : 0;
-    if (rank < kp) L.sel[rank] = me;
+  wave_lds_sync();
+  // Sort the survivors (logit desc, id asc); the first K' are the selection.
+  uint64_t sel[4];
+#pragma unroll
+  for (int r = 0; r < 4; r++) sel[r] = (r * 64 + lane < M) ? F.list[r * 64 + lane] : 0ull;
+  if (M <= 64) {
+    uint64_t x[1] = {sel[0]};
+    wave_sort_desc64<1>(x);
+    sel[0] = x[0];
+  } else if (M <= 128) {
+    uint64_t x[2] = {sel[0], sel[1]};
+    wave_sort_desc64<2>(x);
+    sel[0] = x[0];
+    sel[1] = x[1];
+  } else {
+    wave_sort_desc64<4>(sel);
   }
-  __syncthreads();
-  const int nsel = min(M, kp);
+  const int nsel = min(M, kp);  // == kp: the union holds the row's K' best
 
-  // Probabilities of the survivors and the (p desc, id asc) order.
-  if (stoch && st == XS_ROW_OK) {
-    if (tid < nsel) {
-      const uint64_t e = L.sel[tid];
-      const float p = exact_p(keyf(pk_key(e)), cfg, m_s, S);
-      L.w[tid] = p;
-    }
-    __syncthreads();
-    if (tid < nsel) {
-      const uint64_t me = ((uint64_t)__float_as_uint(L.w[tid] + 0.0f) << 32) | (uint64_t)(0xFFFFFFFFu - pk_id(L.sel[tid]));
-      int rank = 0;
-      for (int j2 = 0; j2 < nsel; j2++) {
-        const uint64_t o = ((uint64_t)__float_as_uint(L.w[j2] + 0.0f) << 32) | (uint64_t)(0xFFFFFFFFu - pk_id(L.sel[j2]));
-        rank += (o > me) ? 1 : 0;
-      }
-      L.psel[rank] = me;
-    }
-    __syncthreads();
-  }
-
-  // Boundary proof (stochastic, top_k < enc): the k-th probability P_k must
-  // not be shared by an entry outside the survivors.
-  int k = cfg.k;
+  // Probabilities of the selection and the (p desc, id asc) order; p is
+  // non-increasing along the logit order, so only runs of equal p move.
+  const int k = cfg.k;
   const bool want_cands = a.cand_id != nullptr || a.cand_w != nullptr;
-  if (stoch && st == XS_ROW_OK && !cfg.full) {
-    if (tid == 0) {
-      // L.w[i] holds p of L.sel[i] (logit order).
-      const float Pk = __uint_as_float((uint32_t)(L.psel[k - 1] >> 32));
-      const float vL = keyf(pk_key(L.sel[nsel - 1]));
-      const float pL = L.w[nsel - 1];
-      int slow = 0;
-      if (nsel < kp) slow = 1;  // cannot happen (k < enc); scan to be safe
-      else if (pL == Pk) {
-        // Safe only if every survivor tied at P_k has logit vL and nothing
-        // below vL reaches P_k: then the tie is an exact logit tie, whose lowest
-        // ids the (logit desc, id asc) selection already kept.
-        bool only_vl = true;
-        for (int i = 0; i < nsel; i++)
-          if (L.w[i] == Pk && keyf(pk_key(L.sel[i])) != vL) only_vl = false;
-        bool below = false;
-        if (vL != -INFINITY) below = exact_p(next_below(vL), cfg, m_s, S) == Pk;
-        slow = (!only_vl || below) ? 1 : 0;
+  float pw[2] = {0.0f, 0.0f};    // p of selection entry r*64+lane (K' <= 128)
+  uint64_t pk[2] = {0ull, 0ull};  // (p bits << 32) | ~id
+  if (stoch && st == XS_ROW_OK) {
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+      const int i = r * 64 + lane;
+      if (i < nsel) {
+        pw[r] = exact_p(keyf(pk_key(sel[r])), cfg, m_s, S);
+        pk[r] = ((uint64_t)__float_as_uint(pw[r] + 0.0f) << 32) | (uint64_t)(0xFFFFFFFFu - pk_id(sel[r]));
+      }
+    }
+    bool bad = false;
+    const uint64_t n0 = shfl64(pk[0], (lane + 1) & 63);
+    const uint64_t n1 = shfl64(pk[1], (lane + 1) & 63);
+    const uint64_t first1 = shfl64(pk[1], 0);
+    if (lane + 1 < nsel && pk[0] < (lane < 63 ? n0 : first1)) bad = true;
+    if (64 + lane + 1 < nsel && pk[1] < n1) bad = true;
+    if (__ballot(bad)) {
+      if (nsel <= 64) {
+        uint64_t x[1] = {pk[0]};
+        wave_sort_desc64<1>(x);
+        pk[0] = x[0];
+      } else {
+        wave_sort_desc64<2>(pk);
+      }
+    }
+
+    // Boundary proof (top_k < enc): the k-th probability P_k must not be shared
+    // by an entry outside the selection.  Safe when the last selected entry is
+    // strictly less probable, or when the tie is an exact logit tie (every
+    // selected entry at P_k has the last logit vL and nothing below vL reaches
+    // P_k), whose lowest ids the (logit desc, id asc) selection already kept.
+    if (!cfg.full) {
+      const float Pk = __uint_as_float((uint32_t)(pick64(pk, k - 1) >> 32));
+      const uint64_t last = pick64(sel, nsel - 1);
+      const float vL = keyf(pk_key(last));
+      const float pL = rdlf(nsel - 1 < 64 ? pw[0] : pw[1], (nsel - 1) & 63);
+      bool slow = nsel < kp;
+      if (!slow && pL == Pk) {
+        bool other = false;
+#pragma unroll
+        for (int r = 0; r < 2; r++)
+          if (r * 64 + lane < nsel && pw[r] == Pk && keyf(pk_key(sel[r])) != vL) other = true;
+        const bool below = vL != -INFINITY && exact_p(next_below(vL), cfg, m_s, S) == Pk;
+        slow = __ballot(other) != 0 || below;
       }
       // Entries tied at P_k = 0 carry no weight: the draw does not depend on
       // which ids fill them, only the returned candidate list does.
-      if (slow && Pk == 0.0f && !want_cands) slow = 0;
-      L.misc[3] = slow;
-      L.misc[4] = (int32_t)__float_as_uint(Pk);
-    }
-    __syncthreads();
-    if (L.misc[3]) {
-      // Slow path: the candidates are every survivor with p > P_k, then the
-      // lowest ids of the whole row with p == P_k, found by an id-ordered scan.
-      const float Pk = __uint_as_float((uint32_t)L.misc[4]);
-      int g = 0;
-      while (g < k && __uint_as_float((uint32_t)(L.psel[g] >> 32)) > Pk) g++;
-      // Band of exp arguments d = s - max whose exp can round to P_k * S: the
-      // rounding interval of P_k, widened generously; every element inside it
-      // gets the exact test, every element outside it provably misses.
-      const double lo_p = Pk == 0.0f ? 0.0 : 0.5 * ((double)Pk + (double)__uint_as_float(__float_as_uint(Pk) - 1u));
-      const double hi_p = 0.5 * ((double)Pk + (double)__uint_as_float(__float_as_uint(Pk) + 1u));
-      const double elo = lo_p * (double)S * (1.0 - 0x1p-10), ehi = hi_p * (double)S * (1.0 + 0x1p-10) + 0x1p-148;
-      const float x_lo = elo > 0x1p-100 ? (float)(log(elo) - 0x1p-8) : -INFINITY;
-      const float x_hi = (float)(log(ehi) + 0x1p-8);
-      __syncthreads();
-      int need = k - g, have = g;
-      for (int64_t base = 0; base < enc && need > 0; base += SLOT) {
-        const int64_t f = base / 4 + tid;
-        float4 qv = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
-        if (4 * f < enc) qv = rp4[f];
-        float xv[4] = {qv.x, qv.y, qv.z, qv.w};
-        int hit[4];
-        int c = 0;
+      if (slow && Pk == 0.0f && !want_cands) slow = false;
+      if (slow) {
+        // the candidates are every selected entry with p > P_k, then the lowest
+        // ids of the whole row with p == P_k, found by an id-ordered scan
+        F.psel[lane] = pk[0];
+        F.psel[64 + lane] = pk[1];
+        int g = 0;
+        while (g < k && __uint_as_float((uint32_t)(pick64(pk, g) >> 32)) > Pk) g++;
+        // exp arguments d = s - max whose exp can round to P_k * S: the rounding
+        // interval of P_k widened generously; inside it every element gets the
+        // exact test, outside it every element provably misses
+        const double lo_p = Pk == 0.0f ? 0.0 : 0.5 * ((double)Pk + (double)__uint_as_float(__float_as_uint(Pk) - 1u));
+        const double hi_p = 0.5 * ((double)Pk + (double)__uint_as_float(__float_as_uint(Pk) + 1u));
+        const double elo = lo_p * (double)S * (1.0 - 0x1p-10), ehi = hi_p * (double)S * (1.0 + 0x1p-10) + 0x1p-148;
+        const float x_lo = elo > 0x1p-100 ? (float)(log(elo) - 0x1p-8) : -INFINITY;
+        const float x_hi = (float)(log(ehi) + 0x1p-8);
+        int need = k - g, have = g;
+        for (int base = 0; base < enc && need > 0; base += 256) {
+          const int f = base / 4 + lane;
+          float4 qv = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+          if (4 * f < enc) qv = rp4[f];
+          const float xv[4] = {qv.x, qv.y, qv.z, qv.w};
+          bool hit[4];
+          int c = 0;
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-          const int64_t id = 4 * f + e;
-          float x = xv[e];
-          if (HAS_MASK && id < enc && !((mrow[id >> 5] >> (id & 31)) & 1u)) x = -INFINITY;
-          hit[e] = 0;
-          if (id < enc) {
-            const float sx = cfg.scale ? x * cfg.inv : x;
-            const float d = sx - m_s;
-            if (d >= x_lo && d <= x_hi) hit[e] = exact_p(x, cfg, m_s, S) == Pk;
+          for (int e = 0; e < 4; e++) {
+            const int id = 4 * f + e;
+            float x = xv[e];
+            if (HAS_MASK && id < enc && !((mrow[id >> 5] >> (id & 31)) & 1u)) x = -INFINITY;
+            hit[e] = false;
+            if (id < enc) {
+              const float sx = cfg.scale ? x * cfg.inv : x;
+              const float d = sx - m_s;
+              if (d >= x_lo && d <= x_hi) hit[e] = exact_p(x, cfg, m_s, S) == Pk;
+            }
+            c += hit[e];
           }
-          c += hit[e];
-        }
-        int tot;
-        int pre = block_excl_scan(c, L.s4, &tot);
+          const int incl = wave_incl_scan(c);
+          int pos = incl - c;
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-          if (hit[e]) {
-            if (pre < need) L.psel[have + pre] = ((uint64_t)__float_as_uint(Pk + 0.0f) << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)(4 * f + e));
-            pre++;
-          }
+          for (int e = 0; e < 4; e++)
+            if (hit[e]) {
+              if (pos < need) F.psel[have + pos] = ((uint64_t)__float_as_uint(Pk + 0.0f) << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)(4 * f + e));
+              pos++;
+            }
+          const int tot = __shfl(incl, 63);
+          have += min(tot, need);
+          need -= tot;
         }
-        have += min(tot, need);
-        need -= tot;
-        __syncthreads();
+        wave_lds_sync();
+        pk[0] = F.psel[lane];
+        pk[1] = F.psel[64 + lane];
       }
     }
   }
 
   // The draw: truncate_top_p (sampler.rs:401-429) and WeightedIndex
-  // (sampler.rs:235-243, rand 0.9), serial f32 in one lane.
-  if (tid == 0) {
-    int tok = -1;
-    if (st == XS_ROW_OK) {
-      if (!stoch) {
-        tok = (int)pk_id(L.sel[0]);
-      } else {
-        for (int i = 0; i < k; i++) L.w[i] = __uint_as_float((uint32_t)(L.psel[i] >> 32));
-        if (!(cfg.top_p >= 1.0f)) {
-          float sum = -0.0f;
-          for (int i = 0; i < k; i++) sum += L.w[i];
-          if (sum > 0.0f) {
-            for (int i = 0; i < k; i++) L.w[i] = L.w[i] / sum;
-            float cs = 0.0f;
-            int keep = k;
-            for (int i = 0; i < k; i++) {
-              cs += L.w[i];
-              if (cs >= cfg.top_p) { keep = i + 1; break; }
-            }
-            for (int i = keep; i < k; i++) L.w[i] = 0.0f;
-          }
+  // (sampler.rs:235-243, rand 0.9) in serial f32.  Every lane reads the same
+  // weights from LDS, 32 at a time, and computes the same uniform results.
+  float w[2];
+  w[0] = __uint_as_float((uint32_t)(pk[0] >> 32));
+  w[1] = __uint_as_float((uint32_t)(pk[1] >> 32));
+  int tok = -1;
+  if (st == XS_ROW_OK) {
+    if (!stoch) {
+      tok = (int)rdl(pk_id(sel[0]), 0);
+    } else {
+      F.wbuf[lane] = lane < k ? w[0] : 0.0f;
+      F.wbuf[64 + lane] = 64 + lane < k ? w[1] : 0.0f;
+      wave_lds_sync();
+      // serial sum of the first n weights, 32 per batch, in order
+      auto serial_sum = [&](int n) -> float {
+        float acc = -0.0f;
+        for (int b0 = 0; b0 < n; b0 += 32) {
+          float4 q[8];
+#pragma unroll
+          for (int u = 0; u < 8; u++) q[u] = reinterpret_cast<const float4*>(F.wbuf + b0)[u];
+          const float* qq = reinterpret_cast<const float*>(q);
+#pragma unroll
+          for (int u = 0; u < 32; u++)
+            if (b0 + u < n) acc += qq[u];
         }
-        float tw = L.w[0];
-        bool okw = tw >= 0.0f;
-        // cumulative weights: cum[i-1] = total before adding w[i]
-        float x_draw = 0.0f;
-        int idx = 0;
-        {
-          float tot = tw;
-          for (int i = 1; i < k; i++) {
-            if (!(L.w[i] >= 0.0f)) okw = false;
-            tot += L.w[i];
-          }
-          if (!okw || tot == 0.0f) {
-            st = XS_ROW_ZERO_WEIGHT;
-          } else {
-            x_draw = a.uniforms[row] * tot + 0.0f;
-            float run = tw;
-            for (int i = 1; i < k; i++) {
-              if (run <= x_draw) idx = i; else break;
-              run += L.w[i];
+        return acc;
+      };
+      if (!(cfg.top_p >= 1.0f)) {
+        const float sum = serial_sum(k);
+        if (sum > 0.0f) {
+          w[0] = lane < k ? __fdiv_rn(w[0], sum) : 0.0f;
+          w[1] = 64 + lane < k ? __fdiv_rn(w[1], sum) : 0.0f;
+          F.wbuf[lane] = w[0];
+          F.wbuf[64 + lane] = w[1];
+          wave_lds_sync();
+          // serial cumsum; keep = 1 + the first index where it reaches top_p
+          // (branch-free: a select per step, no early exit)
+          float csum = 0.0f;
+          int keep = k;
+          for (int b0 = 0; b0 < k && keep == k; b0 += 32) {
+            float4 q[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) q[u] = reinterpret_cast<const float4*>(F.wbuf + b0)[u];
+            const float* qq = reinterpret_cast<const float*>(q);
+#pragma unroll
+            for (int u = 0; u < 32; u++) {
+              const bool live = (b0 + u < k) && (keep == k);
+              const float nxt = csum + qq[u];
+              csum = live ? nxt : csum;
+              keep = (live && nxt >= cfg.top_p) ? b0 + u + 1 : keep;
             }
-            tok = (int)pk_id(L.psel[idx]);
           }
+          if (lane >= keep) w[0] = 0.0f;
+          if (64 + lane >= keep) w[1] = 0.0f;
+          F.wbuf[lane] = w[0];
+          F.wbuf[64 + lane] = w[1];
+          wave_lds_sync();
         }
       }
+      // WeightedIndex: cumulative weights cum[i-1] = w0 + ... + w[i-1] (serial
+      // f32), total = the same sum over all k, x = u * total; the index is the
+      // number of cumulative weights <= x.
+      const float tot = serial_sum(k);
+      bool okw = true;
+      if (lane < k && !(w[0] >= 0.0f)) okw = false;
+      if (64 + lane < k && !(w[1] >= 0.0f)) okw = false;
+      okw = __ballot(!okw) == 0;
+      if (!okw || tot == 0.0f) {
+        st = XS_ROW_ZERO_WEIGHT;
+      } else {
+        const float x_draw = a.uniforms[row] * tot + 0.0f;
+        // partition point of cum[i-1] <= x over i = 1..k-1 (branch-free)
+        float run = 0.0f;
+        int idx = 0;
+        bool stop = false;
+        for (int b0 = 0; b0 < k && !stop; b0 += 32) {
+          float4 q[8];
+#pragma unroll
+          for (int u = 0; u < 8; u++) q[u] = reinterpret_cast<const float4*>(F.wbuf + b0)[u];
+          const float* qq = reinterpret_cast<const float*>(q);
+#pragma unroll
+          for (int u = 0; u < 32; u++) {
+            const int i = b0 + u;
+            if (i == 0) {
+              run = qq[u];
+            } else {
+              const bool live = (i < k) && !stop;
+              const bool take = live && (run <= x_draw);
+              idx = take ? i : idx;
+              run = take ? run + qq[u] : run;
+              stop = stop || (live && !take);
+            }
+          }
+        }
+        tok = (int)pk_id(pick64(pk, idx));
+      }
     }
-    L.misc[5] = st;
-    L.misc[6] = tok;
   }
-  __syncthreads();
-  st = L.misc[5];
-  const int tok = L.misc[6];
 
-  // Outputs.
-  if (tid == 0) {
-    a.token[row] = st == XS_ROW_OK ? tok : -1;
-    a.status[row] = st;
+  // Outputs (sc1 stores: a verify walk on another wave reads token/status).
+  if (lane == 0) {
+    st_agent(&a.token[row], st == XS_ROW_OK ? tok : -1);
+    st_agent(&a.status[row], st);
     if (a.n_cand) a.n_cand[row] = (stoch && st == XS_ROW_OK) ? k : 0;
     if (a.soft_max) a.soft_max[row] = m_s;
     if (a.soft_sum) a.soft_sum[row] = S;
@@ -992,45 +1199,49 @@ __global__ __launch_bounds__(BLOCK) void sample_kernel(Args a) {
   }
   if (want_cands && stoch && st == XS_ROW_OK) {
     const int kw = (int)min((int64_t)k, a.cand_ld);  // a short cand_ld truncates the list
-    for (int i = tid; i < kw; i += BLOCK) {
-      if (a.cand_id) a.cand_id[(int64_t)row * a.cand_ld + i] = (int32_t)(0xFFFFFFFFu - (uint32_t)L.psel[i]);
-      if (a.cand_w) a.cand_w[(int64_t)row * a.cand_ld + i] = L.w[i];
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+      const int i = r * 64 + lane;
+      if (i < kw) {
+        if (a.cand_id) a.cand_id[(int64_t)row * a.cand_ld + i] = (int32_t)(0xFFFFFFFFu - (uint32_t)pk[r]);
+        if (a.cand_w) a.cand_w[(int64_t)row * a.cand_ld + i] = w[r];
+      }
     }
   }
   if (WANT_LSE && a.n_top > 0) {
     const bool ok = !nan_seen && !__builtin_isinf(m_v);
     const double lse = ok ? (double)m_v + log(R_d) : __builtin_nan("");
-    const int nt = (int)min((int64_t)a.n_top, enc);
-    for (int i = tid; i < a.n_top; i += BLOCK) {
-      const bool have = i < nt && i < nsel && !cfg.bad;
-      if (a.top_id) a.top_id[(int64_t)row * a.top_ld + i] = have ? (int32_t)pk_id(L.sel[i]) : -1;
-      if (a.top_logprob)
-        a.top_logprob[(int64_t)row * a.top_ld + i] = have ? (float)((double)keyf(pk_key(L.sel[i])) - lse) : __builtin_nanf("");
+    const int nt = min(a.n_top, enc);
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+      const int i = r * 64 + lane;
+      if (i < a.n_top) {
+        const bool have = i < nt && i < nsel && !cfg.bad && !any_stale;
+        if (a.top_id) a.top_id[(int64_t)row * a.top_ld + i] = have ? (int32_t)pk_id(sel[r]) : -1;
+        if (a.top_logprob)
+          a.top_logprob[(int64_t)row * a.top_ld + i] = have ? (float)((double)keyf(pk_key(sel[r])) - lse) : __builtin_nanf("");
+      }
     }
   }
 
   // Speculative verify: the last finalizer of a sequence walks its rows.
   if (a.span > 0) {
-    __threadfence();
-    __syncthreads();
+    drain();
     const int seq = row / a.span;
-    if (tid == 0) {
-      const int t = atomicAdd(&a.seq_ticket[seq], 1);
-      L.flag = (t == a.span - 1);
-      if (L.flag) a.seq_ticket[seq] = 0;
-    }
-    __syncthreads();
-    if (L.flag && tid == 0) {
-      __threadfence();
+    int ts = 0;
+    if (lane == 0) ts = __hip_atomic_fetch_add(&a.seq_ticket[seq], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    ts = __shfl(ts, 0);
+    if (ts == a.span - 1 && lane == 0) {
+      st_agent(&a.seq_ticket[seq], 0);
       const int span = a.span, D = span - 1;
       const int64_t r0 = (int64_t)seq * span;
       const int bud = a.budget ? a.budget[seq] : 0x7FFFFFFF;
       int mcount = 0, ncom = 0, sst = XS_ROW_OK;
       for (int i = 0; i < span; i++) {
         if (ncom >= bud) break;
-        const int rs = __atomic_load_n(&a.status[r0 + i], __ATOMIC_RELAXED);
+        const int rs = ld_agent(&a.status[r0 + i]);
         if (rs != XS_ROW_OK) { sst = rs; break; }
-        const int s = __atomic_load_n(&a.token[r0 + i], __ATOMIC_RELAXED);
+        const int s = ld_agent(&a.token[r0 + i]);
         const bool matched = i < D && s == a.drafts[(int64_t)seq * D + i];
         a.committed[(int64_t)seq * span + ncom] = s;
         ncom++;
@@ -1087,9 +1298,8 @@ struct xs_context {
   int64_t max_rows, vocab;
   int32_t k_max;
   int32_t max_chunks;
-  xs::Summary* summ;
-  uint32_t* pub;
-  uint64_t* cand;
+  uint32_t epoch;
+  uint64_t* rec;
   int32_t* row_ticket;
   int32_t* seq_ticket;
 };
@@ -1121,7 +1331,7 @@ int check_common(xs_context* ctx, const Call& c) {
   if (c.width > c.ld) return XS_ERR_ARG;
   if (c.enc > c.ld && c.width >= c.enc) return XS_ERR_ARG;
   if (c.allowed && (c.allowed_ld < c.allowed_words || c.allowed_words < 0)) return XS_ERR_ARG;
-  if (chunks_for(c.enc) > ctx->max_chunks || chunks_for(c.enc) > xs::BLOCK) return XS_ERR_CAPACITY;
+  if (chunks_for(c.enc) > ctx->max_chunks) return XS_ERR_CAPACITY;
   return XS_OK;
 }
 
@@ -1148,7 +1358,7 @@ int xs_create(int device, int64_t max_rows, int64_t vocab, int32_t k_max, xs_con
   *out = nullptr;
   if (hipSetDevice(device) != hipSuccess) return XS_ERR_HIP;
   const int32_t mc = chunks_for(vocab);
-  if (mc > xs::BLOCK) return XS_ERR_CAPACITY;
+  if (mc > 64) return XS_ERR_CAPACITY;  // a finalizing wave holds one chunk header per lane
   xs_context* c = (xs_context*)calloc(1, sizeof(xs_context));
   if (!c) return XS_ERR_HIP;
   c->device = device;
@@ -1158,9 +1368,8 @@ int xs_create(int device, int64_t max_rows, int64_t vocab, int32_t k_max, xs_con
   c->k_max = k_max;
   c->max_chunks = mc;
   const int64_t units = max_rows * (int64_t)mc;
-  bool ok = hipMalloc((void**)&c->summ, units * sizeof(xs::Summary)) == hipSuccess;
-  ok = ok && hipMalloc((void**)&c->pub, units * xs::NWAVE * xs::QPUB * sizeof(uint32_t)) == hipSuccess;
-  ok = ok && hipMalloc((void**)&c->cand, units * xs::CAP * sizeof(uint64_t)) == hipSuccess;
+  bool ok = hipMalloc((void**)&c->rec, units * xs::RECW * sizeof(uint64_t)) == hipSuccess;
+  ok = ok && hipMemset(c->rec, 0, units * xs::RECW * sizeof(uint64_t)) == hipSuccess;
   ok = ok && hipMalloc((void**)&c->row_ticket, max_rows * sizeof(int32_t)) == hipSuccess;
   ok = ok && hipMalloc((void**)&c->seq_ticket, max_rows * sizeof(int32_t)) == hipSuccess;
   ok = ok && hipMemset(c->row_ticket, 0, max_rows * sizeof(int32_t)) == hipSuccess;
@@ -1178,9 +1387,7 @@ int xs_destroy(xs_context* c) {
   if (!c) return XS_OK;
   (void)hipSetDevice(c->device);
   if (c->stream) (void)hipStreamSynchronize(c->stream); else (void)hipDeviceSynchronize();
-  (void)hipFree(c->summ);
-  (void)hipFree(c->pub);
-  (void)hipFree(c->cand);
+  (void)hipFree(c->rec);
   (void)hipFree(c->row_ticket);
   (void)hipFree(c->seq_ticket);
   free(c);
@@ -1241,9 +1448,9 @@ int xs_sample(xs_context* ctx, const xs_sample_args* in) {
   a.span = 0;
   a.n_chunks = chunks_for(in->enc);
   a.nslots = (int32_t)slots_for(in->enc);
-  a.summ = ctx->summ;
-  a.pub = ctx->pub;
-  a.cand = ctx->cand;
+  if (++ctx->epoch == 0) ctx->epoch = 1;
+  a.epoch = ctx->epoch;
+  a.rec = ctx->rec;
   a.row_ticket = ctx->row_ticket;
   a.seq_ticket = ctx->seq_ticket;
   return launch(ctx, a, in->rows, in->allowed != nullptr, lse);
@@ -1292,9 +1499,9 @@ int xs_verify(xs_context* ctx, const xs_verify_args* in) {
   a.seq_status = in->seq_status;
   a.n_chunks = chunks_for(in->enc);
   a.nslots = (int32_t)slots_for(in->enc);
-  a.summ = ctx->summ;
-  a.pub = ctx->pub;
-  a.cand = ctx->cand;
+  if (++ctx->epoch == 0) ctx->epoch = 1;
+  a.epoch = ctx->epoch;
+  a.rec = ctx->rec;
   a.row_ticket = ctx->row_ticket;
   a.seq_ticket = ctx->seq_ticket;
   return launch(ctx, a, rows, in->allowed != nullptr, false);

@@ -43,6 +43,7 @@ ROW_STATUS_NAMES = {
     _lib.ROW_ZERO_WEIGHT: "no candidate carries any probability mass after top-k/top-p filtering",
     _lib.ROW_NARROW: "logit row is narrower than the encodable ids the sampler draws over",
     _lib.ROW_BAD_PARAM: "top_k exceeds the sampler context's k_max",
+    _lib.ROW_INTERNAL: "device hand-off read an incomplete record (internal error)",
 }
 
 

@@ -143,29 +143,59 @@ XS_DEV uint32_t pk_id(uint64_t p) { return 0xFFFFFFFFu - (uint32_t)p; }
 XS_DEV int lane_id() { return threadIdx.x & 63; }
 XS_DEV int wave_id() { return threadIdx.x >> 6; }
 
+// Lane exchange with lane ^ d (d a power of two below 64, constant after
+// unrolling).  d = 1, 2: DPP quad permutes; d = 4: two DPP row rotates and a
+// select; d = 8: DPP row rotate; d = 16: ds_swizzle (bitmask mode); d = 32:
+// v_permlane32_swap.  All are register-to-register exchanges with no LDS
+// traffic, much shorter latency than ds_bpermute.
+XS_DEV int xor_lane(int v, int d) {
+  if (d == 1) return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+  if (d == 2) return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+  if (d == 4) {
+    const int up = __builtin_amdgcn_update_dpp(0, v, 0x12C, 0xF, 0xF, false);   // row_ror:12 -> lane+4
+    const int dn = __builtin_amdgcn_update_dpp(0, v, 0x124, 0xF, 0xF, false);   // row_ror:4  -> lane-4
+    return (threadIdx.x & 4) ? dn : up;
+  }
+  if (d == 8) return __builtin_amdgcn_update_dpp(0, v, 0x128, 0xF, 0xF, false);  // row_ror:8
+  if (d == 16) return __builtin_amdgcn_ds_swizzle(v, 0x401F);                     // lane ^ 16
+  const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);          // lane ^ 32
+  return (threadIdx.x & 32) ? (int)r[0] : (int)r[1];
+}
+XS_DEV uint32_t xor_u32(uint32_t v, int d) { return (uint32_t)xor_lane((int)v, d); }
+XS_DEV float xor_f32(float v, int d) { return __int_as_float(xor_lane(__float_as_int(v), d)); }
+XS_DEV double xor_f64(double v, int d) {
+  const long long b = __double_as_longlong(v);
+  const uint32_t lo = (uint32_t)xor_lane((int)(uint32_t)b, d);
+  const uint32_t hi = (uint32_t)xor_lane((int)(uint32_t)((unsigned long long)b >> 32), d);
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+
 XS_DEV float wave_maxf(float v) {
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, xor_f32(v, o));
   return v;
 }
 XS_DEV double wave_sumd(double v) {
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  for (int o = 32; o > 0; o >>= 1) v += xor_f64(v, o);
   return v;
 }
 XS_DEV uint32_t wave_or(uint32_t v) {
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v |= (uint32_t)__shfl_xor((int)v, o);
-  return v;
-}
-XS_DEV uint32_t wave_minu(uint32_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = min(v, (uint32_t)__shfl_xor((int)v, o));
+  for (int o = 32; o > 0; o >>= 1) v |= xor_u32(v, o);
   return v;
 }
 
+// Lane exchange for throughput-bound code (many waves per SIMD): ds_bpermute
+// runs in the LDS pipe and leaves the VALU to the streaming arithmetic.
+// Latency-bound single-wave code uses the DPP forms instead.
+template <bool DPP>
+XS_DEV uint32_t xshfl(uint32_t v, int d) {
+  return DPP ? (uint32_t)xor_lane((int)v, d) : (uint32_t)__shfl_xor((int)v, d);
+}
+
 // Bitonic sort, descending, of 64*R u32 keys held R per lane (element r*64+lane).
-template <int R>
+template <int R, bool DPP = true>
 XS_DEV void wave_sort_desc(uint32_t (&x)[R]) {
   const int lane = lane_id();
   constexpr int N = 64 * R;
@@ -188,7 +218,7 @@ XS_DEV void wave_sort_desc(uint32_t (&x)[R]) {
       } else {
 #pragma unroll
         for (int r = 0; r < R; r++) {
-          const uint32_t b = (uint32_t)__shfl_xor((int)x[r], d);
+          const uint32_t b = xshfl<DPP>(x[r], d);
           const bool desc = ((r * 64 + lane) & size) == 0;
           const bool lower = (lane & d) == 0;
           const uint32_t hi = max(x[r], b), lo = min(x[r], b);
@@ -199,16 +229,13 @@ XS_DEV void wave_sort_desc(uint32_t (&x)[R]) {
   }
 }
 
+XS_DEV int wave_incl_scan(int v);
+
 // Exclusive prefix sum over the block in thread order; *total gets the sum.
 // Contains barriers: call from block-uniform control flow only.
 XS_DEV int block_excl_scan(int v, int* s4, int* total) {
   const int lane = lane_id(), wave = wave_id();
-  int inc = v;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int t = __shfl_up(inc, o);
-    if (lane >= o) inc += t;
-  }
+  const int inc = wave_incl_scan(v);
   if (lane == 63) s4[wave] = inc;
   __syncthreads();
   int pre = 0, tot = 0;
@@ -345,26 +372,28 @@ XS_DEV uint64_t shfl64(uint64_t x, int src) {
   return ((uint64_t)hi << 32) | lo;
 }
 XS_DEV uint64_t shfl_xor64(uint64_t x, int m) {
-  const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)x, m);
-  const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(x >> 32), m);
+  const uint32_t lo = xor_u32((uint32_t)x, m);
+  const uint32_t hi = xor_u32((uint32_t)(x >> 32), m);
   return ((uint64_t)hi << 32) | lo;
 }
 // Lanes below this one whose bit is set in `mask`.
 XS_DEV int lanes_below(uint64_t mask) {
   return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
 }
+// Inclusive prefix sum over the wave: DPP row shifts within each row of 16,
+// then the row totals carried across rows with row broadcasts.
 XS_DEV int wave_incl_scan(int v) {
-  const int lane = lane_id();
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int t = __shfl_up(v, o);
-    if (lane >= o) v += t;
-  }
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, true);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, true);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, true);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, true);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false); // row_bcast:15 -> rows 1, 3
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false); // row_bcast:31 -> rows 2, 3
   return v;
 }
 XS_DEV int wave_sumi(int v) {
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  for (int o = 32; o > 0; o >>= 1) v += xor_lane(v, o);
   return v;
 }
 
@@ -428,7 +457,8 @@ constexpr int STG = 1024;           // finalizer staging words
 constexpr int NLM = 8;              // lane maxima a chunk publishes
 
 struct ChunkLds {
-  uint32_t lanemax[BLOCK];          // each wave's sorted lane maxima (the chunk bound)
+  uint32_t lanemax[BLOCK];          // lane maxima (the chunk bound)
+  uint32_t groupmax[BLOCK / 4];     // maxima of 4-lane groups
   uint64_t hits[NWAVE * CAPH];      // candidates, per wave; flat after an overflow
   int32_t nhit[NWAVE];
   int32_t misc[8];
@@ -441,7 +471,6 @@ struct FinLds {
   uint64_t stage[STG];              // the row's records as first loaded
   uint64_t list[SURV];              // gathered survivors
   uint64_t psel[KSEL];              // the candidate set in draw order: (p bits << 32) | ~id
-  float wbuf[KSEL];                 // weights for the serial draw
 };
 union Lds {
   ChunkLds c;
@@ -664,48 +693,43 @@ __global__ __launch_bounds__(BLOCK) void sample_kernel(Args a) {
     rsum_w = wave_sumd(rsum != 0.0 ? rsum * exp((double)moff - (double)offw) : 0.0);
   }
 
-  // Candidate bound: the K'-th largest of the block's 256 lane maxima (distinct
-  // elements, so at least K' elements of the chunk lie at or above it).  Each
-  // wave sorts its 64 lane maxima, then every wave merges the four sorted lists
-  // with two bitonic top-64 merges (max(A[i], B[63-i]) is bitonic and holds the
-  // top 64 of A u B), or sorts all 256 when K' > 64.
+  // Candidate bound: the K'-th largest of a set of distinct chunk elements, so
+  // at least K' elements of the chunk lie at or above it.  For K' <= 64 the set
+  // is the 64 maxima of 4-lane groups (each group holds 4 x 64 logits); for
+  // K' > 64 it is all 256 lane maxima.  Wave 0 sorts the set; the chunk also
+  // publishes its 8 largest members for the row-level bound.
   {
-    uint32_t srt[1] = {fkey(m)};
-    wave_sort_desc<1>(srt);
-    L.c.lanemax[wave * 64 + lane] = srt[0];
+    const uint32_t km = fkey(m);
+    uint32_t g = max(km, (uint32_t)__shfl_xor((int)km, 1));
+    g = max(g, (uint32_t)__shfl_xor((int)g, 2));
+    if ((lane & 3) == 0) L.c.groupmax[wave * 16 + (lane >> 2)] = g;
+    L.c.lanemax[wave * 64 + lane] = km;
   }
   __syncthreads();
-  uint32_t top, tau_key = 0;
-  if (kp <= 64) {
-    uint32_t c1 = max(L.c.lanemax[lane], L.c.lanemax[64 + 63 - lane]);
-    uint32_t c2 = max(L.c.lanemax[128 + lane], L.c.lanemax[192 + 63 - lane]);
-#pragma unroll
-    for (int d = 32; d > 0; d >>= 1) {
-      const uint32_t b1 = (uint32_t)__shfl_xor((int)c1, d);
-      const uint32_t b2 = (uint32_t)__shfl_xor((int)c2, d);
-      const bool lower = (lane & d) == 0;
-      c1 = lower ? max(c1, b1) : min(c1, b1);
-      c2 = lower ? max(c2, b2) : min(c2, b2);
+  uint32_t top = 0;
+  if (wave == 0) {
+    uint32_t tk = 0;
+    if (kp <= 64) {
+      uint32_t x[1] = {L.c.groupmax[lane]};
+      wave_sort_desc<1, true>(x);
+      top = x[0];
+      tk = rdl(x[0], kp - 1);
     }
-    uint32_t c = max(c1, (uint32_t)__shfl((int)c2, 63 - lane));
+    if (kp > 64 || tk <= fkey(-INFINITY)) {
+      uint32_t all[4];
 #pragma unroll
-    for (int d = 32; d > 0; d >>= 1) {
-      const uint32_t b = (uint32_t)__shfl_xor((int)c, d);
-      c = ((lane & d) == 0) ? max(c, b) : min(c, b);
+      for (int r = 0; r < 4; r++) all[r] = L.c.lanemax[r * 64 + lane];
+      wave_sort_desc<4, true>(all);
+      top = all[0];
+      const int i = kp - 1;  // < 256
+#pragma unroll
+      for (int r = 0; r < 4; r++)
+        if ((i >> 6) == r) tk = rdl(all[r], i & 63);
     }
-    top = c;
-    tau_key = rdl(c, kp - 1);
-  } else {
-    uint32_t all[4];
-#pragma unroll
-    for (int r = 0; r < 4; r++) all[r] = L.c.lanemax[r * 64 + lane];
-    wave_sort_desc<4>(all);
-    top = all[0];
-    const int i = kp - 1;  // < 256
-#pragma unroll
-    for (int r = 0; r < 4; r++)
-      if ((i >> 6) == r) tau_key = rdl(all[r], i & 63);
+    if (lane == 0) L.c.misc[NWAVE + 1] = (int32_t)tk;
   }
+  __syncthreads();
+  const uint32_t tau_key = (uint32_t)L.c.misc[NWAVE + 1];
   const float tau = keyf(tau_key);
 
   // Filter: this wave's elements at or above the bound, compacted with ballots
@@ -716,16 +740,19 @@ __global__ __launch_bounds__(BLOCK) void sample_kernel(Args a) {
   int count = 0;
 #pragma unroll
   for (int j = 0; j < SPC; j++) {
+    const float gm = fmaxf(fmaxf(v[4 * j], v[4 * j + 1]), fmaxf(v[4 * j + 2], v[4 * j + 3]));
+    if (__ballot(gm >= tau && j < ns)) {
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
-      const float x = v[4 * j + e];
-      const int id = base_id + j * SLOT + e;
-      const bool hit = x >= tau && j < ns && id < enc;
-      const uint64_t b = __ballot(hit);
-      if (b) {
-        const int pos = count + lanes_below(b);
-        if (hit && pos < CAPH) hw[pos] = pack(fkey(x), (uint32_t)id);
-        count += __popcll(b);
+      for (int e = 0; e < 4; e++) {
+        const float x = v[4 * j + e];
+        const int id = base_id + j * SLOT + e;
+        const bool hit = x >= tau && j < ns && id < enc;
+        const uint64_t b = __ballot(hit);
+        if (b) {
+          const int pos = count + lanes_below(b);
+          if (hit && pos < CAPH) hw[pos] = pack(fkey(x), (uint32_t)id);
+          count += __popcll(b);
+        }
       }
     }
   }
@@ -798,7 +825,7 @@ __global__ __launch_bounds__(BLOCK) void sample_kernel(Args a) {
   drain();
   int t = 0;
   if (lane == 0) t = __hip_atomic_fetch_add(&a.row_ticket[row], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  t = __shfl(t, 0);
+  t = (int)rdl((uint32_t)t, 0);
   const int nc = a.n_chunks;
   if (t != nc - 1) return;
   if (lane == 0) st_agent(&a.row_ticket[row], 0);
@@ -807,7 +834,11 @@ __global__ __launch_bounds__(BLOCK) void sample_kernel(Args a) {
   // All of the row's records, STG words at most, in one round of loads.
   FinLds& F = L.f;
   const uint64_t* rr = a.rec + (int64_t)row * nc * RECW;
-  const int w1 = min(RECW, STG / nc);  // words of each record staged (>= HDR + 8)
+  // staging stride: odd in u64 words, so lanes reading one word of each record
+  // fall in different LDS banks
+  const int sst = ((STG / nc) & 1) ? STG / nc : STG / nc - 1;
+  const int w1 = min(RECW, sst);  // words of each record staged (>= HDR + 7)
+  const float u_row = a.uniforms[row];  // prefetched for the draw
   {
     constexpr int NB = STG / 64;
     uint64_t sv[NB];
@@ -822,7 +853,10 @@ __global__ __launch_bounds__(BLOCK) void sample_kernel(Args a) {
     }
 #pragma unroll
     for (int u = 0; u < NB; u++)
-      if (u * 64 + lane < nc * w1) F.stage[u * 64 + lane] = sv[u];
+      if (u * 64 + lane < nc * w1) {
+        const int i = u * 64 + lane, c = i / w1;
+        F.stage[c * sst + (i - c * w1)] = sv[u];
+      }
   }
   wave_lds_sync();
   // Lane c holds chunk c's header (nc <= 64 is enforced by the host).
@@ -832,16 +866,16 @@ __global__ __launch_bounds__(BLOCK) void sample_kernel(Args a) {
   int cc = 0;
   bool stale = false;
   if (lane < nc) {
-    uint64_t h3 = F.stage[lane * w1 + 3];
+    uint64_t h3 = F.stage[lane * sst + 3];
     if ((uint32_t)h3 != a.epoch) {
       // not visible yet: re-read the record (bounded), then restage its words
       for (int spin = 0; spin < 1000 && (uint32_t)h3 != a.epoch; spin++) h3 = ld_agent(rr + (int64_t)lane * RECW + 3);
       stale = (uint32_t)h3 != a.epoch;
-      for (int k = 0; k < w1; k++) F.stage[lane * w1 + k] = ld_agent(rr + (int64_t)lane * RECW + k);
+      for (int k = 0; k < w1; k++) F.stage[lane * sst + k] = ld_agent(rr + (int64_t)lane * RECW + k);
     }
-    const uint64_t h0 = F.stage[lane * w1 + 0];
-    const uint64_t h1 = F.stage[lane * w1 + 1];
-    const uint64_t h2 = F.stage[lane * w1 + 2];
+    const uint64_t h0 = F.stage[lane * sst + 0];
+    const uint64_t h1 = F.stage[lane * sst + 1];
+    const uint64_t h2 = F.stage[lane * sst + 2];
     cv = __uint_as_float((uint32_t)h0);
     cs = __uint_as_float((uint32_t)(h0 >> 32));
     cr = __longlong_as_double((long long)h1);
@@ -879,16 +913,18 @@ __global__ __launch_bounds__(BLOCK) void sample_kernel(Args a) {
   // (distinct elements; NLM per chunk, up to 256 values).
   uint32_t tau_row = 0;
   {
-    const int nv = min(nc * NLM, 256);
+    int q = NLM;  // members of each chunk's list used (sorted, largest first)
+    while (q > 1 && nc * q > 64 && nc * (q - 1) >= kp) q--;
+    const int nv = min(nc * q, 256);
     if (nv >= kp) {
       uint32_t x[4];
 #pragma unroll
       for (int r = 0; r < 4; r++) {
         const int i = r * 64 + lane;
-        const int c = i / NLM, k = i - c * NLM;
+        const int c = i / q, k = i - c * q;
         x[r] = 0u;
         if (i < nv) {
-          const uint64_t wv = F.stage[c * w1 + 4 + (k >> 1)];
+          const uint64_t wv = F.stage[c * sst + 4 + (k >> 1)];
           x[r] = (k & 1) ? (uint32_t)(wv >> 32) : (uint32_t)wv;
         }
       }
@@ -910,52 +946,73 @@ __global__ __launch_bounds__(BLOCK) void sample_kernel(Args a) {
     }
   }
   // Gather the survivors (entries at or above the bound) into LDS: lane c
-  // reads chunk c's entries eight at a time (staged words first, the rest from
-  // the workspace); a wave prefix sum places them.
+  // reads chunk c's staged entries eight at a time, then (rarely) the entries
+  // past the staged words from the workspace; a wave prefix sum places them.
   int maxc = cc;
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) maxc = max(maxc, __shfl_xor(maxc, o));
+  for (int o = 32; o > 0; o >>= 1) maxc = max(maxc, xor_lane(maxc, o));
+  const int nstg = w1 - HDR;  // entries of each record in the staging area
+  const int cst = min(cc, nstg);
   uint64_t floor_e = (uint64_t)tau_row << 32;
   int M = 0;
-  for (int pass = 0; pass < 2; pass++) {
-    M = 0;
-    for (int j0 = 0; j0 < maxc; j0 += 8) {
+  auto gather = [&](uint64_t floor_v) __attribute__((always_inline)) -> int {
+    int m = 0;
+    const int mst = min(maxc, nstg);
+    for (int j0 = 0; j0 < mst; j0 += 8) {
       uint64_t e[8];
 #pragma unroll
-      for (int u = 0; u < 8; u++) {
-        const int j = j0 + u;
-        e[u] = 0ull;
-        if (j < cc) e[u] = (HDR + j < w1) ? F.stage[lane * w1 + HDR + j] : ld_agent(rr + (int64_t)lane * RECW + HDR + j);
-      }
+      for (int u = 0; u < 8; u++) e[u] = F.stage[lane * sst + HDR + min(j0 + u, nstg - 1)];
       int h = 0;
 #pragma unroll
-      for (int u = 0; u < 8; u++) h += (j0 + u < cc && e[u] >= floor_e) ? 1 : 0;
+      for (int u = 0; u < 8; u++) h += (j0 + u < cst && e[u] >= floor_v) ? 1 : 0;
       const int incl = wave_incl_scan(h);
-      int pos = M + incl - h;
+      int pos = m + incl - h;
 #pragma unroll
       for (int u = 0; u < 8; u++)
-        if (j0 + u < cc && e[u] >= floor_e) {
+        if (j0 + u < cst && e[u] >= floor_v) {
           if (pos < SURV) F.list[pos] = e[u];
           pos++;
         }
-      M += __shfl(incl, 63);
+      m += (int)rdl((uint32_t)incl, 63);
     }
-    if (M <= SURV) break;
+    for (int j0 = nstg; j0 < maxc; j0 += 8) {  // entries past the staging area
+      uint64_t e[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        const int j = min(j0 + u, CAPB - 1);
+        e[u] = (j0 + u < cc) ? ld_agent(rr + (int64_t)lane * RECW + HDR + j) : 0ull;
+      }
+      int h = 0;
+#pragma unroll
+      for (int u = 0; u < 8; u++) h += (j0 + u < cc && e[u] >= floor_v) ? 1 : 0;
+      const int incl = wave_incl_scan(h);
+      int pos = m + incl - h;
+#pragma unroll
+      for (int u = 0; u < 8; u++)
+        if (j0 + u < cc && e[u] >= floor_v) {
+          if (pos < SURV) F.list[pos] = e[u];
+          pos++;
+        }
+      m += (int)rdl((uint32_t)incl, 63);
+    }
+    return m;
+  };
+  M = gather(floor_e);
+  if (M > SURV) {
     // More survivors than one wave sorts (ties at the bound across many
-    // chunks): move the floor to the exact K'-th largest entry by bisection.
+    // chunks): move the floor to the exact K'-th largest entry by bisection
+    // over the entries, then gather again.
     uint64_t ans = 0;
     for (int bit = 63; bit >= 0; bit--) {
       const uint64_t cnd = ans | (1ull << bit);
       int c = 0;
-      for (int j = 0; j < cc; j++) {
-        const uint64_t e = (HDR + j < w1) ? F.stage[lane * w1 + HDR + j] : ld_agent(rr + (int64_t)lane * RECW + HDR + j);
-        c += e >= cnd ? 1 : 0;
-      }
+      for (int j = 0; j < cst; j++) c += F.stage[lane * sst + HDR + j] >= cnd ? 1 : 0;
+      for (int j = cst; j < cc; j++) c += ld_agent(rr + (int64_t)lane * RECW + HDR + j) >= cnd ? 1 : 0;
       if (wave_sumi(c) >= kp) ans = cnd;
     }
     floor_e = ans;
+    M = gather(floor_e);
   }
-  wave_lds_sync();
   // Sort the survivors (logit desc, id asc); the first K' are the selection.
   uint64_t sel[4];
 #pragma unroll
@@ -1071,7 +1128,7 @@ __global__ __launch_bounds__(BLOCK) void sample_kernel(Args a) {
               if (pos < need) F.psel[have + pos] = ((uint64_t)__float_as_uint(Pk + 0.0f) << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)(4 * f + e));
               pos++;
             }
-          const int tot = __shfl(incl, 63);
+          const int tot = (int)rdl((uint32_t)incl, 63);
           have += min(tot, need);
           need -= tot;
         }
@@ -1083,8 +1140,9 @@ __global__ __launch_bounds__(BLOCK) void sample_kernel(Args a) {
   }
 
   // The draw: truncate_top_p (sampler.rs:401-429) and WeightedIndex
-  // (sampler.rs:235-243, rand 0.9) in serial f32.  Every lane reads the same
-  // weights from LDS, 32 at a time, and computes the same uniform results.
+  // (sampler.rs:235-243, rand 0.9) in serial f32.  Weight i lives in lane
+  // i % 64 of w[i / 64]; the serial chains read it with v_readlane, eight per
+  // batch, and every lane carries the same uniform running values.
   float w[2];
   w[0] = __uint_as_float((uint32_t)(pk[0] >> 32));
   w[1] = __uint_as_float((uint32_t)(pk[1] >> 32));
@@ -1093,92 +1151,75 @@ __global__ __launch_bounds__(BLOCK) void sample_kernel(Args a) {
     if (!stoch) {
       tok = (int)rdl(pk_id(sel[0]), 0);
     } else {
-      F.wbuf[lane] = lane < k ? w[0] : 0.0f;
-      F.wbuf[64 + lane] = 64 + lane < k ? w[1] : 0.0f;
-      wave_lds_sync();
-      // serial sum of the first n weights, 32 per batch, in order
-      auto serial_sum = [&](int n) -> float {
+      if (lane >= k) w[0] = 0.0f;
+      if (64 + lane >= k) w[1] = 0.0f;
+#define XS_W(i) __uint_as_float(rdl(__float_as_uint(((i) < 64) ? w[0] : w[1]), (i) & 63))
+      // serial f32 sum of w[0..k), the order Iterator::sum folds in
+      auto serial_sum = [&]() __attribute__((always_inline)) -> float {
         float acc = -0.0f;
-        for (int b0 = 0; b0 < n; b0 += 32) {
-          float4 q[8];
+        for (int b0 = 0; b0 < k; b0 += 8) {
+          float q[8];
 #pragma unroll
-          for (int u = 0; u < 8; u++) q[u] = reinterpret_cast<const float4*>(F.wbuf + b0)[u];
-          const float* qq = reinterpret_cast<const float*>(q);
+          for (int u = 0; u < 8; u++) q[u] = XS_W(b0 + u);
 #pragma unroll
-          for (int u = 0; u < 32; u++)
-            if (b0 + u < n) acc += qq[u];
+          for (int u = 0; u < 8; u++) acc = (b0 + u < k) ? acc + q[u] : acc;
         }
         return acc;
       };
       if (!(cfg.top_p >= 1.0f)) {
-        const float sum = serial_sum(k);
+        const float sum = serial_sum();
         if (sum > 0.0f) {
-          w[0] = lane < k ? __fdiv_rn(w[0], sum) : 0.0f;
-          w[1] = 64 + lane < k ? __fdiv_rn(w[1], sum) : 0.0f;
-          F.wbuf[lane] = w[0];
-          F.wbuf[64 + lane] = w[1];
-          wave_lds_sync();
+          w[0] = __fdiv_rn(w[0], sum);
+          w[1] = __fdiv_rn(w[1], sum);
           // serial cumsum; keep = 1 + the first index where it reaches top_p
-          // (branch-free: a select per step, no early exit)
           float csum = 0.0f;
           int keep = k;
-          for (int b0 = 0; b0 < k && keep == k; b0 += 32) {
-            float4 q[8];
+          for (int b0 = 0; b0 < k && keep == k; b0 += 8) {
+            float q[8];
 #pragma unroll
-            for (int u = 0; u < 8; u++) q[u] = reinterpret_cast<const float4*>(F.wbuf + b0)[u];
-            const float* qq = reinterpret_cast<const float*>(q);
+            for (int u = 0; u < 8; u++) q[u] = XS_W(b0 + u);
 #pragma unroll
-            for (int u = 0; u < 32; u++) {
+            for (int u = 0; u < 8; u++) {
               const bool live = (b0 + u < k) && (keep == k);
-              const float nxt = csum + qq[u];
+              const float nxt = csum + q[u];
               csum = live ? nxt : csum;
               keep = (live && nxt >= cfg.top_p) ? b0 + u + 1 : keep;
             }
           }
           if (lane >= keep) w[0] = 0.0f;
           if (64 + lane >= keep) w[1] = 0.0f;
-          F.wbuf[lane] = w[0];
-          F.wbuf[64 + lane] = w[1];
-          wave_lds_sync();
         }
       }
-      // WeightedIndex: cumulative weights cum[i-1] = w0 + ... + w[i-1] (serial
-      // f32), total = the same sum over all k, x = u * total; the index is the
-      // number of cumulative weights <= x.
-      const float tot = serial_sum(k);
-      bool okw = true;
-      if (lane < k && !(w[0] >= 0.0f)) okw = false;
-      if (64 + lane < k && !(w[1] >= 0.0f)) okw = false;
+      // WeightedIndex: total = the serial sum; cumulative weights cum[i-1] =
+      // w0 + ... + w[i-1]; x = u * total; the index is the number of
+      // cumulative weights <= x.
+      const float tot = serial_sum();
+      bool okw = !(lane < k && !(w[0] >= 0.0f)) && !(64 + lane < k && !(w[1] >= 0.0f));
       okw = __ballot(!okw) == 0;
       if (!okw || tot == 0.0f) {
         st = XS_ROW_ZERO_WEIGHT;
       } else {
-        const float x_draw = a.uniforms[row] * tot + 0.0f;
-        // partition point of cum[i-1] <= x over i = 1..k-1 (branch-free)
-        float run = 0.0f;
+        const float x_draw = u_row * tot + 0.0f;
+        float run = XS_W(0);
         int idx = 0;
         bool stop = false;
-        for (int b0 = 0; b0 < k && !stop; b0 += 32) {
-          float4 q[8];
+        for (int b0 = 1; b0 < k && !stop; b0 += 8) {
+          float q[8];
 #pragma unroll
-          for (int u = 0; u < 8; u++) q[u] = reinterpret_cast<const float4*>(F.wbuf + b0)[u];
-          const float* qq = reinterpret_cast<const float*>(q);
+          for (int u = 0; u < 8; u++) q[u] = XS_W(b0 + u);
 #pragma unroll
-          for (int u = 0; u < 32; u++) {
+          for (int u = 0; u < 8; u++) {
             const int i = b0 + u;
-            if (i == 0) {
-              run = qq[u];
-            } else {
-              const bool live = (i < k) && !stop;
-              const bool take = live && (run <= x_draw);
-              idx = take ? i : idx;
-              run = take ? run + qq[u] : run;
-              stop = stop || (live && !take);
-            }
+            const bool live = (i < k) && !stop;
+            const bool take = live && (run <= x_draw);
+            idx = take ? i : idx;
+            run = take ? run + q[u] : run;
+            stop = stop || (live && !take);
           }
         }
         tok = (int)pk_id(pick64(pk, idx));
       }
+#undef XS_W
     }
   }
 
@@ -1230,7 +1271,7 @@ __global__ __launch_bounds__(BLOCK) void sample_kernel(Args a) {
     const int seq = row / a.span;
     int ts = 0;
     if (lane == 0) ts = __hip_atomic_fetch_add(&a.seq_ticket[seq], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    ts = __shfl(ts, 0);
+    ts = (int)rdl((uint32_t)ts, 0);
     if (ts == a.span - 1 && lane == 0) {
       st_agent(&a.seq_ticket[seq], 0);
       const int span = a.span, D = span - 1;

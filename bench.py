@@ -9,7 +9,9 @@ exceeds the 256 MiB Infinity Cache, so every step streams its rows from HBM.
 Prints one JSON line (rank 0, N = 1):
   value      rows/s over the timed region (whole job, one GPU)
   roofline   algorithmic bytes per launch (64 x 993,280 B) / mean launch time,
-             against MI355X's 8 TB/s HBM peak
+             against MI355X's 8 TB/s HBM peak; `traffic` is the HBM bytes per
+             launch that rocprofv3's FETCH_SIZE + WRITE_SIZE counters measured
+             (profiles/sample_kernel_c2_traffic.md)
   cpu_baseline  the CPU oracle's restatement of the reference sampler (serial
              f32 softmax with libm expf, streaming top-k, top-p, WeightedIndex),
              one thread, on a bounded sample of the same rows
@@ -59,6 +61,19 @@ def cpu_baseline(wl, seconds: float) -> dict:
     return {"value": round(done / dt, 2), "unit": "rows/s", "cores": 1, "kind": "port",
             "sample": f"{reps} passes over the {rows} batch rows (V=248,320), 1 thread, "
                       f"oracle control path with libm expf, {dt:.1f} s"}
+
+
+def measured_traffic() -> int | None:
+    """HBM bytes per sampler launch from the committed rocprofv3 FETCH_SIZE +
+    WRITE_SIZE passes (scaled by a plain copy of known size), or None."""
+    path = os.path.join(ROOT, "profiles", "sample_kernel_c2_traffic.md")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
 
 
 def calibrate_copy(nbytes: int, reps: int) -> None:
@@ -222,7 +237,8 @@ def main() -> int:
                    "rotating_buffers": args.nbuf,
                    "buffer_bytes_total": args.nbuf * alg_bytes},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic()},
     }
     if not args.no_cpu_baseline:
         log(f"CPU baseline (~{args.cpu_seconds:.0f} s)")

@@ -76,7 +76,8 @@ XS_DEV float neighbour(float f, double t) {
   return __uint_as_float(up ? u + 1u : u - 1u);
 }
 
-XS_DEV float cr_expf(float xf) {
+template <typename TAB>
+XS_DEV float cr_expf(float xf, TAB T) {
   if (xf != xf) return xf + xf;
   if (xf < -104.0f) return 0.0f;
   if (xf > 89.0f) return __builtin_huge_valf();
@@ -99,7 +100,7 @@ XS_DEV float cr_expf(float xf) {
   const double ul = (r1 - (uh - bb)) + (w - bb);
   const int j = k & 31;
   const int e = (k - j) / 32;
-  const double th = kExpT[j][0], tl = kExpT[j][1];
+  const double th = T[2 * j], tl = T[2 * j + 1];
   const double p1 = th * uh;
   const double e1 = __builtin_fma(th, uh, -p1);
   const double s = th + p1;
@@ -334,7 +335,7 @@ struct Args {
   // geometry + workspace
   int32_t n_chunks, nslots;
   uint32_t epoch;
-  uint64_t* rec;     // [rows, n_chunks, RECW]: one record per chunk
+  uint64_t* rec;     // [rows, SRECW, nsp]: word i of sub-record s of a row at i * nsp + s
   int32_t* row_ticket;
   int32_t* seq_ticket;
 };
@@ -442,35 +443,38 @@ XS_DEV uint64_t pick64(const uint64_t (&x)[R], int i) {
   return out;
 }
 
-// Record of one chunk in the workspace, RECW u64 words:
-//   w0  ssum bits << 32 | vmax bits     (softmax partial sum, chunk max)
-//   w1  rsum bits                       (held_row f64 partial sum)
-//   w2  count << 32 | flags
-//   w3  epoch
-//   w4..w7  the chunk's 8 largest lane maxima (u32 keys, two per word)
-//   w8..    count candidate entries
-constexpr int HDR = 8;
-constexpr int CAPB = 1024;          // candidate entries per chunk
-constexpr int RECW = HDR + CAPB;
-constexpr int CAPH = 256;           // candidate entries per wave before the overflow path
-constexpr int STG = 1024;           // finalizer staging words
-constexpr int NLM = 8;              // lane maxima a chunk publishes
+// Sub-record of one wave of one chunk in the workspace, SRECW u64 words:
+//   w0  P (f64 bits): sum over the wave's elements of e^(s - c_s), s the
+//       scaled, controlled logit (the softmax partial)
+//   w1  c_s (f32 bits) | c_r (f32 bits) << 32: the partials' offsets
+//   w2  R (f64 bits): sum of e^(v - c_r) over the raw logits (held_row)
+//   w3  wave max (f32 bits) | flags << 32
+//   w4  entry count | epoch << 32
+//   w5  bound keys 0 | 1 << 32;  w6  bound keys 2 | 3 << 32
+//   w8..  entries: pack(key, id) of the wave's candidates
+// A row has n_chunks * NWAVE sub-records, chunk-major, stored transposed:
+// word i of sub-record s sits at i * nsp + s of the row's block (nsp = the
+// sub-record count rounded up to 64), so the finalizer's lanes read one word
+// of 64 sub-records with one coalesced load.
+constexpr int SHDR = 8;
+constexpr int CAPW = 256;           // entries per sub-record
+constexpr int SRECW = SHDR + CAPW;
+constexpr int NHW = 7;              // header words the finalizer reads
+constexpr int EPRE = 16;            // entries per sub-record read with the headers
+constexpr int GMAX = 4;             // sub-record groups of 64 a finalizer handles
+constexpr uint32_t KEY_NEG_INF = 0x007FFFFFu;  // fkey(-inf)
+constexpr double LN2D = 0.693147180559945309417;
 
 struct ChunkLds {
-  uint32_t lanemax[BLOCK];          // lane maxima (the chunk bound)
   uint32_t groupmax[BLOCK / 4];     // maxima of 4-lane groups
-  uint64_t hits[NWAVE * CAPH];      // candidates, per wave; flat after an overflow
-  int32_t nhit[NWAVE];
-  int32_t misc[8];
-  float wm[NWAVE];                  // each wave's max, flags and partial sums
-  uint32_t wf[NWAVE];
-  double ws[NWAVE];
-  double wr[NWAVE];
+  uint32_t lanemax[BLOCK];          // lane maxima
+  int32_t arrive;                   // waves of this workgroup that have published
 };
 struct FinLds {
-  uint64_t stage[STG];              // the row's records as first loaded
   uint64_t list[SURV];              // gathered survivors
   uint64_t psel[KSEL];              // the candidate set in draw order: (p bits << 32) | ~id
+  double expt[64];                  // kExpT, flattened
+  uint32_t keys[GMAX * 64 * 4];     // published bound keys (more than 64 sub-records)
 };
 union Lds {
   ChunkLds c;
@@ -479,9 +483,11 @@ union Lds {
 
 // p = rn(e / S) of one controlled logit v (the reference's softmax_in_place:
 // v *= inv unless T == 1, then exp(v - max), then / sum; sampler.rs:289-310).
-XS_DEV float exact_p(float v, const Cfg& cfg, float m_s, float S) {
+// T: the 2^(j/32) table (kExpT flattened), here the finalizer's LDS copy.
+template <typename TAB>
+XS_DEV float exact_p(float v, const Cfg& cfg, float m_s, float S, TAB T) {
   const float s = cfg.scale ? v * cfg.inv : v;
-  const float e = cr_expf(s - m_s);
+  const float e = cr_expf(s - m_s, T);
   return __fdiv_rn(e, S);
 }
 
@@ -492,413 +498,434 @@ XS_DEV float next_below(float f) {
   return __uint_as_float(f > 0.0f ? b - 1u : b + 1u);
 }
 
+XS_DEV float xexp2(float x) { return __builtin_amdgcn_exp2f(x); }
+// max without the sNaN-quieting canonicalisation fmaxf brings: a NaN operand
+// may or may not survive, which is fine wherever a NaN already fails the row
+XS_DEV float vmax(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+XS_DEV float vmax3(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+XS_DEV float q4(const v4f& q, int e) { return e == 0 ? q.x : e == 1 ? q.y : e == 2 ? q.z : q.w; }
+
 // ---------------------------------------------------------------------------
-// Rare path of the chunk pass: more than CAPH of a wave's elements lie at or
-// above the chunk bound (ties at the bound: constant or masked stretches).
-// Writes the chunk's exact K' best (logit desc, id asc) into `out`: everything
-// strictly above a threshold, then the lowest ids equal to it.  When even the
-// strict set would not fit, the threshold first moves to the chunk's exact
-// K'-th largest key by bisection.  Re-reads the chunk from memory so the
-// streaming path keeps no registers for it.  Every lane of the block calls it
-// (it contains barriers); returns the entry count.
-template <bool HAS_MASK>
-__device__ __noinline__ int chunk_overflow(const float* rowp, const uint32_t* mrow, int s0, int ns,
-                                           int enc, uint32_t tau_key, int kp, uint64_t* out,
-                                           int32_t* s4, int32_t* counter) {
-  const int tid = threadIdx.x;
-  // element e of this lane in slot j; NaN marks an absent element
-  auto load = [&](int j, int e, int* idp) -> float {
-    const int id = (s0 + j) * SLOT + 4 * tid + e;
-    *idp = id;
-    if (j >= ns || id >= enc) return __builtin_nanf("");
-    float x = rowp[id];
-    if (HAS_MASK && !((mrow[id >> 5] >> (id & 31)) & 1u)) x = -INFINITY;
-    return x;
-  };
-  auto count_ge = [&](uint32_t key, bool strict) -> int {
+// Rare path of the chunk pass: more than CAPW of this wave's elements lie at
+// or above the chunk bound (ties at the bound, or a bound far below the
+// wave's values).  Writes the wave's exact K' best (logit desc, id asc)
+// elements from its registers: every key above a threshold key, then the
+// lowest ids equal to it.  The threshold is the bound when fewer than K' keys
+// lie strictly above it, else the wave's K'-th largest key (bisection).
+// Elements that are -inf or NaN never become candidates.  Returns the count.
+XS_DEV int wave_overflow(const v4f (&q)[SPC], uint64_t* sub, int nsp, int kp, uint32_t tk, int base_id) {
+  const int lane = lane_id();
+  auto valid = [](float x) __attribute__((always_inline)) { return x == x && x > -INFINITY; };
+  auto count = [&](uint32_t key, bool strict) __attribute__((always_inline)) -> int {
     int c = 0;
-    for (int j = 0; j < ns; j++)
+#pragma unroll
+    for (int j = 0; j < SPC; j++)
+#pragma unroll
       for (int e = 0; e < 4; e++) {
-        int id;
-        const float x = load(j, e, &id);
-        if (x == x) c += strict ? (fkey(x) > key) : (fkey(x) >= key);
+        const float x = q4(q[j], e);
+        const uint32_t k = fkey(x);
+        c += (valid(x) && (strict ? k > key : k >= key)) ? 1 : 0;
       }
-    int tot;
-    block_excl_scan(c, s4, &tot);
-    return tot;
+    return wave_sumi(c);
   };
-  uint32_t eq_key = tau_key;
-  if (count_ge(tau_key, true) > CAPB - KSEL) {
+  uint32_t eq = max(tk, fkey(-__FLT_MAX__));
+  if (count(eq, true) >= kp) {
     uint32_t ans = 0;
     for (int bit = 31; bit >= 0; bit--) {
-      const uint32_t cnd = ans | (1u << bit);
-      if (count_ge(cnd, false) >= kp) ans = cnd;
+      const uint32_t cand = ans | (1u << bit);
+      if (count(cand, false) >= kp) ans = cand;
     }
-    eq_key = ans;
+    eq = ans;
   }
-  if (tid == 0) *counter = 0;
-  __syncthreads();
-  for (int j = 0; j < ns; j++)
+  int n = 0;
+#pragma unroll
+  for (int j = 0; j < SPC; j++)
+#pragma unroll
     for (int e = 0; e < 4; e++) {
-      int id;
-      const float x = load(j, e, &id);
-      if (x == x && fkey(x) > eq_key) {
-        const int pos = atomicAdd(counter, 1);
-        if (pos < CAPB) out[pos] = pack(fkey(x), (uint32_t)id);
-      }
+      const float x = q4(q[j], e);
+      const bool hit = valid(x) && fkey(x) > eq;
+      const uint64_t b = __ballot(hit);
+      const int pos = n + lanes_below(b);
+      if (hit && pos < CAPW) st_agent(sub + (int64_t)(SHDR + pos) * nsp, pack(fkey(x), (uint32_t)(base_id + j * SLOT + e)));
+      n += __popcll(b);
     }
-  __syncthreads();
-  const int gt = min(*counter, CAPB);
-  __syncthreads();
-  // ties at eq_key, lowest ids first: slot j covers ids s0*SLOT + j*SLOT +
-  // [0, SLOT) in lane order, so a block prefix count per slot is id order
-  int need = kp - gt, have = gt;
-  for (int j = 0; j < ns && need > 0; j++) {
-    int c = 0;
-    float xs[4];
-    int ids[4];
-    for (int e = 0; e < 4; e++) {
-      xs[e] = load(j, e, &ids[e]);
-      c += (xs[e] == xs[e] && fkey(xs[e]) == eq_key) ? 1 : 0;
-    }
-    int tot;
-    int pre = block_excl_scan(c, s4, &tot);
-    for (int e = 0; e < 4; e++)
-      if (xs[e] == xs[e] && fkey(xs[e]) == eq_key) {
-        if (pre < need) out[have + pre] = pack(eq_key, (uint32_t)ids[e]);
-        pre++;
+  n = min(n, CAPW);
+  // ties at eq, lowest ids first: slot j covers ids base + j*SLOT in lane order
+  int need = kp - n;
+#pragma unroll
+  for (int j = 0; j < SPC; j++) {
+    if (need > 0) {  // uniform; the loop stays unrolled so q[j] stays in registers
+      bool t[4];
+      int c = 0;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const float x = q4(q[j], e);
+        t[e] = valid(x) && fkey(x) == eq;
+        c += t[e] ? 1 : 0;
       }
-    have += min(tot, need);
-    need -= tot;
-    __syncthreads();
+      const int incl = wave_incl_scan(c);
+      int pos = incl - c;
+#pragma unroll
+      for (int e = 0; e < 4; e++)
+        if (t[e]) {
+          if (pos < need && n + pos < CAPW) st_agent(sub + (int64_t)(SHDR + n + pos) * nsp, pack(eq, (uint32_t)(base_id + j * SLOT + e)));
+          pos++;
+        }
+      const int tot = (int)rdl((uint32_t)incl, 63);
+      n += min(tot, need);
+      need -= tot;
+    }
   }
-  return have;
+  (void)lane;
+  return min(n, CAPW);
 }
 
 // ---------------------------------------------------------------------------
-// The kernel.
+// The kernel.  Grid: rows x n_chunks workgroups of BLOCK lanes; chunk c of a
+// row covers slots [c*SPC, c*SPC + SPC).  Every wave reduces its own share of
+// the chunk and publishes it as one sub-record; the row's last wave (atomic
+// ticket over all of the row's waves) finalizes the row.
 
 template <bool HAS_MASK, bool WANT_LSE>
-__global__ __launch_bounds__(BLOCK) void sample_kernel(Args a) {
+__global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) void sample_kernel(Args a) {
   __shared__ Lds L;
   const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
-  const int row = blockIdx.x / a.n_chunks;
-  const int chunk = blockIdx.x - row * a.n_chunks;
+  const int nc = a.n_chunks;
+  const int row = blockIdx.x / nc;
+  const int chunk = blockIdx.x - row * nc;
   const int enc = (int)a.enc;
   const Cfg cfg = make_cfg(a.params[row], a.enc, a.n_top);
   const bool stoch = !cfg.greedy && !cfg.bad;
   const int kp = cfg.kp;
 
   // ---------------- chunk pass ----------------
-  const int s0 = (int)((int64_t)chunk * a.nslots / a.n_chunks);
-  const int s1 = (int)((int64_t)(chunk + 1) * a.nslots / a.n_chunks);
-  const int ns = s1 - s0;  // <= SPC by construction of n_chunks
+  const int s0 = chunk * SPC;
+  const int ns = min(SPC, a.nslots - s0);
   const float* rowp = a.logits + (int64_t)row * a.ld;
-  const float4* rp4 = reinterpret_cast<const float4*>(rowp);
+  const v4f* rp4 = reinterpret_cast<const v4f*>(rowp);
   const uint32_t* mrow = HAS_MASK ? a.allowed + (int64_t)row * a.allowed_ld : nullptr;
+  const int fmax = (enc - 1) >> 2;  // last float4 holding an encodable id
 
-  float v[SPC * 4];
+  // Every load is unconditional (clamped to the row's last float4), so the
+  // compiler can wait for them one at a time, in order, while the arithmetic
+  // below runs on the ones that have arrived.
+  v4f q[SPC];
+  uint32_t mw[SPC];
 #pragma unroll
   for (int j = 0; j < SPC; j++) {
-    const int f = (s0 + j) * BLOCK + tid;  // float4 index in the row
-    float4 q = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
-    if (j < ns && 4 * f < enc) {
-      const v4f t = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(rp4 + f));
-      q = make_float4(t.x, t.y, t.z, t.w);
-      if (4 * f + 3 >= enc) {  // ids past the encodable bound take no part
-        if (4 * f + 1 >= enc) q.y = -INFINITY;
-        if (4 * f + 2 >= enc) q.z = -INFINITY;
-        q.w = -INFINITY;
-      }
-    }
-    v[4 * j + 0] = q.x;
-    v[4 * j + 1] = q.y;
-    v[4 * j + 2] = q.z;
-    v[4 * j + 3] = q.w;
+    const int f = min((s0 + j) * BLOCK + tid, fmax);
+    q[j] = __builtin_nontemporal_load(rp4 + f);
+    if (HAS_MASK) mw[j] = mrow[f >> 3];
   }
 
-  // held_row partial sum over the raw logits (no mask with WANT_LSE).
-  float m_raw = -INFINITY;
-  double rsum = 0.0;
-  if (WANT_LSE) {
+  // Online reduction, one float4 at a time, branch-free.  The softmax partial
+  // is summed in the reference's scaled domain, s = v * inv rounded to f32 as
+  // softmax_in_place does, as sum exp2(s*log2e - cL) with a per-lane offset
+  // cL = rn(c*log2e), c the lane's first scaled float4 max (0 if that is
+  // -inf); the constant error of cL is taken out exactly (an fma) when the
+  // lanes are combined.  A lane whose later values could overflow a term
+  // (more than 60 above c) is summed again after the loop against its max.
+  // A NaN, or a +inf value (inf - inf at the recount), makes the sum NaN: the
+  // stochastic NaN test.  The four terms of a float4 are added pairwise.
+  //
+  // The held_row partial (raw logits, f64 like the reference's denominator)
+  // keeps its per-lane offset at the lane's running max instead, so the
+  // largest term is exactly exp2(0) = 1 and the others, far smaller,
+  // accumulate in f64 without being absorbed: ln of a near-1 sum stays
+  // accurate to ~1e-15.
+  const float inv = cfg.inv;
+  float mr = -INFINITY;
+  float gm[SPC];
+  float sum = 0.0f, cL = 0.0f, c_s = 0.0f;
+  double racc = 0.0;
+  float rc = -__FLT_MAX__;
+  uint32_t nanl = 0;
 #pragma unroll
-    for (int i = 0; i < SPC * 4; i++) m_raw = fmaxf(m_raw, v[i]);
-    const float off = __builtin_isinf(m_raw) ? 0.0f : m_raw;
+  for (int j = 0; j < SPC; j++) {
+    float x[4] = {q[j].x, q[j].y, q[j].z, q[j].w};
+    if (HAS_MASK) {
+      const uint32_t bits = mw[j] >> ((((s0 + j) * BLOCK + tid) & 7) * 4);
 #pragma unroll
-    for (int i = 0; i < SPC * 4; i++) rsum += (double)expf(v[i] - off);
-  }
-
-  if (HAS_MASK) {
+      for (int e = 0; e < 4; e++)
+        if (!((bits >> e) & 1u)) x[e] = -INFINITY;
+    }
+    if (j >= ns || (s0 + j + 1) * SLOT > enc) {  // absent or partial slot (uniform)
+      const int id0 = (s0 + j) * SLOT + 4 * tid;
 #pragma unroll
-    for (int j = 0; j < SPC; j++) {
-      const int f = (s0 + j) * BLOCK + tid;
-      if (j < ns && 4 * f < enc) {
-        const uint32_t bits = mrow[f >> 3] >> ((f & 7) * 4);
-#pragma unroll
-        for (int e = 0; e < 4; e++)
-          if (!((bits >> e) & 1u)) v[4 * j + e] = -INFINITY;
+      for (int e = 0; e < 4; e++)
+        if (j >= ns || id0 + e >= enc) x[e] = -INFINITY;
+    }
+    q[j] = v4f{x[0], x[1], x[2], x[3]};
+    gm[j] = vmax(vmax3(x[0], x[1], x[2]), x[3]);
+    mr = vmax(mr, gm[j]);
+    if (stoch) {
+      if (j == 0) {
+        const float c = cfg.scale ? gm[0] * inv : gm[0];
+        c_s = (c > -INFINITY && c < INFINITY) ? c : 0.0f;
+        cL = c_s * LOG2E;
       }
-    }
-  }
-  float m = -INFINITY;
+      float t[4];
+      if (cfg.scale) {
 #pragma unroll
-  for (int i = 0; i < SPC * 4; i++) m = fmaxf(m, v[i]);
-  // flags: bit 0 a NaN (or, on stochastic rows, a +inf) was seen; bit 1 a
-  // finite value was seen (only needed with an allow-mask)
-  uint32_t flags = 0;
-  if (HAS_MASK) {
-    if (__builtin_isfinite(m)) {
-      flags |= 2u;
-    } else if (m == INFINITY) {
+        for (int e = 0; e < 4; e++) t[e] = xexp2(__builtin_fmaf(x[e] * inv, LOG2E, -cL));
+      } else {
 #pragma unroll
-      for (int i = 0; i < SPC * 4; i++) flags |= __builtin_isfinite(v[i]) ? 2u : 0u;
-    }
-  }
-  // Softmax partial sum in the reference's scaled domain: s = v * inv rounded to
-  // f32 exactly as softmax_in_place does, then exp(s - off_s) with off_s the
-  // lane's scaled max.  The exponent is one fma, s*log2(e) - rn(off_s*log2(e));
-  // the constant rounding error of rn(off_s*log2(e)) is exact (an fma) and is
-  // taken back out of the lane's sum once.  A NaN, or a +inf max (inf - inf),
-  // makes the sum NaN, which is the stochastic path's NaN test.
-  float ssum = 0.0f;
-  const float off = (m == -INFINITY) ? 0.0f : m;
-  const float off_s = cfg.scale ? off * cfg.inv : off;
-  if (stoch) {
-    const float offl = off_s * LOG2E;
-    const float err = __builtin_fmaf(off_s, LOG2E, -offl);  // off_s*log2e - offl, exact
-    if (cfg.scale) {
-#pragma unroll
-      for (int i = 0; i < SPC * 4; i++) ssum += __builtin_amdgcn_exp2f(__builtin_fmaf(v[i] * cfg.inv, LOG2E, -offl));
+        for (int e = 0; e < 4; e++) t[e] = xexp2(__builtin_fmaf(x[e], LOG2E, -cL));
+      }
+      sum += (t[0] + t[1]) + (t[2] + t[3]);
     } else {
 #pragma unroll
-      for (int i = 0; i < SPC * 4; i++) ssum += __builtin_amdgcn_exp2f(__builtin_fmaf(v[i], LOG2E, -offl));
+      for (int e = 0; e < 4; e++) nanl |= (x[e] != x[e]) ? 1u : 0u;
     }
-    ssum *= __builtin_amdgcn_exp2f(-err);
-    if (ssum != ssum) flags |= 1u;
-  } else {
+    if (WANT_LSE) {
+      if (gm[j] > rc) {
+        racc = (racc != 0.0) ? racc * (double)xexp2((rc - gm[j]) * LOG2E) : 0.0;
+        rc = gm[j];
+      }
 #pragma unroll
-    for (int i = 0; i < SPC * 4; i++) flags |= (v[i] != v[i]) ? 1u : 0u;
+      for (int e = 0; e < 4; e++) racc += (double)xexp2((x[e] - rc) * LOG2E);
+    }
   }
-  if (WANT_LSE && rsum != rsum) flags |= 1u;
-
-  // Wave reductions: max, flags, and the partial sums rescaled to the wave max.
-  const float m_w = wave_maxf(m);
-  const uint32_t f_w = wave_or(flags);
-  const float offw = (m_w == -INFINITY) ? 0.0f : m_w;
-  const float offw_s = cfg.scale ? offw * cfg.inv : offw;
-  double ssum_w = 0.0, rsum_w = 0.0;
-  if (stoch) ssum_w = wave_sumd(ssum != 0.0f ? (double)ssum * exp((double)off_s - (double)offw_s) : 0.0);
+  const float m_w = wave_maxf(mr);
+  double P = 0.0, R = 0.0;
+  float c_w = 0.0f;  // offset of the published softmax partial
+  uint32_t flags = 0;
+  if (stoch) {
+    // lanes whose max sits more than 60 above their offset: recount against
+    // the max (rare; makes +inf a NaN)
+    const float ms = cfg.scale ? mr * inv : mr;
+    const bool redo = ms > c_s + 60.0f;
+    if (__ballot(redo)) {
+      const float cn = redo ? ms : c_s;
+      const float cLn = cn * LOG2E;
+      float s2 = 0.0f;
+#pragma unroll
+      for (int j = 0; j < SPC; j++) {
+        float t[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const float xv = q4(q[j], e);
+          t[e] = xexp2(__builtin_fmaf(cfg.scale ? xv * inv : xv, LOG2E, -cLn));
+        }
+        s2 += (t[0] + t[1]) + (t[2] + t[3]);
+      }
+      if (redo) {
+        sum = s2;
+        c_s = cn;
+        cL = cLn;
+      }
+    }
+    // lanes to the wave's scaled max: factor e^(c_s - m_s) * 2^-(c_s*log2e - cL)
+    c_w = cfg.scale ? m_w * inv : m_w;
+    const float err = __builtin_fmaf(c_s, LOG2E, -cL);
+    const float d = __builtin_fmaf(c_s - c_w, LOG2E, -err);
+    const double part = (sum != 0.0f) ? (double)sum * (double)xexp2(d) : (double)sum;
+    P = wave_sumd(part);
+    if (P != P) flags |= 1u;
+  } else if (wave_or(nanl)) {
+    flags |= 1u;
+  }
   if (WANT_LSE) {
-    const float moff = __builtin_isinf(m_raw) ? 0.0f : m_raw;
-    rsum_w = wave_sumd(rsum != 0.0 ? rsum * exp((double)moff - (double)offw) : 0.0);
+    // lanes to the wave max (the max's own lane by exactly exp2(0) = 1)
+    R = wave_sumd((racc != 0.0) ? racc * (double)xexp2((rc - m_w) * LOG2E) : racc);
+    if (R != R) flags |= 1u;
+  }
+  const float c_r = m_w;
+  if (HAS_MASK) {
+    if (__builtin_isfinite(m_w)) {
+      flags |= 2u;
+    } else if (m_w == INFINITY) {
+      bool fin = false;
+#pragma unroll
+      for (int j = 0; j < SPC; j++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) fin |= __builtin_isfinite(q4(q[j], e));
+      if (__ballot(fin)) flags |= 2u;
+    }
   }
 
   // Candidate bound: the K'-th largest of a set of distinct chunk elements, so
   // at least K' elements of the chunk lie at or above it.  For K' <= 64 the set
   // is the 64 maxima of 4-lane groups (each group holds 4 x 64 logits); for
-  // K' > 64 it is all 256 lane maxima.  Wave 0 sorts the set; the chunk also
-  // publishes its 8 largest members for the row-level bound.
+  // K' > 64, or when fewer than K' groups hold a finite value, it is all 256
+  // lane maxima.  Every wave sorts the set for itself (no second barrier).
+  const uint32_t km = fkey(mr);
   {
-    const uint32_t km = fkey(m);
-    uint32_t g = max(km, (uint32_t)__shfl_xor((int)km, 1));
-    g = max(g, (uint32_t)__shfl_xor((int)g, 2));
+    uint32_t g = max(km, xor_u32(km, 1));
+    g = max(g, xor_u32(g, 2));
     if ((lane & 3) == 0) L.c.groupmax[wave * 16 + (lane >> 2)] = g;
-    L.c.lanemax[wave * 64 + lane] = km;
+    L.c.lanemax[tid] = km;
+    if (tid == 0) L.c.arrive = 0;
   }
   __syncthreads();
-  uint32_t top = 0;
-  if (wave == 0) {
-    uint32_t tk = 0;
+  uint32_t tk = 0;
+  // Keys this sub-record publishes for the row's survivor bound: the wave max
+  // (K' <= 64), or the chunk's lane maxima of rank wave + 4r (K' > 64).
+  uint32_t pub[4] = {fkey(m_w), 0u, 0u, 0u};
+  if (!cfg.bad) {
     if (kp <= 64) {
       uint32_t x[1] = {L.c.groupmax[lane]};
       wave_sort_desc<1, true>(x);
-      top = x[0];
       tk = rdl(x[0], kp - 1);
     }
-    if (kp > 64 || tk <= fkey(-INFINITY)) {
+    if (kp > 64 || tk <= KEY_NEG_INF) {
       uint32_t all[4];
 #pragma unroll
       for (int r = 0; r < 4; r++) all[r] = L.c.lanemax[r * 64 + lane];
       wave_sort_desc<4, true>(all);
-      top = all[0];
-      const int i = kp - 1;  // < 256
+      const int i = kp - 1;
 #pragma unroll
       for (int r = 0; r < 4; r++)
         if ((i >> 6) == r) tk = rdl(all[r], i & 63);
+      if (kp > 64) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) pub[r] = rdl(all[0], wave + 4 * r);
+      }
     }
-    if (lane == 0) L.c.misc[NWAVE + 1] = (int32_t)tk;
   }
-  __syncthreads();
-  const uint32_t tau_key = (uint32_t)L.c.misc[NWAVE + 1];
-  const float tau = keyf(tau_key);
 
-  // Filter: this wave's elements at or above the bound, compacted with ballots
-  // into the wave's LDS list.  One compare per element; the ballot branch is
-  // taken for the ~K' hits of the whole block.
-  uint64_t* hw = L.c.hits + wave * CAPH;
+  // Filter: this wave's elements at or above the bound (never -inf, never
+  // NaN), compacted with ballots straight into the wave's sub-record.
+  const int nsp = ((nc * NWAVE + 63) >> 6) << 6;
+  uint64_t* const rowrec = a.rec + (int64_t)row * SRECW * nsp;
+  uint64_t* sub = rowrec + chunk * NWAVE + wave;
   const int base_id = s0 * SLOT + 4 * tid;
-  int count = 0;
+  int cnt = 0;
+  if (!cfg.bad) {
+    const float tf = (tk <= KEY_NEG_INF) ? -__FLT_MAX__ : keyf(tk);
 #pragma unroll
-  for (int j = 0; j < SPC; j++) {
-    const float gm = fmaxf(fmaxf(v[4 * j], v[4 * j + 1]), fmaxf(v[4 * j + 2], v[4 * j + 3]));
-    if (__ballot(gm >= tau && j < ns)) {
+    for (int j = 0; j < SPC; j++) {
+      if (__ballot(gm[j] >= tf)) {
 #pragma unroll
-      for (int e = 0; e < 4; e++) {
-        const float x = v[4 * j + e];
-        const int id = base_id + j * SLOT + e;
-        const bool hit = x >= tau && j < ns && id < enc;
-        const uint64_t b = __ballot(hit);
-        if (b) {
-          const int pos = count + lanes_below(b);
-          if (hit && pos < CAPH) hw[pos] = pack(fkey(x), (uint32_t)id);
-          count += __popcll(b);
+        for (int e = 0; e < 4; e++) {
+          const float x = q4(q[j], e);
+          const bool hit = x >= tf;
+          const uint64_t b = __ballot(hit);
+          if (b) {
+            const int pos = cnt + lanes_below(b);
+            if (hit && pos < CAPW) st_agent(sub + (int64_t)(SHDR + pos) * nsp, pack(fkey(x), (uint32_t)(base_id + j * SLOT + e)));
+            cnt += __popcll(b);
+          }
         }
       }
     }
-  }
-  if (lane == 0) {
-    L.c.nhit[wave] = count;
-    L.c.wm[wave] = m_w;
-    L.c.wf[wave] = f_w;
-    L.c.ws[wave] = ssum_w;
-    L.c.wr[wave] = rsum_w;
-  }
-  __syncthreads();
-  int cnt[NWAVE], total = 0;
-  bool ovf = false;
-#pragma unroll
-  for (int w = 0; w < NWAVE; w++) {
-    cnt[w] = L.c.nhit[w];
-    total += cnt[w];
-    ovf |= cnt[w] > CAPH;
-  }
-  if (ovf) {
-    __syncthreads();
-    total = chunk_overflow<HAS_MASK>(rowp, mrow, s0, ns, enc, tau_key, kp, L.c.hits, L.c.misc,
-                                     &L.c.misc[NWAVE]);
-    cnt[0] = total;
-    cnt[1] = cnt[2] = cnt[3] = 0;
-  }
-  if (wave != 0) return;
-
-  // Chunk statistics: the four waves' partials rescaled to the chunk max.
-  float m_c = L.c.wm[0];
-  uint32_t f_c = L.c.wf[0];
-#pragma unroll
-  for (int w = 1; w < NWAVE; w++) {
-    m_c = fmaxf(m_c, L.c.wm[w]);
-    f_c |= L.c.wf[w];
-  }
-  double ssum_c = 0.0, rsum_c = 0.0;
-  {
-    const float oc = (m_c == -INFINITY) ? 0.0f : m_c;
-    const float oc_s = cfg.scale ? oc * cfg.inv : oc;
-#pragma unroll
-    for (int w = 0; w < NWAVE; w++) {
-      const float ow = (L.c.wm[w] == -INFINITY) ? 0.0f : L.c.wm[w];
-      const float ow_s = cfg.scale ? ow * cfg.inv : ow;
-      if (L.c.ws[w] != 0.0) ssum_c += L.c.ws[w] * exp((double)ow_s - (double)oc_s);
-      if (WANT_LSE && L.c.wr[w] != 0.0) rsum_c += L.c.wr[w] * exp((double)ow - (double)oc);
-    }
+    if (cnt > CAPW) cnt = wave_overflow(q, sub, nsp, kp, tk, base_id);
   }
 
-  // Wave 0 publishes the chunk record, then takes the row's arrival ticket.
-  uint64_t* rec = a.rec + ((int64_t)row * a.n_chunks + chunk) * RECW;
-  for (int i = lane; i < total; i += 64) {
-    int w = 0, j = i;
-    if (!ovf) {
-      while (j >= cnt[w]) { j -= cnt[w]; w++; }
-    }
-    st_agent(rec + HDR + i, L.c.hits[(ovf ? 0 : w * CAPH) + j]);
-  }
-  {
-    const uint32_t t0 = (uint32_t)__shfl((int)top, (2 * lane) & 63);
-    const uint32_t t1 = (uint32_t)__shfl((int)top, (2 * lane + 1) & 63);
-    if (lane < NLM / 2) st_agent(rec + 4 + lane, ((uint64_t)t1 << 32) | t0);
-  }
+  // Publish the sub-record header, wait for every store to land, then take
+  // the row's arrival ticket.
   if (lane == 0) {
-    st_agent(rec + 0, ((uint64_t)__float_as_uint((float)ssum_c) << 32) | __float_as_uint(m_c));
-    st_agent(rec + 1, (uint64_t)__double_as_longlong(rsum_c));
-    st_agent(rec + 2, ((uint64_t)(uint32_t)total << 32) | f_c);
-    st_agent(rec + 3, (uint64_t)a.epoch);
+    st_agent(sub + 0 * nsp, (uint64_t)__double_as_longlong(P));
+    st_agent(sub + 1 * nsp, ((uint64_t)__float_as_uint(c_r) << 32) | __float_as_uint(c_w));
+    st_agent(sub + 2 * nsp, (uint64_t)__double_as_longlong(R));
+    st_agent(sub + 3 * nsp, ((uint64_t)flags << 32) | __float_as_uint(m_w));
+    st_agent(sub + 4 * nsp, ((uint64_t)a.epoch << 32) | (uint32_t)cnt);
+    st_agent(sub + 5 * nsp, ((uint64_t)pub[1] << 32) | pub[0]);
+    st_agent(sub + 6 * nsp, ((uint64_t)pub[3] << 32) | pub[2]);
   }
+  // The workgroup's last wave to get here (an LDS counter) takes the row's
+  // ticket for all four: one global atomic per workgroup, not per wave.
   drain();
+  const int nsub = nc * NWAVE;
+  int tb = 0;
+  if (lane == 0) tb = atomicAdd(&L.c.arrive, 1);
+  tb = (int)rdl((uint32_t)tb, 0);
+  if (tb != NWAVE - 1) return;
   int t = 0;
   if (lane == 0) t = __hip_atomic_fetch_add(&a.row_ticket[row], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   t = (int)rdl((uint32_t)t, 0);
-  const int nc = a.n_chunks;
   if (t != nc - 1) return;
   if (lane == 0) st_agent(&a.row_ticket[row], 0);
 
-  // ---------------- row finalize: wave 0 of the last block ----------------
-  // All of the row's records, STG words at most, in one round of loads.
+  // ---------------- row finalize: the row's last wave ----------------
+  // Every wave of this workgroup has published (the LDS counter), so the
+  // workgroup's LDS is free.  Lane l handles sub-records l + 64g.
   FinLds& F = L.f;
-  const uint64_t* rr = a.rec + (int64_t)row * nc * RECW;
-  // staging stride: odd in u64 words, so lanes reading one word of each record
-  // fall in different LDS banks
-  const int sst = ((STG / nc) & 1) ? STG / nc : STG / nc - 1;
-  const int w1 = min(RECW, sst);  // words of each record staged (>= HDR + 7)
+  const uint64_t* rr = rowrec;
+  const int G = (nsub + 63) >> 6;
   const float u_row = a.uniforms[row];  // prefetched for the draw
-  {
-    constexpr int NB = STG / 64;
-    uint64_t sv[NB];
+  const double et = (&kExpT[0][0])[lane];  // the exp table, staged into LDS below
+  // Group 0's headers (and first EPRE entries) live in registers; the
+  // headers of further groups (vocabularies above 64 sub-records) are re-read
+  // from the workspace where they are used.
+  uint64_t h0[NHW];
+  uint64_t E[EPRE];
 #pragma unroll
-    for (int u = 0; u < NB; u++) {
-      const int i = u * 64 + lane;
-      sv[u] = 0ull;
-      if (i < nc * w1) {
-        const int c = i / w1, k = i - c * w1;
-        sv[u] = ld_agent(rr + (int64_t)c * RECW + k);
-      }
-    }
+  for (int i = 0; i < NHW; i++) h0[i] = 0ull;
 #pragma unroll
-    for (int u = 0; u < NB; u++)
-      if (u * 64 + lane < nc * w1) {
-        const int i = u * 64 + lane, c = i / w1;
-        F.stage[c * sst + (i - c * w1)] = sv[u];
-      }
-  }
-  wave_lds_sync();
-  // Lane c holds chunk c's header (nc <= 64 is enforced by the host).
-  float cv = -INFINITY, cs = 0.0f;
-  double cr = 0.0;
-  uint32_t cf = 0;
-  int cc = 0;
-  bool stale = false;
-  if (lane < nc) {
-    uint64_t h3 = F.stage[lane * sst + 3];
-    if ((uint32_t)h3 != a.epoch) {
-      // not visible yet: re-read the record (bounded), then restage its words
-      for (int spin = 0; spin < 1000 && (uint32_t)h3 != a.epoch; spin++) h3 = ld_agent(rr + (int64_t)lane * RECW + 3);
-      stale = (uint32_t)h3 != a.epoch;
-      for (int k = 0; k < w1; k++) F.stage[lane * sst + k] = ld_agent(rr + (int64_t)lane * RECW + k);
+  for (int j = 0; j < EPRE; j++) E[j] = 0ull;
+  auto load0 = [&]() __attribute__((always_inline)) {
+    if (lane < nsub) {
+#pragma unroll
+      for (int i = 0; i < NHW; i++) h0[i] = ld_agent(rr + i * nsp + lane);
+#pragma unroll
+      for (int j = 0; j < EPRE; j++) E[j] = ld_agent(rr + (SHDR + j) * nsp + lane);
     }
-    const uint64_t h0 = F.stage[lane * sst + 0];
-    const uint64_t h1 = F.stage[lane * sst + 1];
-    const uint64_t h2 = F.stage[lane * sst + 2];
-    cv = __uint_as_float((uint32_t)h0);
-    cs = __uint_as_float((uint32_t)(h0 >> 32));
-    cr = __longlong_as_double((long long)h1);
-    cf = (uint32_t)h2;
-    cc = (int)(h2 >> 32);
+  };
+  auto hdr = [&](int g, int i) __attribute__((always_inline)) -> uint64_t {
+    const int s = g * 64 + lane;
+    if (g == 0) return h0[i];
+    return (g < G && s < nsub) ? ld_agent(rr + i * nsp + s) : 0ull;
+  };
+  auto has = [&](int g) __attribute__((always_inline)) { return g < G && g * 64 + lane < nsub; };
+  load0();  // one round of loads
+  // Every record carries the launch's epoch: one that is not visible yet is
+  // re-read (bounded), then reported rather than used.
+  auto stale_now = [&]() __attribute__((always_inline)) {
+    bool st0 = false;
+#pragma unroll
+    for (int g = 0; g < GMAX; g++)
+      if (has(g) && (uint32_t)(hdr(g, 4) >> 32) != a.epoch) st0 = true;
+    return st0;
+  };
+  bool stale = stale_now();
+  for (int spin = 0; spin < 1000 && __ballot(stale); spin++) {
+    load0();
+    stale = stale_now();
   }
-  wave_lds_sync();
   const bool any_stale = __ballot(stale) != 0;
-  const float m_v = wave_maxf(cv);
-  const uint32_t fl = wave_or(cf);
-  const float moff = (m_v == -INFINITY) ? 0.0f : m_v;
-  const float moff_s = cfg.scale ? moff * cfg.inv : moff;
+
+  float mv = -INFINITY;
+  uint32_t fw = 0;
+  int maxc = 0;
+#pragma unroll
+  for (int g = 0; g < GMAX; g++) {
+    if (has(g)) {
+      const uint64_t h3 = hdr(g, 3), h4 = hdr(g, 4);
+      mv = fmaxf(mv, __uint_as_float((uint32_t)h3));
+      fw |= (uint32_t)(h3 >> 32);
+      maxc = max(maxc, (int)(uint32_t)h4);
+    }
+  }
+  const float m_v = wave_maxf(mv);
+  const uint32_t fl = wave_or(fw);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) maxc = max(maxc, xor_lane(maxc, o));
+  const float m_s = cfg.scale ? m_v * cfg.inv : m_v;
   double S_d = 0.0, R_d = 0.0;
-  {
-    const float co = (cv == -INFINITY) ? 0.0f : cv;
-    const float co_s = cfg.scale ? co * cfg.inv : co;
-    if (cs != 0.0f) S_d = (double)cs * exp((double)co_s - (double)moff_s);
-    if (WANT_LSE && cr != 0.0) R_d = cr * exp((double)co - (double)moff);
+#pragma unroll
+  for (int g = 0; g < GMAX; g++) {
+    if (has(g)) {
+      const uint64_t h1 = hdr(g, 1);
+      const double p = __longlong_as_double((long long)hdr(g, 0));
+      if (p != 0.0) S_d += p * (double)xexp2((__uint_as_float((uint32_t)h1) - m_s) * LOG2E);
+      if (WANT_LSE) {
+        const double r = __longlong_as_double((long long)hdr(g, 2));
+        if (r != 0.0) R_d += r * (double)xexp2((__uint_as_float((uint32_t)(h1 >> 32)) - m_v) * LOG2E);
+      }
+    }
   }
   S_d = wave_sumd(S_d);
   if (WANT_LSE) R_d = wave_sumd(R_d);
   const float S = (float)S_d;
-  const float m_s = cfg.scale ? m_v * cfg.inv : m_v;
   const bool nan_seen = fl & 1u;
   const bool finite_seen = fl & 2u;
 
@@ -909,33 +936,43 @@ __global__ __launch_bounds__(BLOCK) void sample_kernel(Args a) {
   else if (cfg.greedy) st = nan_seen ? XS_ROW_NAN : (m_v == -INFINITY ? XS_ROW_NO_FINITE : XS_ROW_OK);
   else if (nan_seen || __builtin_isinf(m_s)) st = XS_ROW_NAN;
 
-  // Survivor bound: the K'-th largest of the chunks' published lane maxima
-  // (distinct elements; NLM per chunk, up to 256 values).
+  // Survivor bound: the K'-th largest of the published keys (distinct
+  // elements: wave maxima, or the chunks' top lane maxima when K' > 64).
   uint32_t tau_row = 0;
   {
-    int q = NLM;  // members of each chunk's list used (sorted, largest first)
-    while (q > 1 && nc * q > 64 && nc * (q - 1) >= kp) q--;
-    const int nv = min(nc * q, 256);
-    if (nv >= kp) {
-      uint32_t x[4];
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const int i = r * 64 + lane;
-        const int c = i / q, k = i - c * q;
-        x[r] = 0u;
-        if (i < nv) {
-          const uint64_t wv = F.stage[c * sst + 4 + (k >> 1)];
-          x[r] = (k & 1) ? (uint32_t)(wv >> 32) : (uint32_t)wv;
+    int qk = 1;  // keys used per sub-record
+    if (kp > 64) qk = (G == 1) ? 4 : (nsub >= kp ? 1 : 2);
+    const int nv = qk * nsub;
+    if (nv >= kp && !cfg.bad) {
+      uint32_t x[4] = {0u, 0u, 0u, 0u};
+      if (G == 1) {
+        if (lane < nsub) {
+          x[0] = (uint32_t)h0[5];
+          if (qk == 4) {
+            x[1] = (uint32_t)(h0[5] >> 32);
+            x[2] = (uint32_t)h0[6];
+            x[3] = (uint32_t)(h0[6] >> 32);
+          }
         }
+      } else {
+#pragma unroll
+        for (int g = 0; g < GMAX; g++) {
+          const int s = g * 64 + lane;
+          if (has(g)) {
+            const uint64_t h5 = hdr(g, 5);
+            F.keys[s * qk] = (uint32_t)h5;
+            if (qk == 2) F.keys[s * qk + 1] = (uint32_t)(h5 >> 32);
+          }
+        }
+        wave_lds_sync();
+#pragma unroll
+        for (int r = 0; r < 4; r++) x[r] = (r * 64 + lane < nv) ? F.keys[r * 64 + lane] : 0u;
+        wave_lds_sync();
       }
-      if (nv <= 64) {
+      if (G == 1 && qk == 1) {
         uint32_t y[1] = {x[0]};
         wave_sort_desc<1>(y);
         tau_row = rdl(y[0], kp - 1);
-      } else if (nv <= 128) {
-        uint32_t y[2] = {x[0], x[1]};
-        wave_sort_desc<2>(y);
-        tau_row = (kp - 1) < 64 ? rdl(y[0], kp - 1) : rdl(y[1], kp - 65);
       } else {
         wave_sort_desc<4>(x);
         const int i = kp - 1;
@@ -945,74 +982,66 @@ __global__ __launch_bounds__(BLOCK) void sample_kernel(Args a) {
       }
     }
   }
-  // Gather the survivors (entries at or above the bound) into LDS: lane c
-  // reads chunk c's staged entries eight at a time, then (rarely) the entries
-  // past the staged words from the workspace; a wave prefix sum places them.
-  int maxc = cc;
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) maxc = max(maxc, xor_lane(maxc, o));
-  const int nstg = w1 - HDR;  // entries of each record in the staging area
-  const int cst = min(cc, nstg);
+
+  // Gather the survivors (entries at or above the bound) into LDS.
   uint64_t floor_e = (uint64_t)tau_row << 32;
   int M = 0;
-  auto gather = [&](uint64_t floor_v) __attribute__((always_inline)) -> int {
-    int m = 0;
-    const int mst = min(maxc, nstg);
-    for (int j0 = 0; j0 < mst; j0 += 8) {
-      uint64_t e[8];
-#pragma unroll
-      for (int u = 0; u < 8; u++) e[u] = F.stage[lane * sst + HDR + min(j0 + u, nstg - 1)];
-      int h = 0;
-#pragma unroll
-      for (int u = 0; u < 8; u++) h += (j0 + u < cst && e[u] >= floor_v) ? 1 : 0;
-      const int incl = wave_incl_scan(h);
-      int pos = m + incl - h;
-#pragma unroll
-      for (int u = 0; u < 8; u++)
-        if (j0 + u < cst && e[u] >= floor_v) {
-          if (pos < SURV) F.list[pos] = e[u];
-          pos++;
-        }
-      m += (int)rdl((uint32_t)incl, 63);
+  auto put = [&](uint64_t e, bool ok) __attribute__((always_inline)) {
+    const uint64_t b = __ballot(ok);
+    if (b) {
+      const int pos = M + lanes_below(b);
+      if (ok && pos < SURV) F.list[pos] = e;
+      M += __popcll(b);
     }
-    for (int j0 = nstg; j0 < maxc; j0 += 8) {  // entries past the staging area
-      uint64_t e[8];
-#pragma unroll
-      for (int u = 0; u < 8; u++) {
-        const int j = min(j0 + u, CAPB - 1);
-        e[u] = (j0 + u < cc) ? ld_agent(rr + (int64_t)lane * RECW + HDR + j) : 0ull;
-      }
-      int h = 0;
-#pragma unroll
-      for (int u = 0; u < 8; u++) h += (j0 + u < cc && e[u] >= floor_v) ? 1 : 0;
-      const int incl = wave_incl_scan(h);
-      int pos = m + incl - h;
-#pragma unroll
-      for (int u = 0; u < 8; u++)
-        if (j0 + u < cc && e[u] >= floor_v) {
-          if (pos < SURV) F.list[pos] = e[u];
-          pos++;
-        }
-      m += (int)rdl((uint32_t)incl, 63);
-    }
-    return m;
   };
-  M = gather(floor_e);
+  auto gather_global = [&](int s, int c, int j0, uint64_t fl_e) __attribute__((always_inline)) {
+    // entries j0..c-1 of sub-record s, read from the workspace
+    for (int j = j0; j < maxc; j += 8) {
+      uint64_t e[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) e[u] = (j + u < c) ? ld_agent(rr + (int64_t)(SHDR + j + u) * nsp + s) : 0ull;
+#pragma unroll
+      for (int u = 0; u < 8; u++) put(e[u], j + u < c && e[u] >= fl_e);
+    }
+  };
+  auto gather = [&](uint64_t fl_e) __attribute__((always_inline)) {
+    M = 0;
+    if (G == 1) {
+      const int c = lane < nsub ? (int)(uint32_t)h0[4] : 0;
+#pragma unroll
+      for (int j = 0; j < EPRE; j++) put(E[j], j < c && E[j] >= fl_e);
+      if (maxc > EPRE) gather_global(lane, c, EPRE, fl_e);
+    } else {
+#pragma unroll
+      for (int g = 0; g < GMAX; g++) {
+        const int s = g * 64 + lane;
+        if (g < G) gather_global(s, has(g) ? (int)(uint32_t)hdr(g, 4) : 0, 0, fl_e);
+      }
+    }
+  };
+  if (!cfg.bad) gather(floor_e);
   if (M > SURV) {
     // More survivors than one wave sorts (ties at the bound across many
-    // chunks): move the floor to the exact K'-th largest entry by bisection
-    // over the entries, then gather again.
+    // waves): move the floor to the exact K'-th largest entry by bisection
+    // over every entry, then gather again.
     uint64_t ans = 0;
     for (int bit = 63; bit >= 0; bit--) {
       const uint64_t cnd = ans | (1ull << bit);
       int c = 0;
-      for (int j = 0; j < cst; j++) c += F.stage[lane * sst + HDR + j] >= cnd ? 1 : 0;
-      for (int j = cst; j < cc; j++) c += ld_agent(rr + (int64_t)lane * RECW + HDR + j) >= cnd ? 1 : 0;
+#pragma unroll
+      for (int g = 0; g < GMAX; g++) {
+        const int s = g * 64 + lane;
+        const int n = has(g) ? (int)(uint32_t)hdr(g, 4) : 0;
+        for (int j = 0; j < n; j++) c += ld_agent(rr + (int64_t)(SHDR + j) * nsp + s) >= cnd ? 1 : 0;
+      }
       if (wave_sumi(c) >= kp) ans = cnd;
     }
     floor_e = ans;
-    M = gather(floor_e);
+    gather(floor_e);
   }
+  F.expt[lane] = et;
+  wave_lds_sync();
+
   // Sort the survivors (logit desc, id asc); the first K' are the selection.
   uint64_t sel[4];
 #pragma unroll
@@ -1029,7 +1058,7 @@ __global__ __launch_bounds__(BLOCK) void sample_kernel(Args a) {
   } else {
     wave_sort_desc64<4>(sel);
   }
-  const int nsel = min(M, kp);  // == kp: the union holds the row's K' best
+  const int nsel = min(M, kp);  // == kp unless the row holds fewer finite values
 
   // Probabilities of the selection and the (p desc, id asc) order; p is
   // non-increasing along the logit order, so only runs of equal p move.
@@ -1037,14 +1066,39 @@ __global__ __launch_bounds__(BLOCK) void sample_kernel(Args a) {
   const bool want_cands = a.cand_id != nullptr || a.cand_w != nullptr;
   float pw[2] = {0.0f, 0.0f};    // p of selection entry r*64+lane (K' <= 128)
   uint64_t pk[2] = {0ull, 0ull};  // (p bits << 32) | ~id
+  const double* T = F.expt;
+  // the value the boundary proof needs, p(next_below(vL)), is computed in the
+  // same pass, by the lane just past the selection
+  const float vL = nsel > 0 ? keyf(pk_key(pick64(sel, nsel - 1))) : -INFINITY;
+  float pbelow = 0.0f;
   if (stoch && st == XS_ROW_OK) {
+    const bool need_below = !cfg.full && vL != -INFINITY;
 #pragma unroll
     for (int r = 0; r < 2; r++) {
-      const int i = r * 64 + lane;
-      if (i < nsel) {
-        pw[r] = exact_p(keyf(pk_key(sel[r])), cfg, m_s, S);
-        pk[r] = ((uint64_t)__float_as_uint(pw[r] + 0.0f) << 32) | (uint64_t)(0xFFFFFFFFu - pk_id(sel[r]));
+      if (r * 64 <= nsel) {
+        const int i = r * 64 + lane;
+        const bool in = i < nsel;
+        if (in || (i == nsel && need_below)) {
+          const float pe = exact_p(in ? keyf(pk_key(sel[r])) : next_below(vL), cfg, m_s, S, T);
+          if (in) {
+            pw[r] = pe;
+            pk[r] = ((uint64_t)__float_as_uint(pe + 0.0f) << 32) | (uint64_t)(0xFFFFFFFFu - pk_id(sel[r]));
+          } else {
+            pw[r] = pe;  // lane nsel: the boundary value, read below and then cleared
+          }
+        }
       }
+    }
+    if (need_below) {
+      if (nsel < 128) {
+        pbelow = rdlf(nsel < 64 ? pw[0] : pw[1], nsel & 63);
+      } else {
+        pbelow = exact_p(next_below(vL), cfg, m_s, S, T);
+      }
+    }
+    if (lane == (nsel & 63)) {
+      if (nsel < 64) pw[0] = 0.0f;
+      else if (nsel < 128) pw[1] = 0.0f;
     }
     bool bad = false;
     const uint64_t n0 = shfl64(pk[0], (lane + 1) & 63);
@@ -1069,8 +1123,6 @@ __global__ __launch_bounds__(BLOCK) void sample_kernel(Args a) {
     // P_k), whose lowest ids the (logit desc, id asc) selection already kept.
     if (!cfg.full) {
       const float Pk = __uint_as_float((uint32_t)(pick64(pk, k - 1) >> 32));
-      const uint64_t last = pick64(sel, nsel - 1);
-      const float vL = keyf(pk_key(last));
       const float pL = rdlf(nsel - 1 < 64 ? pw[0] : pw[1], (nsel - 1) & 63);
       bool slow = nsel < kp;
       if (!slow && pL == Pk) {
@@ -1078,7 +1130,7 @@ __global__ __launch_bounds__(BLOCK) void sample_kernel(Args a) {
 #pragma unroll
         for (int r = 0; r < 2; r++)
           if (r * 64 + lane < nsel && pw[r] == Pk && keyf(pk_key(sel[r])) != vL) other = true;
-        const bool below = vL != -INFINITY && exact_p(next_below(vL), cfg, m_s, S) == Pk;
+        const bool below = vL != -INFINITY && pbelow == Pk;
         slow = __ballot(other) != 0 || below;
       }
       // Entries tied at P_k = 0 carry no weight: the draw does not depend on
@@ -1103,7 +1155,7 @@ __global__ __launch_bounds__(BLOCK) void sample_kernel(Args a) {
         for (int base = 0; base < enc && need > 0; base += 256) {
           const int f = base / 4 + lane;
           float4 qv = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
-          if (4 * f < enc) qv = rp4[f];
+          if (4 * f < enc) qv = reinterpret_cast<const float4*>(rowp)[f];
           const float xv[4] = {qv.x, qv.y, qv.z, qv.w};
           bool hit[4];
           int c = 0;
@@ -1116,7 +1168,7 @@ __global__ __launch_bounds__(BLOCK) void sample_kernel(Args a) {
             if (id < enc) {
               const float sx = cfg.scale ? x * cfg.inv : x;
               const float d = sx - m_s;
-              if (d >= x_lo && d <= x_hi) hit[e] = exact_p(x, cfg, m_s, S) == Pk;
+              if (d >= x_lo && d <= x_hi) hit[e] = exact_p(x, cfg, m_s, S, T) == Pk;
             }
             c += hit[e];
           }
@@ -1140,9 +1192,11 @@ __global__ __launch_bounds__(BLOCK) void sample_kernel(Args a) {
   }
 
   // The draw: truncate_top_p (sampler.rs:401-429) and WeightedIndex
-  // (sampler.rs:235-243, rand 0.9) in serial f32.  Weight i lives in lane
-  // i % 64 of w[i / 64]; the serial chains read it with v_readlane, eight per
-  // batch, and every lane carries the same uniform running values.
+  // (sampler.rs:235-243, rand 0.9), serial f32.  Weight i lives in lane i % 64
+  // of w[i / 64].  Every lane runs the serial chain over weights 0..i of its
+  // own index (adding 0.0 for the later ones, which changes nothing), so lane
+  // i ends with the serial prefix sum through i: the top-p cumsum, the
+  // WeightedIndex cumulative weights and its total all come from one chain.
   float w[2];
   w[0] = __uint_as_float((uint32_t)(pk[0] >> 32));
   w[1] = __uint_as_float((uint32_t)(pk[1] >> 32));
@@ -1153,73 +1207,75 @@ __global__ __launch_bounds__(BLOCK) void sample_kernel(Args a) {
     } else {
       if (lane >= k) w[0] = 0.0f;
       if (64 + lane >= k) w[1] = 0.0f;
-#define XS_W(i) __uint_as_float(rdl(__float_as_uint(((i) < 64) ? w[0] : w[1]), (i) & 63))
-      // serial f32 sum of w[0..k), the order Iterator::sum folds in
-      auto serial_sum = [&]() __attribute__((always_inline)) -> float {
-        float acc = -0.0f;
-        for (int b0 = 0; b0 < k; b0 += 8) {
-          float q[8];
+      // prefix[r] = init + w_0 + ... + w_(r*64+lane), left to right in f32
+      auto prefix = [&](float init, float (&pre)[2]) __attribute__((always_inline)) {
+        float acc = init;
+        const int k0 = min(k, 64);
+        for (int b0 = 0; b0 < k0; b0 += 8) {
+          float qv[8];
 #pragma unroll
-          for (int u = 0; u < 8; u++) q[u] = XS_W(b0 + u);
+          for (int u = 0; u < 8; u++) qv[u] = rdlf(w[0], (b0 + u) & 63);
 #pragma unroll
-          for (int u = 0; u < 8; u++) acc = (b0 + u < k) ? acc + q[u] : acc;
+          for (int u = 0; u < 8; u++) acc = acc + ((lane >= b0 + u) ? qv[u] : 0.0f);
         }
-        return acc;
+        pre[0] = acc;
+        pre[1] = acc;
+        if (k > 64) {
+          float acc1 = rdlf(acc, 63);
+          for (int b0 = 0; b0 < k - 64; b0 += 8) {
+            float qv[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) qv[u] = rdlf(w[1], (b0 + u) & 63);
+#pragma unroll
+            for (int u = 0; u < 8; u++) acc1 = acc1 + ((lane >= b0 + u) ? qv[u] : 0.0f);
+          }
+          pre[1] = acc1;
+        }
       };
+      auto at = [&](const float (&pre)[2], int i) __attribute__((always_inline)) -> float {
+        return rdlf(i < 64 ? pre[0] : pre[1], i & 63);
+      };
+      bool zero = false;
       if (!(cfg.top_p >= 1.0f)) {
-        const float sum = serial_sum();
-        if (sum > 0.0f) {
+        float pre[2];
+        prefix(-0.0f, pre);  // the serial sum folds from -0.0 as Rust's f32 Sum does
+        const float sum = at(pre, k - 1);
+        if (!(sum > 0.0f)) {
+          zero = true;  // all weights zero: truncate_top_p returns them unchanged
+        } else {
           w[0] = __fdiv_rn(w[0], sum);
           w[1] = __fdiv_rn(w[1], sum);
-          // serial cumsum; keep = 1 + the first index where it reaches top_p
-          float csum = 0.0f;
-          int keep = k;
-          for (int b0 = 0; b0 < k && keep == k; b0 += 8) {
-            float q[8];
-#pragma unroll
-            for (int u = 0; u < 8; u++) q[u] = XS_W(b0 + u);
-#pragma unroll
-            for (int u = 0; u < 8; u++) {
-              const bool live = (b0 + u < k) && (keep == k);
-              const float nxt = csum + q[u];
-              csum = live ? nxt : csum;
-              keep = (live && nxt >= cfg.top_p) ? b0 + u + 1 : keep;
-            }
-          }
+        }
+      }
+      if (zero) {
+        st = XS_ROW_ZERO_WEIGHT;
+      } else {
+        float c[2];
+        prefix(0.0f, c);
+        int keep = k;
+        if (!(cfg.top_p >= 1.0f)) {
+          const uint64_t b0m = __ballot(lane < k && c[0] >= cfg.top_p);
+          const uint64_t b1m = __ballot(64 + lane < k && c[1] >= cfg.top_p);
+          keep = b0m ? (int)__builtin_ctzll(b0m) + 1 : (b1m ? 64 + (int)__builtin_ctzll(b1m) + 1 : k);
           if (lane >= keep) w[0] = 0.0f;
           if (64 + lane >= keep) w[1] = 0.0f;
         }
-      }
-      // WeightedIndex: total = the serial sum; cumulative weights cum[i-1] =
-      // w0 + ... + w[i-1]; x = u * total; the index is the number of
-      // cumulative weights <= x.
-      const float tot = serial_sum();
-      bool okw = !(lane < k && !(w[0] >= 0.0f)) && !(64 + lane < k && !(w[1] >= 0.0f));
-      okw = __ballot(!okw) == 0;
-      if (!okw || tot == 0.0f) {
-        st = XS_ROW_ZERO_WEIGHT;
-      } else {
-        const float x_draw = u_row * tot + 0.0f;
-        float run = XS_W(0);
-        int idx = 0;
-        bool stop = false;
-        for (int b0 = 1; b0 < k && !stop; b0 += 8) {
-          float q[8];
-#pragma unroll
-          for (int u = 0; u < 8; u++) q[u] = XS_W(b0 + u);
-#pragma unroll
-          for (int u = 0; u < 8; u++) {
-            const int i = b0 + u;
-            const bool live = (i < k) && !stop;
-            const bool take = live && (run <= x_draw);
-            idx = take ? i : idx;
-            run = take ? run + q[u] : run;
-            stop = stop || (live && !take);
-          }
+        const float tot = at(c, keep - 1);
+        bool okw = !(lane < k && !(w[0] >= 0.0f)) && !(64 + lane < k && !(w[1] >= 0.0f));
+        okw = __ballot(!okw) == 0;
+        if (!okw || tot == 0.0f) {
+          st = XS_ROW_ZERO_WEIGHT;
+        } else {
+          // cumulative weights cum[i] = prefix through i (i < keep - 1), the
+          // total after it; the index is the number of them <= x
+          const float x_draw = u_row * tot + 0.0f;
+          const float cum0 = (lane < keep - 1) ? c[0] : tot;
+          const float cum1 = (64 + lane < keep - 1) ? c[1] : tot;
+          const int idx = (int)__popcll(__ballot(lane < k - 1 && cum0 <= x_draw)) +
+                          (int)__popcll(__ballot(64 + lane < k - 1 && cum1 <= x_draw));
+          tok = (int)pk_id(pick64(pk, idx));
         }
-        tok = (int)pk_id(pick64(pk, idx));
       }
-#undef XS_W
     }
   }
 
@@ -1325,7 +1381,7 @@ __global__ void fill_verify_kernel(const xs_verify_args a, int32_t st) {
 
 __global__ void exp_kernel(const float* x, float* y, int64_t n) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) y[i] = cr_expf(x[i]);
+  if (i < n) y[i] = cr_expf(x[i], &xs::kExpT[0][0]);
 }
 
 }  // namespace xs
@@ -1399,7 +1455,7 @@ int xs_create(int device, int64_t max_rows, int64_t vocab, int32_t k_max, xs_con
   *out = nullptr;
   if (hipSetDevice(device) != hipSuccess) return XS_ERR_HIP;
   const int32_t mc = chunks_for(vocab);
-  if (mc > 64) return XS_ERR_CAPACITY;  // a finalizing wave holds one chunk header per lane
+  if (mc * xs::NWAVE > xs::GMAX * 64) return XS_ERR_CAPACITY;  // sub-records a finalizing wave reads
   xs_context* c = (xs_context*)calloc(1, sizeof(xs_context));
   if (!c) return XS_ERR_HIP;
   c->device = device;
@@ -1408,9 +1464,10 @@ int xs_create(int device, int64_t max_rows, int64_t vocab, int32_t k_max, xs_con
   c->vocab = vocab;
   c->k_max = k_max;
   c->max_chunks = mc;
-  const int64_t units = max_rows * (int64_t)mc;
-  bool ok = hipMalloc((void**)&c->rec, units * xs::RECW * sizeof(uint64_t)) == hipSuccess;
-  ok = ok && hipMemset(c->rec, 0, units * xs::RECW * sizeof(uint64_t)) == hipSuccess;
+  const int64_t nsp = ((int64_t)mc * xs::NWAVE + 63) / 64 * 64;  // sub-records per row, padded
+  const int64_t units = max_rows * nsp;
+  bool ok = hipMalloc((void**)&c->rec, units * xs::SRECW * sizeof(uint64_t)) == hipSuccess;
+  ok = ok && hipMemset(c->rec, 0, units * xs::SRECW * sizeof(uint64_t)) == hipSuccess;
   ok = ok && hipMalloc((void**)&c->row_ticket, max_rows * sizeof(int32_t)) == hipSuccess;
   ok = ok && hipMalloc((void**)&c->seq_ticket, max_rows * sizeof(int32_t)) == hipSuccess;
   ok = ok && hipMemset(c->row_ticket, 0, max_rows * sizeof(int32_t)) == hipSuccess;

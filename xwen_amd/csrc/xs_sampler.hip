@@ -35,6 +35,8 @@
 // __builtin_fma calls) and IEEE f32 denormals.
 
 #include <hip/hip_runtime.h>
+
+#include <algorithm>
 #include <math.h>
 #include <stdint.h>
 #include <stdlib.h>
@@ -293,13 +295,9 @@ XS_DEV Cfg make_cfg(const xs_row_params& p, int64_t enc, int n_top) {
 // ---------------------------------------------------------------------------
 // Workspace and launch arguments.
 //
-// Chunks hand their results to the row's finalizing wave through the workspace
-// with agent-scope (sc1) stores and loads, which are coherent across the XCDs'
-// L2 caches without the whole-L2 writeback / invalidate a __threadfence()
-// costs.  A writer waits for its stores to be acknowledged (s_waitcnt) before
-// it bumps the row's arrival ticket; the wave that brings the ticket to its
-// last value reads everything back with sc1 loads.  Every record carries the
-// launch's epoch, so a stale read is detected (and reported) instead of used.
+// chunk_kernel writes one sub-record per wave into the workspace;
+// finalize_kernel, launched after it on the same stream, reads them.  The
+// kernel boundary is the hand-off: no atomics, no flags, no fences.
 
 struct Args {
   const float* logits;
@@ -334,25 +332,10 @@ struct Args {
   int32_t* seq_status;
   // geometry + workspace
   int32_t n_chunks, nslots;
-  uint32_t epoch;
   uint64_t* rec;     // [rows, SRECW, nsp]: word i of sub-record s of a row at i * nsp + s
-  int32_t* row_ticket;
-  int32_t* seq_ticket;
 };
 
-XS_DEV void st_agent(uint64_t* p, uint64_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-XS_DEV void st_agent(uint32_t* p, uint32_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-XS_DEV void st_agent(int32_t* p, int32_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-XS_DEV uint64_t ld_agent(const uint64_t* p) { return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-XS_DEV uint32_t ld_agent(const uint32_t* p) { return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
-XS_DEV int32_t ld_agent(const int32_t* p) { return __hip_atomic_load(const_cast<int32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 
-// Wait until every memory operation this wave issued has completed.
-XS_DEV void drain() {
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt(0);
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
 
 // Order this wave's LDS writes before its later LDS reads by other lanes.
 XS_DEV void wave_lds_sync() {
@@ -449,7 +432,7 @@ XS_DEV uint64_t pick64(const uint64_t (&x)[R], int i) {
 //   w1  c_s (f32 bits) | c_r (f32 bits) << 32: the partials' offsets
 //   w2  R (f64 bits): sum of e^(v - c_r) over the raw logits (held_row)
 //   w3  wave max (f32 bits) | flags << 32
-//   w4  entry count | epoch << 32
+//   w4  entry count
 //   w5  bound keys 0 | 1 << 32;  w6  bound keys 2 | 3 << 32
 //   w8..  entries: pack(key, id) of the wave's candidates
 // A row has n_chunks * NWAVE sub-records, chunk-major, stored transposed:
@@ -468,7 +451,6 @@ constexpr double LN2D = 0.693147180559945309417;
 struct ChunkLds {
   uint32_t groupmax[BLOCK / 4];     // maxima of 4-lane groups
   uint32_t lanemax[BLOCK];          // lane maxima
-  int32_t arrive;                   // waves of this workgroup that have published
 };
 struct FinLds {
   uint64_t list[SURV];              // gathered survivors
@@ -517,20 +499,31 @@ XS_DEV float q4(const v4f& q, int e) { return e == 0 ? q.x : e == 1 ? q.y : e ==
 // Rare path of the chunk pass: more than CAPW of this wave's elements lie at
 // or above the chunk bound (ties at the bound, or a bound far below the
 // wave's values).  Writes the wave's exact K' best (logit desc, id asc)
-// elements from its registers: every key above a threshold key, then the
-// lowest ids equal to it.  The threshold is the bound when fewer than K' keys
-// lie strictly above it, else the wave's K'-th largest key (bisection).
-// Elements that are -inf or NaN never become candidates.  Returns the count.
-XS_DEV int wave_overflow(const v4f (&q)[SPC], uint64_t* sub, int nsp, int kp, uint32_t tk, int base_id) {
-  const int lane = lane_id();
+// elements: every key above a threshold key, then the lowest ids equal to it.
+// The threshold is the bound when fewer than K' keys lie strictly above it,
+// else the wave's K'-th largest key (bisection).  Elements that are -inf or
+// NaN never become candidates.  Re-reads the wave's elements from memory, so
+// the streaming path keeps no registers for it.  Returns the count.
+template <bool HAS_MASK>
+XS_DEV int wave_overflow(const float* rowp, const uint32_t* mrow, int s0, int ns,
+                                          int enc, uint64_t* sub, int nsp, int kp, uint32_t tk) {
+  const int tid = threadIdx.x;
+  // element e of this lane's float4 in slot j, controlled; -inf when absent
+  auto elem = [&](int j, int e) __attribute__((always_inline)) -> float {
+    const int id = (s0 + j) * SLOT + 4 * tid + e;
+    if (j >= ns || id >= enc) return -INFINITY;
+    float x = rowp[id];
+    if (HAS_MASK && !((mrow[id >> 5] >> (id & 31)) & 1u)) x = -INFINITY;
+    return x;
+  };
   auto valid = [](float x) __attribute__((always_inline)) { return x == x && x > -INFINITY; };
   auto count = [&](uint32_t key, bool strict) __attribute__((always_inline)) -> int {
     int c = 0;
-#pragma unroll
+#pragma unroll 1
     for (int j = 0; j < SPC; j++)
-#pragma unroll
+#pragma unroll 1
       for (int e = 0; e < 4; e++) {
-        const float x = q4(q[j], e);
+        const float x = elem(j, e);
         const uint32_t k = fkey(x);
         c += (valid(x) && (strict ? k > key : k >= key)) ? 1 : 0;
       }
@@ -539,6 +532,7 @@ XS_DEV int wave_overflow(const v4f (&q)[SPC], uint64_t* sub, int nsp, int kp, ui
   uint32_t eq = max(tk, fkey(-__FLT_MAX__));
   if (count(eq, true) >= kp) {
     uint32_t ans = 0;
+#pragma unroll 1
     for (int bit = 31; bit >= 0; bit--) {
       const uint32_t cand = ans | (1u << bit);
       if (count(cand, false) >= kp) ans = cand;
@@ -546,309 +540,312 @@ XS_DEV int wave_overflow(const v4f (&q)[SPC], uint64_t* sub, int nsp, int kp, ui
     eq = ans;
   }
   int n = 0;
-#pragma unroll
+#pragma unroll 1
   for (int j = 0; j < SPC; j++)
-#pragma unroll
+#pragma unroll 1
     for (int e = 0; e < 4; e++) {
-      const float x = q4(q[j], e);
+      const float x = elem(j, e);
       const bool hit = valid(x) && fkey(x) > eq;
       const uint64_t b = __ballot(hit);
       const int pos = n + lanes_below(b);
-      if (hit && pos < CAPW) st_agent(sub + (int64_t)(SHDR + pos) * nsp, pack(fkey(x), (uint32_t)(base_id + j * SLOT + e)));
+      if (hit && pos < CAPW) sub[(int64_t)(SHDR + pos) * nsp] = pack(fkey(x), (uint32_t)((s0 + j) * SLOT + 4 * tid + e));
       n += __popcll(b);
     }
   n = min(n, CAPW);
-  // ties at eq, lowest ids first: slot j covers ids base + j*SLOT in lane order
+  // ties at eq, lowest ids first: slot j covers ids (s0 + j) * SLOT in lane order
   int need = kp - n;
+#pragma unroll 1
+  for (int j = 0; j < SPC && need > 0; j++) {
+    bool t[4];
+    int c = 0;
 #pragma unroll
-  for (int j = 0; j < SPC; j++) {
-    if (need > 0) {  // uniform; the loop stays unrolled so q[j] stays in registers
-      bool t[4];
-      int c = 0;
-#pragma unroll
-      for (int e = 0; e < 4; e++) {
-        const float x = q4(q[j], e);
-        t[e] = valid(x) && fkey(x) == eq;
-        c += t[e] ? 1 : 0;
-      }
-      const int incl = wave_incl_scan(c);
-      int pos = incl - c;
-#pragma unroll
-      for (int e = 0; e < 4; e++)
-        if (t[e]) {
-          if (pos < need && n + pos < CAPW) st_agent(sub + (int64_t)(SHDR + n + pos) * nsp, pack(eq, (uint32_t)(base_id + j * SLOT + e)));
-          pos++;
-        }
-      const int tot = (int)rdl((uint32_t)incl, 63);
-      n += min(tot, need);
-      need -= tot;
+    for (int e = 0; e < 4; e++) {
+      const float x = elem(j, e);
+      t[e] = valid(x) && fkey(x) == eq;
+      c += t[e] ? 1 : 0;
     }
+    const int incl = wave_incl_scan(c);
+    int pos = incl - c;
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+      if (t[e]) {
+        if (pos < need && n + pos < CAPW) sub[(int64_t)(SHDR + n + pos) * nsp] = pack(eq, (uint32_t)((s0 + j) * SLOT + 4 * tid + e));
+        pos++;
+      }
+    const int tot = (int)rdl((uint32_t)incl, 63);
+    n += min(tot, need);
+    need -= tot;
   }
-  (void)lane;
   return min(n, CAPW);
 }
 
 // ---------------------------------------------------------------------------
-// The kernel.  Grid: rows x n_chunks workgroups of BLOCK lanes; chunk c of a
-// row covers slots [c*SPC, c*SPC + SPC).  Every wave reduces its own share of
-// the chunk and publishes it as one sub-record; the row's last wave (atomic
-// ticket over all of the row's waves) finalizes the row.
+// Wave reductions to a uniform value: an inclusive pass within each row of 16
+// lanes (DPP row_shr 1, 2, 4, 8), then the row totals carried with row_bcast
+// 15 and 31, so lane 63 holds the result; all VALU, no LDS traffic.
+template <int CTRL, int RM>
+XS_DEV int dppi(int old, int v) { return __builtin_amdgcn_update_dpp(old, v, CTRL, RM, 0xF, false); }
+template <int CTRL, int RM>
+XS_DEV float dppf(float old, float v) { return __int_as_float(dppi<CTRL, RM>(__float_as_int(old), __float_as_int(v))); }
+template <int CTRL, int RM>
+XS_DEV double dppd(double v) {  // identity 0.0 (the f64 sum)
+  const long long b = __double_as_longlong(v);
+  const int lo = dppi<CTRL, RM>(0, (int)(uint32_t)b);
+  const int hi = dppi<CTRL, RM>(0, (int)(uint32_t)((unsigned long long)b >> 32));
+  return __longlong_as_double((long long)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo));
+}
+#define XS_ROWRED(STEP)                                                        \
+  STEP(0x111, 0xF) STEP(0x112, 0xF) STEP(0x114, 0xF) STEP(0x118, 0xF)          \
+  STEP(0x142, 0xA) STEP(0x143, 0xC)
+XS_DEV float red_maxf(float v) {
+#define XS_S(C, R) v = fmaxf(v, dppf<C, R>(-INFINITY, v));
+  XS_ROWRED(XS_S)
+#undef XS_S
+  return rdlf(v, 63);
+}
+XS_DEV int red_maxi(int v) {
+#define XS_S(C, R) v = max(v, dppi<C, R>(INT32_MIN, v));
+  XS_ROWRED(XS_S)
+#undef XS_S
+  return (int)rdl((uint32_t)v, 63);
+}
+XS_DEV uint32_t red_or(uint32_t v) {
+#define XS_S(C, R) v |= (uint32_t)dppi<C, R>(0, (int)v);
+  XS_ROWRED(XS_S)
+#undef XS_S
+  return rdl(v, 63);
+}
+XS_DEV double red_sumd(double v) {
+#define XS_S(C, R) v += dppd<C, R>(v);
+  XS_ROWRED(XS_S)
+#undef XS_S
+  const long long b = __double_as_longlong(v);
+  const uint32_t lo = rdl((uint32_t)b, 63), hi = rdl((uint32_t)((unsigned long long)b >> 32), 63);
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+#undef XS_ROWRED
 
+// ---------------------------------------------------------------------------
+// Row finalize, common case: at most 64 sub-records (one per lane), K' <= 64,
+// at most EPRE entries per sub-record, at most 64 survivors, and no boundary
+// tie that needs the id-ordered row scan.  Returns false (having written
+// nothing) when the row is outside that case; the general finalizer then
+// does the row.  Same arithmetic, in the same order, as the general path.
 template <bool HAS_MASK, bool WANT_LSE>
-__global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) void sample_kernel(Args a) {
-  __shared__ Lds L;
-  const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
-  const int nc = a.n_chunks;
-  const int row = blockIdx.x / nc;
-  const int chunk = blockIdx.x - row * nc;
-  const int enc = (int)a.enc;
-  const Cfg cfg = make_cfg(a.params[row], a.enc, a.n_top);
-  const bool stoch = !cfg.greedy && !cfg.bad;
-  const int kp = cfg.kp;
+XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, const uint64_t* rr, int nsp, int nsub,
+                     FinLds& F) {
+  const int lane = lane_id();
+  const bool live = lane < nsub;
+  const bool stoch = !cfg.greedy;
+  const int kp = cfg.kp, k = cfg.k;
+  // One round of coalesced loads: every header word and the first EPRE
+  // entries of every sub-record, the row's uniform and the exp table.
+  uint64_t h[NHW], E[EPRE];
+#pragma unroll
+  for (int i = 0; i < NHW; i++) h[i] = live ? *(rr + i * nsp + lane) : 0ull;
+#pragma unroll
+  for (int j = 0; j < EPRE; j++) E[j] = live ? *(rr + (SHDR + j) * nsp + lane) : 0ull;
+  const float u_row = a.uniforms[row];
+  const double et = (&kExpT[0][0])[lane];
 
-  // ---------------- chunk pass ----------------
-  const int s0 = chunk * SPC;
-  const int ns = min(SPC, a.nslots - s0);
-  const float* rowp = a.logits + (int64_t)row * a.ld;
-  const v4f* rp4 = reinterpret_cast<const v4f*>(rowp);
-  const uint32_t* mrow = HAS_MASK ? a.allowed + (int64_t)row * a.allowed_ld : nullptr;
-  const int fmax = (enc - 1) >> 2;  // last float4 holding an encodable id
-
-  // Every load is unconditional (clamped to the row's last float4), so the
-  // compiler can wait for them one at a time, in order, while the arithmetic
-  // below runs on the ones that have arrived.
-  v4f q[SPC];
-  uint32_t mw[SPC];
-#pragma unroll
-  for (int j = 0; j < SPC; j++) {
-    const int f = min((s0 + j) * BLOCK + tid, fmax);
-    q[j] = __builtin_nontemporal_load(rp4 + f);
-    if (HAS_MASK) mw[j] = mrow[f >> 3];
-  }
-
-  // Online reduction, one float4 at a time, branch-free.  The softmax partial
-  // is summed in the reference's scaled domain, s = v * inv rounded to f32 as
-  // softmax_in_place does, as sum exp2(s*log2e - cL) with a per-lane offset
-  // cL = rn(c*log2e), c the lane's first scaled float4 max (0 if that is
-  // -inf); the constant error of cL is taken out exactly (an fma) when the
-  // lanes are combined.  A lane whose later values could overflow a term
-  // (more than 60 above c) is summed again after the loop against its max.
-  // A NaN, or a +inf value (inf - inf at the recount), makes the sum NaN: the
-  // stochastic NaN test.  The four terms of a float4 are added pairwise.
-  //
-  // The held_row partial (raw logits, f64 like the reference's denominator)
-  // keeps its per-lane offset at the lane's running max instead, so the
-  // largest term is exactly exp2(0) = 1 and the others, far smaller,
-  // accumulate in f64 without being absorbed: ln of a near-1 sum stays
-  // accurate to ~1e-15.
-  const float inv = cfg.inv;
-  float mr = -INFINITY;
-  float gm[SPC];
-  float sum = 0.0f, cL = 0.0f, c_s = 0.0f;
-  double racc = 0.0;
-  float rc = -__FLT_MAX__;
-  uint32_t nanl = 0;
-#pragma unroll
-  for (int j = 0; j < SPC; j++) {
-    float x[4] = {q[j].x, q[j].y, q[j].z, q[j].w};
-    if (HAS_MASK) {
-      const uint32_t bits = mw[j] >> ((((s0 + j) * BLOCK + tid) & 7) * 4);
-#pragma unroll
-      for (int e = 0; e < 4; e++)
-        if (!((bits >> e) & 1u)) x[e] = -INFINITY;
-    }
-    if (j >= ns || (s0 + j + 1) * SLOT > enc) {  // absent or partial slot (uniform)
-      const int id0 = (s0 + j) * SLOT + 4 * tid;
-#pragma unroll
-      for (int e = 0; e < 4; e++)
-        if (j >= ns || id0 + e >= enc) x[e] = -INFINITY;
-    }
-    q[j] = v4f{x[0], x[1], x[2], x[3]};
-    gm[j] = vmax(vmax3(x[0], x[1], x[2]), x[3]);
-    mr = vmax(mr, gm[j]);
-    if (stoch) {
-      if (j == 0) {
-        const float c = cfg.scale ? gm[0] * inv : gm[0];
-        c_s = (c > -INFINITY && c < INFINITY) ? c : 0.0f;
-        cL = c_s * LOG2E;
-      }
-      float t[4];
-      if (cfg.scale) {
-#pragma unroll
-        for (int e = 0; e < 4; e++) t[e] = xexp2(__builtin_fmaf(x[e] * inv, LOG2E, -cL));
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; e++) t[e] = xexp2(__builtin_fmaf(x[e], LOG2E, -cL));
-      }
-      sum += (t[0] + t[1]) + (t[2] + t[3]);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 4; e++) nanl |= (x[e] != x[e]) ? 1u : 0u;
-    }
+  const int cnt = live ? (int)(uint32_t)h[4] : 0;
+  const float m_v = red_maxf(live ? __uint_as_float((uint32_t)h[3]) : -INFINITY);
+  const uint32_t fl = red_or(live ? (uint32_t)(h[3] >> 32) : 0u);
+  if (red_maxi(cnt) > EPRE) return false;
+  const float m_s = cfg.scale ? m_v * cfg.inv : m_v;
+  double part = 0.0, rpart = 0.0;
+  if (live) {
+    const double p = __longlong_as_double((long long)h[0]);
+    if (p != 0.0) part = p * (double)xexp2((__uint_as_float((uint32_t)h[1]) - m_s) * LOG2E);
     if (WANT_LSE) {
-      if (gm[j] > rc) {
-        racc = (racc != 0.0) ? racc * (double)xexp2((rc - gm[j]) * LOG2E) : 0.0;
-        rc = gm[j];
-      }
-#pragma unroll
-      for (int e = 0; e < 4; e++) racc += (double)xexp2((x[e] - rc) * LOG2E);
+      const double r = __longlong_as_double((long long)h[2]);
+      if (r != 0.0) rpart = r * (double)xexp2((__uint_as_float((uint32_t)(h[1] >> 32)) - m_v) * LOG2E);
     }
   }
-  const float m_w = wave_maxf(mr);
-  double P = 0.0, R = 0.0;
-  float c_w = 0.0f;  // offset of the published softmax partial
-  uint32_t flags = 0;
-  if (stoch) {
-    // lanes whose max sits more than 60 above their offset: recount against
-    // the max (rare; makes +inf a NaN)
-    const float ms = cfg.scale ? mr * inv : mr;
-    const bool redo = ms > c_s + 60.0f;
-    if (__ballot(redo)) {
-      const float cn = redo ? ms : c_s;
-      const float cLn = cn * LOG2E;
-      float s2 = 0.0f;
-#pragma unroll
-      for (int j = 0; j < SPC; j++) {
-        float t[4];
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          const float xv = q4(q[j], e);
-          t[e] = xexp2(__builtin_fmaf(cfg.scale ? xv * inv : xv, LOG2E, -cLn));
-        }
-        s2 += (t[0] + t[1]) + (t[2] + t[3]);
-      }
-      if (redo) {
-        sum = s2;
-        c_s = cn;
-        cL = cLn;
-      }
-    }
-    // lanes to the wave's scaled max: factor e^(c_s - m_s) * 2^-(c_s*log2e - cL)
-    c_w = cfg.scale ? m_w * inv : m_w;
-    const float err = __builtin_fmaf(c_s, LOG2E, -cL);
-    const float d = __builtin_fmaf(c_s - c_w, LOG2E, -err);
-    const double part = (sum != 0.0f) ? (double)sum * (double)xexp2(d) : (double)sum;
-    P = wave_sumd(part);
-    if (P != P) flags |= 1u;
-  } else if (wave_or(nanl)) {
-    flags |= 1u;
-  }
-  if (WANT_LSE) {
-    // lanes to the wave max (the max's own lane by exactly exp2(0) = 1)
-    R = wave_sumd((racc != 0.0) ? racc * (double)xexp2((rc - m_w) * LOG2E) : racc);
-    if (R != R) flags |= 1u;
-  }
-  const float c_r = m_w;
-  if (HAS_MASK) {
-    if (__builtin_isfinite(m_w)) {
-      flags |= 2u;
-    } else if (m_w == INFINITY) {
-      bool fin = false;
-#pragma unroll
-      for (int j = 0; j < SPC; j++)
-#pragma unroll
-        for (int e = 0; e < 4; e++) fin |= __builtin_isfinite(q4(q[j], e));
-      if (__ballot(fin)) flags |= 2u;
-    }
-  }
+  const double S_d = red_sumd(part);
+  const double R_d = WANT_LSE ? red_sumd(rpart) : 0.0;
+  const float S = (float)S_d;
+  const bool nan_seen = fl & 1u;
+  const bool finite_seen = fl & 2u;
+  int st = XS_ROW_OK;
+  if (HAS_MASK && !finite_seen) st = XS_ROW_NO_FINITE;
+  else if (cfg.greedy) st = nan_seen ? XS_ROW_NAN : (m_v == -INFINITY ? XS_ROW_NO_FINITE : XS_ROW_OK);
+  else if (nan_seen || __builtin_isinf(m_s)) st = XS_ROW_NAN;
 
-  // Candidate bound: the K'-th largest of a set of distinct chunk elements, so
-  // at least K' elements of the chunk lie at or above it.  For K' <= 64 the set
-  // is the 64 maxima of 4-lane groups (each group holds 4 x 64 logits); for
-  // K' > 64, or when fewer than K' groups hold a finite value, it is all 256
-  // lane maxima.  Every wave sorts the set for itself (no second barrier).
-  const uint32_t km = fkey(mr);
-  {
-    uint32_t g = max(km, xor_u32(km, 1));
-    g = max(g, xor_u32(g, 2));
-    if ((lane & 3) == 0) L.c.groupmax[wave * 16 + (lane >> 2)] = g;
-    L.c.lanemax[tid] = km;
-    if (tid == 0) L.c.arrive = 0;
+  // Survivor bound: the K'-th largest published wave max.
+  uint32_t tau = 0;
+  if (nsub >= kp) {
+    uint32_t x[1] = {live ? (uint32_t)h[5] : 0u};
+    wave_sort_desc<1>(x);
+    tau = rdl(x[0], kp - 1);
   }
-  __syncthreads();
-  uint32_t tk = 0;
-  // Keys this sub-record publishes for the row's survivor bound: the wave max
-  // (K' <= 64), or the chunk's lane maxima of rank wave + 4r (K' > 64).
-  uint32_t pub[4] = {fkey(m_w), 0u, 0u, 0u};
-  if (!cfg.bad) {
-    if (kp <= 64) {
-      uint32_t x[1] = {L.c.groupmax[lane]};
-      wave_sort_desc<1, true>(x);
-      tk = rdl(x[0], kp - 1);
-    }
-    if (kp > 64 || tk <= KEY_NEG_INF) {
-      uint32_t all[4];
+  // Gather the survivors into LDS, then order them by rank: a survivor's
+  // position is the number of survivors above it ((key, ~id) are distinct).
+  const uint64_t floor_e = (uint64_t)tau << 32;
+  int M = 0;
 #pragma unroll
-      for (int r = 0; r < 4; r++) all[r] = L.c.lanemax[r * 64 + lane];
-      wave_sort_desc<4, true>(all);
-      const int i = kp - 1;
-#pragma unroll
-      for (int r = 0; r < 4; r++)
-        if ((i >> 6) == r) tk = rdl(all[r], i & 63);
-      if (kp > 64) {
-#pragma unroll
-        for (int r = 0; r < 4; r++) pub[r] = rdl(all[0], wave + 4 * r);
-      }
+  for (int j = 0; j < EPRE; j++) {
+    const bool ok = j < cnt && E[j] >= floor_e;
+    const uint64_t b = __ballot(ok);
+    if (b) {
+      const int pos = M + lanes_below(b);
+      if (ok && pos < 64) F.list[pos] = E[j];
+      M += __popcll(b);
     }
   }
+  if (M > 64) return false;
+  F.expt[lane] = et;
+  wave_lds_sync();
+  const uint64_t xv = lane < M ? F.list[lane] : 0ull;
+  int rank = 0;
+  for (int j0 = 0; j0 < M; j0 += 8) {
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      const uint64_t y = rdl64(xv, (j0 + u) & 63);
+      rank += (j0 + u < M && y > xv) ? 1 : 0;
+    }
+  }
+  if (lane < M) F.psel[rank] = xv;
+  wave_lds_sync();
+  const uint64_t sel = lane < M ? F.psel[lane] : 0ull;
+  const int nsel = min(M, kp);
 
-  // Filter: this wave's elements at or above the bound (never -inf, never
-  // NaN), compacted with ballots straight into the wave's sub-record.
-  const int nsp = ((nc * NWAVE + 63) >> 6) << 6;
-  uint64_t* const rowrec = a.rec + (int64_t)row * SRECW * nsp;
-  uint64_t* sub = rowrec + chunk * NWAVE + wave;
-  const int base_id = s0 * SLOT + 4 * tid;
-  int cnt = 0;
-  if (!cfg.bad) {
-    const float tf = (tk <= KEY_NEG_INF) ? -__FLT_MAX__ : keyf(tk);
+  // Probabilities of the selection (lanes < nsel) and, on lane nsel, of the
+  // largest value below the last selected logit (the boundary proof).
+  const bool want_cands = a.cand_id != nullptr || a.cand_w != nullptr;
+  const double* T = F.expt;
+  float pw = 0.0f;
+  uint64_t pk = 0ull;
+  float w = 0.0f;
+  int tok = -1;
+  if (stoch && st == XS_ROW_OK) {
+    const float vL = nsel > 0 ? keyf(pk_key(rdl64(sel, nsel - 1))) : -INFINITY;
+    const bool need_below = !cfg.full && vL != -INFINITY;
+    const bool in = lane < nsel;
+    float pe = 0.0f;
+    if (in || (lane == nsel && need_below)) pe = exact_p(in ? keyf(pk_key(sel)) : next_below(vL), cfg, m_s, S, T);
+    if (in) {
+      pw = pe;
+      pk = ((uint64_t)__float_as_uint(pe + 0.0f) << 32) | (uint64_t)(0xFFFFFFFFu - pk_id(sel));
+    }
+    float pbelow = 0.0f;
+    if (need_below) pbelow = nsel < 64 ? rdlf(pe, nsel) : exact_p(next_below(vL), cfg, m_s, S, T);
+    // (p desc, id asc): p is non-increasing along the logit order, so only
+    // runs of equal p can be out of order
+    const uint64_t nxt = shfl64(pk, (lane + 1) & 63);
+    if (__ballot(lane + 1 < nsel && pk < nxt)) {
+      uint64_t x[1] = {pk};
+      wave_sort_desc64<1>(x);
+      pk = x[0];
+    }
+    if (!cfg.full) {
+      const float Pk = __uint_as_float((uint32_t)(rdl64(pk, k - 1) >> 32));
+      const float pL = rdlf(pw, nsel - 1);
+      bool slow = nsel < kp;
+      if (!slow && pL == Pk) {
+        const bool other = __ballot(in && pw == Pk && keyf(pk_key(sel)) != vL) != 0;
+        slow = other || pbelow == Pk;
+      }
+      if (slow && Pk == 0.0f && !want_cands) slow = false;
+      if (slow) return false;  // ties at P_k: the general path scans the row
+    }
+
+    // The draw (truncate_top_p, then WeightedIndex), serial f32: lane i
+    // ends each chain with the serial prefix sum through weight i.
+    w = lane < k ? __uint_as_float((uint32_t)(pk >> 32)) : 0.0f;
+    auto chain = [&](float init) __attribute__((always_inline)) -> float {
+      float acc = init;
 #pragma unroll
-    for (int j = 0; j < SPC; j++) {
-      if (__ballot(gm[j] >= tf)) {
+      for (int b0 = 0; b0 < 64; b0 += 8) {
+        if (b0 < k) {
+          float q[8];
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-          const float x = q4(q[j], e);
-          const bool hit = x >= tf;
-          const uint64_t b = __ballot(hit);
-          if (b) {
-            const int pos = cnt + lanes_below(b);
-            if (hit && pos < CAPW) st_agent(sub + (int64_t)(SHDR + pos) * nsp, pack(fkey(x), (uint32_t)(base_id + j * SLOT + e)));
-            cnt += __popcll(b);
-          }
+          for (int u = 0; u < 8; u++) q[u] = rdlf(w, b0 + u);
+#pragma unroll
+          for (int u = 0; u < 8; u++) acc = acc + ((lane >= b0 + u) ? q[u] : 0.0f);
         }
       }
+      return acc;
+    };
+    bool zero = false;
+    if (!(cfg.top_p >= 1.0f)) {
+      const float sum = rdlf(chain(-0.0f), k - 1);  // folds from -0.0 as Rust's f32 Sum does
+      if (!(sum > 0.0f)) zero = true;  // all weights zero: returned unchanged
+      else w = __fdiv_rn(w, sum);
     }
-    if (cnt > CAPW) cnt = wave_overflow(q, sub, nsp, kp, tk, base_id);
+    if (zero) {
+      st = XS_ROW_ZERO_WEIGHT;
+    } else {
+      const float c = chain(0.0f);
+      int keep = k;
+      if (!(cfg.top_p >= 1.0f)) {
+        const uint64_t bm = __ballot(lane < k && c >= cfg.top_p);
+        if (bm) keep = (int)__builtin_ctzll(bm) + 1;
+        if (lane >= keep) w = 0.0f;
+      }
+      const float tot = rdlf(c, keep - 1);
+      if (__ballot(lane < k && !(w >= 0.0f)) || tot == 0.0f) {
+        st = XS_ROW_ZERO_WEIGHT;
+      } else {
+        const float x_draw = u_row * tot + 0.0f;
+        const float cum = lane < keep - 1 ? c : tot;
+        const int idx = (int)__popcll(__ballot(lane < k - 1 && cum <= x_draw));
+        tok = (int)pk_id(rdl64(pk, idx));
+      }
+    }
+  } else if (st == XS_ROW_OK) {
+    tok = (int)pk_id(rdl64(sel, 0));
   }
 
-  // Publish the sub-record header, wait for every store to land, then take
-  // the row's arrival ticket.
+  // Outputs.
   if (lane == 0) {
-    st_agent(sub + 0 * nsp, (uint64_t)__double_as_longlong(P));
-    st_agent(sub + 1 * nsp, ((uint64_t)__float_as_uint(c_r) << 32) | __float_as_uint(c_w));
-    st_agent(sub + 2 * nsp, (uint64_t)__double_as_longlong(R));
-    st_agent(sub + 3 * nsp, ((uint64_t)flags << 32) | __float_as_uint(m_w));
-    st_agent(sub + 4 * nsp, ((uint64_t)a.epoch << 32) | (uint32_t)cnt);
-    st_agent(sub + 5 * nsp, ((uint64_t)pub[1] << 32) | pub[0]);
-    st_agent(sub + 6 * nsp, ((uint64_t)pub[3] << 32) | pub[2]);
+    a.token[row] = st == XS_ROW_OK ? tok : -1;
+    a.status[row] = st;
+    if (a.n_cand) a.n_cand[row] = (stoch && st == XS_ROW_OK) ? k : 0;
+    if (a.soft_max) a.soft_max[row] = m_s;
+    if (a.soft_sum) a.soft_sum[row] = S;
+    if (WANT_LSE) {
+      if (a.row_max) a.row_max[row] = m_v;
+      if (a.row_lse) a.row_lse[row] = (!nan_seen && !__builtin_isinf(m_v)) ? (double)m_v + log(R_d) : __builtin_nan("");
+    }
   }
-  // The workgroup's last wave to get here (an LDS counter) takes the row's
-  // ticket for all four: one global atomic per workgroup, not per wave.
-  drain();
-  const int nsub = nc * NWAVE;
-  int tb = 0;
-  if (lane == 0) tb = atomicAdd(&L.c.arrive, 1);
-  tb = (int)rdl((uint32_t)tb, 0);
-  if (tb != NWAVE - 1) return;
-  int t = 0;
-  if (lane == 0) t = __hip_atomic_fetch_add(&a.row_ticket[row], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  t = (int)rdl((uint32_t)t, 0);
-  if (t != nc - 1) return;
-  if (lane == 0) st_agent(&a.row_ticket[row], 0);
+  if (want_cands && stoch && st == XS_ROW_OK) {
+    const int kw = (int)min((int64_t)k, a.cand_ld);
+    if (lane < kw) {
+      if (a.cand_id) a.cand_id[(int64_t)row * a.cand_ld + lane] = (int32_t)(0xFFFFFFFFu - (uint32_t)pk);
+      if (a.cand_w) a.cand_w[(int64_t)row * a.cand_ld + lane] = w;
+    }
+  }
+  if (WANT_LSE && a.n_top > 0) {
+    const bool ok = !nan_seen && !__builtin_isinf(m_v);
+    const double lse = ok ? (double)m_v + log(R_d) : __builtin_nan("");
+    const int nt = min(a.n_top, (int)a.enc);
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+      const int i = r * 64 + lane;
+      if (i < a.n_top) {
+        const bool have = r == 0 && i < nt && i < nsel;
+        if (a.top_id) a.top_id[(int64_t)row * a.top_ld + i] = have ? (int32_t)pk_id(sel) : -1;
+        if (a.top_logprob)
+          a.top_logprob[(int64_t)row * a.top_ld + i] = have ? (float)((double)keyf(pk_key(sel)) - lse) : __builtin_nanf("");
+      }
+    }
+  }
+  return true;
+}
 
-  // ---------------- row finalize: the row's last wave ----------------
-  // Every wave of this workgroup has published (the LDS counter), so the
-  // workgroup's LDS is free.  Lane l handles sub-records l + 64g.
-  FinLds& F = L.f;
+// ---------------------------------------------------------------------------
+// Row finalize, general case (the rows fin_fast leaves): any number of
+// sub-records up to GMAX * 64, K' up to KSEL, survivors past 64, entries past
+// EPRE, and the id-ordered scan for probability ties at the top-k boundary.
+// Lane l handles sub-records l + 64g.  Out of line: it is rare, and inlined
+// it would cost the streaming path registers.
+template <bool HAS_MASK, bool WANT_LSE>
+XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* rowrec,
+                        int nsp, int nsub, const float* rowp, const uint32_t* mrow, FinLds& F) {
+  const int lane = lane_id();
+  const int kp = cfg.kp, enc = (int)a.enc;
+  const bool stoch = !cfg.greedy && !cfg.bad;
   const uint64_t* rr = rowrec;
   const int G = (nsub + 63) >> 6;
   const float u_row = a.uniforms[row];  // prefetched for the draw
@@ -865,33 +862,18 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
   auto load0 = [&]() __attribute__((always_inline)) {
     if (lane < nsub) {
 #pragma unroll
-      for (int i = 0; i < NHW; i++) h0[i] = ld_agent(rr + i * nsp + lane);
+      for (int i = 0; i < NHW; i++) h0[i] = *(rr + i * nsp + lane);
 #pragma unroll
-      for (int j = 0; j < EPRE; j++) E[j] = ld_agent(rr + (SHDR + j) * nsp + lane);
+      for (int j = 0; j < EPRE; j++) E[j] = *(rr + (SHDR + j) * nsp + lane);
     }
   };
   auto hdr = [&](int g, int i) __attribute__((always_inline)) -> uint64_t {
     const int s = g * 64 + lane;
     if (g == 0) return h0[i];
-    return (g < G && s < nsub) ? ld_agent(rr + i * nsp + s) : 0ull;
+    return (g < G && s < nsub) ? *(rr + i * nsp + s) : 0ull;
   };
   auto has = [&](int g) __attribute__((always_inline)) { return g < G && g * 64 + lane < nsub; };
   load0();  // one round of loads
-  // Every record carries the launch's epoch: one that is not visible yet is
-  // re-read (bounded), then reported rather than used.
-  auto stale_now = [&]() __attribute__((always_inline)) {
-    bool st0 = false;
-#pragma unroll
-    for (int g = 0; g < GMAX; g++)
-      if (has(g) && (uint32_t)(hdr(g, 4) >> 32) != a.epoch) st0 = true;
-    return st0;
-  };
-  bool stale = stale_now();
-  for (int spin = 0; spin < 1000 && __ballot(stale); spin++) {
-    load0();
-    stale = stale_now();
-  }
-  const bool any_stale = __ballot(stale) != 0;
 
   float mv = -INFINITY;
   uint32_t fw = 0;
@@ -930,8 +912,7 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
   const bool finite_seen = fl & 2u;
 
   int st = XS_ROW_OK;
-  if (any_stale) st = XS_ROW_INTERNAL;
-  else if (cfg.bad) st = XS_ROW_BAD_PARAM;
+  if (cfg.bad) st = XS_ROW_BAD_PARAM;
   else if (HAS_MASK && !finite_seen) st = XS_ROW_NO_FINITE;
   else if (cfg.greedy) st = nan_seen ? XS_ROW_NAN : (m_v == -INFINITY ? XS_ROW_NO_FINITE : XS_ROW_OK);
   else if (nan_seen || __builtin_isinf(m_s)) st = XS_ROW_NAN;
@@ -999,7 +980,7 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
     for (int j = j0; j < maxc; j += 8) {
       uint64_t e[8];
 #pragma unroll
-      for (int u = 0; u < 8; u++) e[u] = (j + u < c) ? ld_agent(rr + (int64_t)(SHDR + j + u) * nsp + s) : 0ull;
+      for (int u = 0; u < 8; u++) e[u] = (j + u < c) ? *(rr + (int64_t)(SHDR + j + u) * nsp + s) : 0ull;
 #pragma unroll
       for (int u = 0; u < 8; u++) put(e[u], j + u < c && e[u] >= fl_e);
     }
@@ -1032,7 +1013,7 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
       for (int g = 0; g < GMAX; g++) {
         const int s = g * 64 + lane;
         const int n = has(g) ? (int)(uint32_t)hdr(g, 4) : 0;
-        for (int j = 0; j < n; j++) c += ld_agent(rr + (int64_t)(SHDR + j) * nsp + s) >= cnd ? 1 : 0;
+        for (int j = 0; j < n; j++) c += *(rr + (int64_t)(SHDR + j) * nsp + s) >= cnd ? 1 : 0;
       }
       if (wave_sumi(c) >= kp) ans = cnd;
     }
@@ -1279,10 +1260,10 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
     }
   }
 
-  // Outputs (sc1 stores: a verify walk on another wave reads token/status).
+  // Outputs.
   if (lane == 0) {
-    st_agent(&a.token[row], st == XS_ROW_OK ? tok : -1);
-    st_agent(&a.status[row], st);
+    a.token[row] = st == XS_ROW_OK ? tok : -1;
+    a.status[row] = st;
     if (a.n_cand) a.n_cand[row] = (stoch && st == XS_ROW_OK) ? k : 0;
     if (a.soft_max) a.soft_max[row] = m_s;
     if (a.soft_sum) a.soft_sum[row] = S;
@@ -1313,7 +1294,7 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
     for (int r = 0; r < 2; r++) {
       const int i = r * 64 + lane;
       if (i < a.n_top) {
-        const bool have = i < nt && i < nsel && !cfg.bad && !any_stale;
+        const bool have = i < nt && i < nsel && !cfg.bad;
         if (a.top_id) a.top_id[(int64_t)row * a.top_ld + i] = have ? (int32_t)pk_id(sel[r]) : -1;
         if (a.top_logprob)
           a.top_logprob[(int64_t)row * a.top_ld + i] = have ? (float)((double)keyf(pk_key(sel[r])) - lse) : __builtin_nanf("");
@@ -1321,24 +1302,295 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
     }
   }
 
-  // Speculative verify: the last finalizer of a sequence walks its rows.
+}
+
+// ---------------------------------------------------------------------------
+// The kernel.  Grid: rows x n_chunks workgroups of BLOCK lanes; chunk c of a
+// row covers slots [c*SPC, c*SPC + SPC).  Every wave reduces its own share of
+// the chunk and publishes it as one sub-record; the row's last wave (atomic
+// ticket over all of the row's waves) finalizes the row.
+
+template <bool HAS_MASK, bool WANT_LSE>
+__global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) void chunk_kernel(Args a) {
+  __shared__ ChunkLds Lc;
+  const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
+  const int nc = a.n_chunks;
+  const int row = blockIdx.x / nc;
+  const int chunk = blockIdx.x - row * nc;
+  const int enc = (int)a.enc;
+
+  // ---------------- chunk pass ----------------
+  const int s0 = chunk * SPC;
+  const int ns = min(SPC, a.nslots - s0);
+  const float* rowp = a.logits + (int64_t)row * a.ld;
+  const v4f* rp4 = reinterpret_cast<const v4f*>(rowp);
+  const uint32_t* mrow = HAS_MASK ? a.allowed + (int64_t)row * a.allowed_ld : nullptr;
+  const int fmax = (enc - 1) >> 2;  // last float4 holding an encodable id
+
+  // Every load is unconditional (clamped to the row's last float4), so the
+  // compiler can wait for them one at a time, in order, while the arithmetic
+  // below runs on the ones that have arrived.
+  v4f q[SPC];
+  uint32_t mw[SPC];
+#pragma unroll
+  for (int j = 0; j < SPC; j++) {
+    const int f = min((s0 + j) * BLOCK + tid, fmax);
+    q[j] = __builtin_nontemporal_load(rp4 + f);
+    if (HAS_MASK) mw[j] = mrow[f >> 3];
+  }
+  // The row's parameters are read only now, so that round trip overlaps the
+  // loads instead of delaying them.
+  const Cfg cfg = make_cfg(a.params[row], a.enc, a.n_top);
+  const bool stoch = !cfg.greedy && !cfg.bad;
+  const int kp = cfg.kp;
+
+  // Online reduction, one float4 at a time, branch-free.  The softmax partial
+  // is summed in the reference's scaled domain, s = v * inv rounded to f32 as
+  // softmax_in_place does, as sum exp2(s*log2e - cL) with a per-lane offset
+  // cL = rn(c*log2e), c the lane's first scaled float4 max (0 if that is
+  // -inf); the constant error of cL is taken out exactly (an fma) when the
+  // lanes are combined.  A lane whose later values could overflow a term
+  // (more than 60 above c) is summed again after the loop against its max.
+  // A NaN, or a +inf value (inf - inf at the recount), makes the sum NaN: the
+  // stochastic NaN test.  The four terms of a float4 are added pairwise.
+  //
+  // The held_row partial (raw logits, f64 like the reference's denominator)
+  // keeps its per-lane offset at the lane's running max instead, so the
+  // largest term is exactly exp2(0) = 1 and the others, far smaller,
+  // accumulate in f64 without being absorbed: ln of a near-1 sum stays
+  // accurate to ~1e-15.
+  const float inv = cfg.inv;
+  float mr = -INFINITY;
+  float gm[SPC];
+  float sum = 0.0f, cL = 0.0f, c_s = 0.0f;
+  double racc = 0.0;
+  float rc = -__FLT_MAX__;
+  uint32_t nanl = 0;
+#pragma unroll
+  for (int j = 0; j < SPC; j++) {
+    float x[4] = {q[j].x, q[j].y, q[j].z, q[j].w};
+    if (HAS_MASK) {
+      const uint32_t bits = mw[j] >> ((((s0 + j) * BLOCK + tid) & 7) * 4);
+#pragma unroll
+      for (int e = 0; e < 4; e++)
+        if (!((bits >> e) & 1u)) x[e] = -INFINITY;
+    }
+    if (j >= ns || (s0 + j + 1) * SLOT > enc) {  // absent or partial slot (uniform)
+      const int id0 = (s0 + j) * SLOT + 4 * tid;
+#pragma unroll
+      for (int e = 0; e < 4; e++)
+        if (j >= ns || id0 + e >= enc) x[e] = -INFINITY;
+    }
+    q[j] = v4f{x[0], x[1], x[2], x[3]};
+    gm[j] = vmax(vmax3(x[0], x[1], x[2]), x[3]);
+    mr = vmax(mr, gm[j]);
+    if (stoch) {
+      if (j == 0) {
+        const float c = cfg.scale ? gm[0] * inv : gm[0];
+        c_s = (c > -INFINITY && c < INFINITY) ? c : 0.0f;
+        cL = c_s * LOG2E;
+      }
+      float t[4];
+      if (cfg.scale) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) t[e] = xexp2(__builtin_fmaf(x[e] * inv, LOG2E, -cL));
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; e++) t[e] = xexp2(__builtin_fmaf(x[e], LOG2E, -cL));
+      }
+      sum += (t[0] + t[1]) + (t[2] + t[3]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; e++) nanl |= (x[e] != x[e]) ? 1u : 0u;
+    }
+    if (WANT_LSE) {
+      if (gm[j] > rc) {
+        racc = (racc != 0.0) ? racc * (double)xexp2((rc - gm[j]) * LOG2E) : 0.0;
+        rc = gm[j];
+      }
+#pragma unroll
+      for (int e = 0; e < 4; e++) racc += (double)xexp2((x[e] - rc) * LOG2E);
+    }
+  }
+  const float m_w = wave_maxf(mr);
+  double P = 0.0, R = 0.0;
+  float c_w = 0.0f;  // offset of the published softmax partial
+  uint32_t flags = 0;
+  if (stoch) {
+    // lanes whose max sits more than 60 above their offset: recount against
+    // the max (rare; makes +inf a NaN)
+    const float ms = cfg.scale ? mr * inv : mr;
+    const bool redo = ms > c_s + 60.0f;
+    if (__ballot(redo)) {
+      const float cn = redo ? ms : c_s;
+      const float cLn = cn * LOG2E;
+      float s2 = 0.0f;
+#pragma unroll
+      for (int j = 0; j < SPC; j++) {
+        float t[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const float xv = q4(q[j], e);
+          t[e] = xexp2(__builtin_fmaf(cfg.scale ? xv * inv : xv, LOG2E, -cLn));
+        }
+        s2 += (t[0] + t[1]) + (t[2] + t[3]);
+      }
+      if (redo) {
+        sum = s2;
+        c_s = cn;
+        cL = cLn;
+      }
+    }
+    // lanes to the wave's scaled max: factor e^(c_s - m_s) * 2^-(c_s*log2e - cL)
+    c_w = cfg.scale ? m_w * inv : m_w;
+    const float err = __builtin_fmaf(c_s, LOG2E, -cL);
+    const float d = __builtin_fmaf(c_s - c_w, LOG2E, -err);
+    const double part = (sum != 0.0f) ? (double)sum * (double)xexp2(d) : (double)sum;
+    P = wave_sumd(part);
+    if (P != P) flags |= 1u;
+  } else if (wave_or(nanl)) {
+    flags |= 1u;
+  }
+  if (WANT_LSE) {
+    // lanes to the wave max (the max's own lane by exactly exp2(0) = 1)
+    R = wave_sumd((racc != 0.0) ? racc * (double)xexp2((rc - m_w) * LOG2E) : racc);
+    if (R != R) flags |= 1u;
+  }
+  const float c_r = m_w;
+  if (HAS_MASK) {
+    if (__builtin_isfinite(m_w)) {
+      flags |= 2u;
+    } else if (m_w == INFINITY) {
+      bool fin = false;
+#pragma unroll
+      for (int j = 0; j < SPC; j++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) fin |= __builtin_isfinite(q4(q[j], e));
+      if (__ballot(fin)) flags |= 2u;
+    }
+  }
+
+  // Candidate bound: the K'-th largest of a set of distinct chunk elements, so
+  // at least K' elements of the chunk lie at or above it.  For K' <= 64 the set
+  // is the 64 maxima of 4-lane groups (each group holds 4 x 64 logits); for
+  // K' > 64, or when fewer than K' groups hold a finite value, it is all 256
+  // lane maxima.  Every wave sorts the set for itself (no second barrier).
+  const uint32_t km = fkey(mr);
+  {
+    uint32_t g = max(km, xor_u32(km, 1));
+    g = max(g, xor_u32(g, 2));
+    if ((lane & 3) == 0) Lc.groupmax[wave * 16 + (lane >> 2)] = g;
+    Lc.lanemax[tid] = km;
+  }
+  __syncthreads();
+  uint32_t tk = 0;
+  // Keys this sub-record publishes for the row's survivor bound: the wave max
+  // (K' <= 64), or the chunk's lane maxima of rank wave + 4r (K' > 64).
+  uint32_t pub[4] = {fkey(m_w), 0u, 0u, 0u};
+  if (!cfg.bad) {
+    if (kp <= 64) {
+      uint32_t x[1] = {Lc.groupmax[lane]};
+      wave_sort_desc<1, true>(x);
+      tk = rdl(x[0], kp - 1);
+    }
+    if (kp > 64 || tk <= KEY_NEG_INF) {
+      uint32_t all[4];
+#pragma unroll
+      for (int r = 0; r < 4; r++) all[r] = Lc.lanemax[r * 64 + lane];
+      wave_sort_desc<4, true>(all);
+      const int i = kp - 1;
+#pragma unroll
+      for (int r = 0; r < 4; r++)
+        if ((i >> 6) == r) tk = rdl(all[r], i & 63);
+      if (kp > 64) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) pub[r] = rdl(all[0], wave + 4 * r);
+      }
+    }
+  }
+
+  // Filter: this wave's elements at or above the bound (never -inf, never
+  // NaN), compacted with ballots straight into the wave's sub-record.
+  const int nsp = ((nc * NWAVE + 63) >> 6) << 6;
+  uint64_t* const rowrec = a.rec + (int64_t)row * SRECW * nsp;
+  uint64_t* sub = rowrec + chunk * NWAVE + wave;
+  const int base_id = s0 * SLOT + 4 * tid;
+  int cnt = 0;
+  if (!cfg.bad) {
+    const float tf = (tk <= KEY_NEG_INF) ? -__FLT_MAX__ : keyf(tk);
+#pragma unroll
+    for (int j = 0; j < SPC; j++) {
+      if (__ballot(gm[j] >= tf)) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const float x = q4(q[j], e);
+          const bool hit = x >= tf;
+          const uint64_t b = __ballot(hit);
+          if (b) {
+            const int pos = cnt + lanes_below(b);
+            if (hit && pos < CAPW) sub[(int64_t)(SHDR + pos) * nsp] = pack(fkey(x), (uint32_t)(base_id + j * SLOT + e));
+            cnt += __popcll(b);
+          }
+        }
+      }
+    }
+    if (cnt > CAPW) cnt = wave_overflow<HAS_MASK>(rowp, mrow, s0, ns, enc, sub, nsp, kp, tk);
+  }
+
+  // Publish the sub-record header.  The finalize kernel, launched after this
+  // one on the same stream, reads all of it.
+  if (lane == 0) {
+    sub[0 * nsp] = (uint64_t)__double_as_longlong(P);
+    sub[1 * nsp] = ((uint64_t)__float_as_uint(c_r) << 32) | __float_as_uint(c_w);
+    sub[2 * nsp] = (uint64_t)__double_as_longlong(R);
+    sub[3 * nsp] = ((uint64_t)flags << 32) | __float_as_uint(m_w);
+    sub[4 * nsp] = (uint64_t)(uint32_t)cnt;
+    sub[5 * nsp] = ((uint64_t)pub[1] << 32) | pub[0];
+    sub[6 * nsp] = ((uint64_t)pub[3] << 32) | pub[2];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// The finalize kernel, launched after chunk_kernel on the same stream: one
+// workgroup per sequence (per row for a plain batch), one wave per row of it
+// (a wave takes every FWAVES-th row when the sequence has more).  A row takes
+// fin_fast, or fin_general when it falls outside the common case.  For a
+// speculative block the workgroup then walks its sequence (accept_drafts).
+constexpr int FWAVES = 8;
+
+template <bool HAS_MASK, bool WANT_LSE>
+__global__ __launch_bounds__(64 * FWAVES) void finalize_kernel(Args a) {
+  __shared__ FinLds Fw[FWAVES];
+  const int lane = lane_id(), wave = wave_id();
+  const int nwaves = (int)(blockDim.x >> 6);
+  const int span = a.span > 0 ? a.span : 1;
+  const int seq = blockIdx.x;
+  const int nc = a.n_chunks, nsub = nc * NWAVE, nsp = ((nsub + 63) >> 6) << 6;
+  for (int r = wave; r < span; r += nwaves) {
+    const int row = seq * span + r;
+    const Cfg cfg = make_cfg(a.params[row], a.enc, a.n_top);
+    const uint64_t* rowrec = a.rec + (int64_t)row * SRECW * nsp;
+    const float* rowp = a.logits + (int64_t)row * a.ld;
+    const uint32_t* mrow = HAS_MASK ? a.allowed + (int64_t)row * a.allowed_ld : nullptr;
+    const bool done = nsub <= 64 && cfg.kp <= 64 && !cfg.bad &&
+                      fin_fast<HAS_MASK, WANT_LSE>(a, cfg, row, rowrec, nsp, nsub, Fw[wave]);
+    if (!done) fin_general<HAS_MASK, WANT_LSE>(a, cfg, row, rowrec, nsp, nsub, rowp, mrow, Fw[wave]);
+  }
+  (void)lane;
+
+  // Speculative verify: accept_drafts over the sequence's sampled rows.
   if (a.span > 0) {
-    drain();
-    const int seq = row / a.span;
-    int ts = 0;
-    if (lane == 0) ts = __hip_atomic_fetch_add(&a.seq_ticket[seq], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    ts = (int)rdl((uint32_t)ts, 0);
-    if (ts == a.span - 1 && lane == 0) {
-      st_agent(&a.seq_ticket[seq], 0);
-      const int span = a.span, D = span - 1;
+    __syncthreads();  // every row of the sequence has its token and status
+    if (threadIdx.x == 0) {
+      const int D = span - 1;
       const int64_t r0 = (int64_t)seq * span;
       const int bud = a.budget ? a.budget[seq] : 0x7FFFFFFF;
       int mcount = 0, ncom = 0, sst = XS_ROW_OK;
       for (int i = 0; i < span; i++) {
         if (ncom >= bud) break;
-        const int rs = ld_agent(&a.status[r0 + i]);
+        const int rs = a.status[r0 + i];
         if (rs != XS_ROW_OK) { sst = rs; break; }
-        const int s = ld_agent(&a.token[r0 + i]);
+        const int s = a.token[r0 + i];
         const bool matched = i < D && s == a.drafts[(int64_t)seq * D + i];
         a.committed[(int64_t)seq * span + ncom] = s;
         ncom++;
@@ -1395,10 +1647,7 @@ struct xs_context {
   int64_t max_rows, vocab;
   int32_t k_max;
   int32_t max_chunks;
-  uint32_t epoch;
   uint64_t* rec;
-  int32_t* row_ticket;
-  int32_t* seq_ticket;
 };
 
 namespace {
@@ -1432,15 +1681,23 @@ int check_common(xs_context* ctx, const Call& c) {
   return XS_OK;
 }
 
-int launch(xs_context* ctx, xs::Args& a, int64_t rows, bool mask, bool lse) {
+// chunk_kernel over rows x n_chunks workgroups, then finalize_kernel with one
+// workgroup per sequence of `span` rows (span 1: a plain batch).
+template <bool M, bool S>
+void launch2(xs_context* ctx, xs::Args& a, dim3 g1, dim3 g2, dim3 b2) {
+  hipLaunchKernelGGL((xs::chunk_kernel<M, S>), g1, dim3(xs::BLOCK), 0, ctx->stream, a);
+  hipLaunchKernelGGL((xs::finalize_kernel<M, S>), g2, b2, 0, ctx->stream, a);
+}
+
+int launch(xs_context* ctx, xs::Args& a, int64_t rows, int span, bool mask, bool lse) {
   const int64_t grid = rows * (int64_t)a.n_chunks;
   if (grid == 0) return XS_OK;
-  if (grid > 0x7FFFFFFF) return XS_ERR_CAPACITY;
-  dim3 g((unsigned)grid), b(xs::BLOCK);
+  if (grid > 0x7FFFFFFF || span < 1) return XS_ERR_CAPACITY;
   if (mask && lse) return XS_ERR_ARG;
-  if (mask) hipLaunchKernelGGL((xs::sample_kernel<true, false>), g, b, 0, ctx->stream, a);
-  else if (lse) hipLaunchKernelGGL((xs::sample_kernel<false, true>), g, b, 0, ctx->stream, a);
-  else hipLaunchKernelGGL((xs::sample_kernel<false, false>), g, b, 0, ctx->stream, a);
+  const dim3 g1((unsigned)grid), g2((unsigned)(rows / span)), b2(64 * (unsigned)std::min(span, xs::FWAVES));
+  if (mask) launch2<true, false>(ctx, a, g1, g2, b2);
+  else if (lse) launch2<false, true>(ctx, a, g1, g2, b2);
+  else launch2<false, false>(ctx, a, g1, g2, b2);
   return hipGetLastError() == hipSuccess ? XS_OK : XS_ERR_HIP;
 }
 
@@ -1468,10 +1725,6 @@ int xs_create(int device, int64_t max_rows, int64_t vocab, int32_t k_max, xs_con
   const int64_t units = max_rows * nsp;
   bool ok = hipMalloc((void**)&c->rec, units * xs::SRECW * sizeof(uint64_t)) == hipSuccess;
   ok = ok && hipMemset(c->rec, 0, units * xs::SRECW * sizeof(uint64_t)) == hipSuccess;
-  ok = ok && hipMalloc((void**)&c->row_ticket, max_rows * sizeof(int32_t)) == hipSuccess;
-  ok = ok && hipMalloc((void**)&c->seq_ticket, max_rows * sizeof(int32_t)) == hipSuccess;
-  ok = ok && hipMemset(c->row_ticket, 0, max_rows * sizeof(int32_t)) == hipSuccess;
-  ok = ok && hipMemset(c->seq_ticket, 0, max_rows * sizeof(int32_t)) == hipSuccess;
   ok = ok && hipDeviceSynchronize() == hipSuccess;
   if (!ok) {
     xs_destroy(c);
@@ -1486,8 +1739,6 @@ int xs_destroy(xs_context* c) {
   (void)hipSetDevice(c->device);
   if (c->stream) (void)hipStreamSynchronize(c->stream); else (void)hipDeviceSynchronize();
   (void)hipFree(c->rec);
-  (void)hipFree(c->row_ticket);
-  (void)hipFree(c->seq_ticket);
   free(c);
   return XS_OK;
 }
@@ -1546,12 +1797,8 @@ int xs_sample(xs_context* ctx, const xs_sample_args* in) {
   a.span = 0;
   a.n_chunks = chunks_for(in->enc);
   a.nslots = (int32_t)slots_for(in->enc);
-  if (++ctx->epoch == 0) ctx->epoch = 1;
-  a.epoch = ctx->epoch;
   a.rec = ctx->rec;
-  a.row_ticket = ctx->row_ticket;
-  a.seq_ticket = ctx->seq_ticket;
-  return launch(ctx, a, in->rows, in->allowed != nullptr, lse);
+  return launch(ctx, a, in->rows, 1, in->allowed != nullptr, lse);
 }
 
 int xs_verify(xs_context* ctx, const xs_verify_args* in) {
@@ -1597,12 +1844,8 @@ int xs_verify(xs_context* ctx, const xs_verify_args* in) {
   a.seq_status = in->seq_status;
   a.n_chunks = chunks_for(in->enc);
   a.nslots = (int32_t)slots_for(in->enc);
-  if (++ctx->epoch == 0) ctx->epoch = 1;
-  a.epoch = ctx->epoch;
   a.rec = ctx->rec;
-  a.row_ticket = ctx->row_ticket;
-  a.seq_ticket = ctx->seq_ticket;
-  return launch(ctx, a, rows, in->allowed != nullptr, false);
+  return launch(ctx, a, rows, (int)in->span, in->allowed != nullptr, false);
 }
 
 int64_t xs_keep_confident(const float* probs, int64_t n, float p_min) {

@@ -345,6 +345,34 @@ XS_DEV void wave_lds_sync() {
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
 }
 
+// Sorts n <= 256 distinct u64 keys from src into dst, descending: a key's
+// position is the number of keys above it, counted by every lane over all n
+// keys (LDS broadcast reads).  One wave; both arrays in LDS.
+XS_DEV void rank_sort_lds(const uint64_t* src, uint64_t* dst, int n) {
+  const int lane = threadIdx.x & 63;
+  uint64_t x[4];
+  int rk[4];
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    x[r] = (r * 64 + lane < n) ? src[r * 64 + lane] : 0ull;
+    rk[r] = 0;
+  }
+#pragma unroll 8
+  for (int j = 0; j < n; j++) {
+    const uint64_t y = src[j];
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+      if (r * 64 < n) rk[r] += (y > x[r]) ? 1 : 0;
+  }
+#pragma unroll
+  for (int r = 0; r < 4; r++)
+    if (r * 64 + lane < n) dst[rk[r]] = x[r];
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+}
+
 XS_DEV uint32_t rdl(uint32_t x, int i) { return (uint32_t)__builtin_amdgcn_readlane((int)x, i); }
 XS_DEV float rdlf(float x, int i) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), i)); }
 XS_DEV uint64_t rdl64(uint64_t x, int i) {
@@ -451,9 +479,11 @@ constexpr double LN2D = 0.693147180559945309417;
 struct ChunkLds {
   uint32_t groupmax[BLOCK / 4];     // maxima of 4-lane groups
   uint32_t lanemax[BLOCK];          // lane maxima
+  int32_t nhit[NWAVE];              // each wave's entry count (filter)
 };
 struct FinLds {
   uint64_t list[SURV];              // gathered survivors
+  uint64_t srt[SURV];               // survivors in (logit desc, id asc) order
   uint64_t psel[KSEL];              // the candidate set in draw order: (p bits << 32) | ~id
   double expt[64];                  // kExpT, flattened
   uint32_t keys[GMAX * 64 * 4];     // published bound keys (more than 64 sub-records)
@@ -632,23 +662,16 @@ XS_DEV double red_sumd(double v) {
 // nothing) when the row is outside that case; the general finalizer then
 // does the row.  Same arithmetic, in the same order, as the general path.
 template <bool HAS_MASK, bool WANT_LSE>
-XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, const uint64_t* rr, int nsp, int nsub,
-                     FinLds& F) {
+XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, int nsub, const uint64_t (&h)[NHW],
+                     const uint64_t (&E)[EPRE], FinLds& F) {
   const int lane = lane_id();
   const bool live = lane < nsub;
   const bool stoch = !cfg.greedy;
   const int kp = cfg.kp, k = cfg.k;
-  // One round of coalesced loads: every header word and the first EPRE
-  // entries of every sub-record, the row's uniform and the exp table.
-  uint64_t h[NHW], E[EPRE];
-#pragma unroll
-  for (int i = 0; i < NHW; i++) h[i] = live ? *(rr + i * nsp + lane) : 0ull;
-#pragma unroll
-  for (int j = 0; j < EPRE; j++) E[j] = live ? *(rr + (SHDR + j) * nsp + lane) : 0ull;
   const float u_row = a.uniforms[row];
   const double et = (&kExpT[0][0])[lane];
 
-  const int cnt = live ? (int)(uint32_t)h[4] : 0;
+  const int cnt = live ? (int)min((uint32_t)h[4], (uint32_t)CAPW) : 0;  // clamped: never read past a sub-record
   const float m_v = red_maxf(live ? __uint_as_float((uint32_t)h[3]) : -INFINITY);
   const uint32_t fl = red_or(live ? (uint32_t)(h[3] >> 32) : 0u);
   if (red_maxi(cnt) > EPRE) return false;
@@ -850,30 +873,13 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
   const int G = (nsub + 63) >> 6;
   const float u_row = a.uniforms[row];  // prefetched for the draw
   const double et = (&kExpT[0][0])[lane];  // the exp table, staged into LDS below
-  // Group 0's headers (and first EPRE entries) live in registers; the
-  // headers of further groups (vocabularies above 64 sub-records) are re-read
-  // from the workspace where they are used.
-  uint64_t h0[NHW];
-  uint64_t E[EPRE];
-#pragma unroll
-  for (int i = 0; i < NHW; i++) h0[i] = 0ull;
-#pragma unroll
-  for (int j = 0; j < EPRE; j++) E[j] = 0ull;
-  auto load0 = [&]() __attribute__((always_inline)) {
-    if (lane < nsub) {
-#pragma unroll
-      for (int i = 0; i < NHW; i++) h0[i] = *(rr + i * nsp + lane);
-#pragma unroll
-      for (int j = 0; j < EPRE; j++) E[j] = *(rr + (SHDR + j) * nsp + lane);
-    }
-  };
-  auto hdr = [&](int g, int i) __attribute__((always_inline)) -> uint64_t {
-    const int s = g * 64 + lane;
-    if (g == 0) return h0[i];
-    return (g < G && s < nsub) ? *(rr + i * nsp + s) : 0ull;
-  };
+  // Headers and entries are read from the workspace where they are used
+  // (this path is rare; holding them in registers would cost the kernel's
+  // common path its register budget).
   auto has = [&](int g) __attribute__((always_inline)) { return g < G && g * 64 + lane < nsub; };
-  load0();  // one round of loads
+  auto hdr = [&](int g, int i) __attribute__((always_inline)) -> uint64_t {
+    return has(g) ? rr[i * nsp + g * 64 + lane] : 0ull;
+  };
 
   float mv = -INFINITY;
   uint32_t fw = 0;
@@ -884,7 +890,7 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
       const uint64_t h3 = hdr(g, 3), h4 = hdr(g, 4);
       mv = fmaxf(mv, __uint_as_float((uint32_t)h3));
       fw |= (uint32_t)(h3 >> 32);
-      maxc = max(maxc, (int)(uint32_t)h4);
+      maxc = max(maxc, (int)min((uint32_t)h4, (uint32_t)CAPW));
     }
   }
   const float m_v = wave_maxf(mv);
@@ -928,11 +934,12 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
       uint32_t x[4] = {0u, 0u, 0u, 0u};
       if (G == 1) {
         if (lane < nsub) {
-          x[0] = (uint32_t)h0[5];
+          const uint64_t h5 = hdr(0, 5), h6 = hdr(0, 6);
+          x[0] = (uint32_t)h5;
           if (qk == 4) {
-            x[1] = (uint32_t)(h0[5] >> 32);
-            x[2] = (uint32_t)h0[6];
-            x[3] = (uint32_t)(h0[6] >> 32);
+            x[1] = (uint32_t)(h5 >> 32);
+            x[2] = (uint32_t)h6;
+            x[3] = (uint32_t)(h6 >> 32);
           }
         }
       } else {
@@ -977,27 +984,20 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
   };
   auto gather_global = [&](int s, int c, int j0, uint64_t fl_e) __attribute__((always_inline)) {
     // entries j0..c-1 of sub-record s, read from the workspace
-    for (int j = j0; j < maxc; j += 8) {
-      uint64_t e[8];
+    for (int j = j0; j < maxc; j += 4) {
+      uint64_t e[4];
 #pragma unroll
-      for (int u = 0; u < 8; u++) e[u] = (j + u < c) ? *(rr + (int64_t)(SHDR + j + u) * nsp + s) : 0ull;
+      for (int u = 0; u < 4; u++) e[u] = (j + u < c) ? *(rr + (int64_t)(SHDR + j + u) * nsp + s) : 0ull;
 #pragma unroll
-      for (int u = 0; u < 8; u++) put(e[u], j + u < c && e[u] >= fl_e);
+      for (int u = 0; u < 4; u++) put(e[u], j + u < c && e[u] >= fl_e);
     }
   };
   auto gather = [&](uint64_t fl_e) __attribute__((always_inline)) {
     M = 0;
-    if (G == 1) {
-      const int c = lane < nsub ? (int)(uint32_t)h0[4] : 0;
 #pragma unroll
-      for (int j = 0; j < EPRE; j++) put(E[j], j < c && E[j] >= fl_e);
-      if (maxc > EPRE) gather_global(lane, c, EPRE, fl_e);
-    } else {
-#pragma unroll
-      for (int g = 0; g < GMAX; g++) {
-        const int s = g * 64 + lane;
-        if (g < G) gather_global(s, has(g) ? (int)(uint32_t)hdr(g, 4) : 0, 0, fl_e);
-      }
+    for (int g = 0; g < GMAX; g++) {
+      const int s = g * 64 + lane;
+      if (g < G) gather_global(s, has(g) ? (int)min((uint32_t)hdr(g, 4), (uint32_t)CAPW) : 0, 0, fl_e);
     }
   };
   if (!cfg.bad) gather(floor_e);
@@ -1012,7 +1012,7 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
 #pragma unroll
       for (int g = 0; g < GMAX; g++) {
         const int s = g * 64 + lane;
-        const int n = has(g) ? (int)(uint32_t)hdr(g, 4) : 0;
+        const int n = has(g) ? (int)min((uint32_t)hdr(g, 4), (uint32_t)CAPW) : 0;
         for (int j = 0; j < n; j++) c += *(rr + (int64_t)(SHDR + j) * nsp + s) >= cnd ? 1 : 0;
       }
       if (wave_sumi(c) >= kp) ans = cnd;
@@ -1024,22 +1024,11 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
   wave_lds_sync();
 
   // Sort the survivors (logit desc, id asc); the first K' are the selection.
-  uint64_t sel[4];
-#pragma unroll
-  for (int r = 0; r < 4; r++) sel[r] = (r * 64 + lane < M) ? F.list[r * 64 + lane] : 0ull;
-  if (M <= 64) {
-    uint64_t x[1] = {sel[0]};
-    wave_sort_desc64<1>(x);
-    sel[0] = x[0];
-  } else if (M <= 128) {
-    uint64_t x[2] = {sel[0], sel[1]};
-    wave_sort_desc64<2>(x);
-    sel[0] = x[0];
-    sel[1] = x[1];
-  } else {
-    wave_sort_desc64<4>(sel);
-  }
+  rank_sort_lds(F.list, F.srt, min(M, SURV));
   const int nsel = min(M, kp);  // == kp unless the row holds fewer finite values
+  uint64_t sel[2];
+#pragma unroll
+  for (int r = 0; r < 2; r++) sel[r] = (r * 64 + lane < nsel) ? F.srt[r * 64 + lane] : 0ull;
 
   // Probabilities of the selection and the (p desc, id asc) order; p is
   // non-increasing along the logit order, so only runs of equal p move.
@@ -1050,7 +1039,7 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
   const double* T = F.expt;
   // the value the boundary proof needs, p(next_below(vL)), is computed in the
   // same pass, by the lane just past the selection
-  const float vL = nsel > 0 ? keyf(pk_key(pick64(sel, nsel - 1))) : -INFINITY;
+  const float vL = nsel > 0 ? keyf(pk_key(F.srt[nsel - 1])) : -INFINITY;
   float pbelow = 0.0f;
   if (stoch && st == XS_ROW_OK) {
     const bool need_below = !cfg.full && vL != -INFINITY;
@@ -1088,13 +1077,12 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
     if (lane + 1 < nsel && pk[0] < (lane < 63 ? n0 : first1)) bad = true;
     if (64 + lane + 1 < nsel && pk[1] < n1) bad = true;
     if (__ballot(bad)) {
-      if (nsel <= 64) {
-        uint64_t x[1] = {pk[0]};
-        wave_sort_desc64<1>(x);
-        pk[0] = x[0];
-      } else {
-        wave_sort_desc64<2>(pk);
-      }
+      F.psel[lane] = pk[0];
+      F.psel[64 + lane] = pk[1];
+      wave_lds_sync();
+      rank_sort_lds(F.psel, F.list, nsel);
+      pk[0] = lane < nsel ? F.list[lane] : 0ull;
+      pk[1] = 64 + lane < nsel ? F.list[64 + lane] : 0ull;
     }
 
     // Boundary proof (top_k < enc): the k-th probability P_k must not be shared
@@ -1412,7 +1400,7 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
       for (int e = 0; e < 4; e++) racc += (double)xexp2((x[e] - rc) * LOG2E);
     }
   }
-  const float m_w = wave_maxf(mr);
+  const float m_w = red_maxf(mr);
   double P = 0.0, R = 0.0;
   float c_w = 0.0f;  // offset of the published softmax partial
   uint32_t flags = 0;
@@ -1446,14 +1434,14 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
     const float err = __builtin_fmaf(c_s, LOG2E, -cL);
     const float d = __builtin_fmaf(c_s - c_w, LOG2E, -err);
     const double part = (sum != 0.0f) ? (double)sum * (double)xexp2(d) : (double)sum;
-    P = wave_sumd(part);
+    P = red_sumd(part);
     if (P != P) flags |= 1u;
-  } else if (wave_or(nanl)) {
+  } else if (red_or(nanl)) {
     flags |= 1u;
   }
   if (WANT_LSE) {
     // lanes to the wave max (the max's own lane by exactly exp2(0) = 1)
-    R = wave_sumd((racc != 0.0) ? racc * (double)xexp2((rc - m_w) * LOG2E) : racc);
+    R = red_sumd((racc != 0.0) ? racc * (double)xexp2((rc - m_w) * LOG2E) : racc);
     if (R != R) flags |= 1u;
   }
   const float c_r = m_w;
@@ -1474,13 +1462,15 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
   // at least K' elements of the chunk lie at or above it.  For K' <= 64 the set
   // is the 64 maxima of 4-lane groups (each group holds 4 x 64 logits); for
   // K' > 64, or when fewer than K' groups hold a finite value, it is all 256
-  // lane maxima.  Every wave sorts the set for itself (no second barrier).
+  // lane maxima.  Every wave finds it for itself (no second barrier), by a
+  // bitwise search: the largest key with at least K' members at or above it.
   const uint32_t km = fkey(mr);
   {
     uint32_t g = max(km, xor_u32(km, 1));
     g = max(g, xor_u32(g, 2));
     if ((lane & 3) == 0) Lc.groupmax[wave * 16 + (lane >> 2)] = g;
     Lc.lanemax[tid] = km;
+    if (lane == 0) Lc.nhit[wave] = 0;
   }
   __syncthreads();
   uint32_t tk = 0;
@@ -1489,11 +1479,14 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
   uint32_t pub[4] = {fkey(m_w), 0u, 0u, 0u};
   if (!cfg.bad) {
     if (kp <= 64) {
-      uint32_t x[1] = {Lc.groupmax[lane]};
-      wave_sort_desc<1, true>(x);
-      tk = rdl(x[0], kp - 1);
+      const uint32_t gv = Lc.groupmax[lane];
+#pragma unroll
+      for (int bit = 31; bit >= 0; bit--) {
+        const uint32_t c = tk | (1u << bit);
+        if ((int)__popcll(__ballot(gv >= c)) >= kp) tk = c;
+      }
     }
-    if (kp > 64 || tk <= KEY_NEG_INF) {
+    if (kp > 64) {
       uint32_t all[4];
 #pragma unroll
       for (int r = 0; r < 4; r++) all[r] = Lc.lanemax[r * 64 + lane];
@@ -1502,15 +1495,28 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
 #pragma unroll
       for (int r = 0; r < 4; r++)
         if ((i >> 6) == r) tk = rdl(all[r], i & 63);
-      if (kp > 64) {
 #pragma unroll
-        for (int r = 0; r < 4; r++) pub[r] = rdl(all[0], wave + 4 * r);
+      for (int r = 0; r < 4; r++) pub[r] = rdl(all[0], wave + 4 * r);
+    } else if (tk <= KEY_NEG_INF) {
+      uint32_t all[4];
+#pragma unroll
+      for (int r = 0; r < 4; r++) all[r] = Lc.lanemax[r * 64 + lane];
+      tk = 0;
+#pragma unroll
+      for (int bit = 31; bit >= 0; bit--) {
+        const uint32_t c = tk | (1u << bit);
+        int n = 0;
+#pragma unroll
+        for (int r = 0; r < 4; r++) n += (int)__popcll(__ballot(all[r] >= c));
+        if (n >= kp) tk = c;
       }
     }
   }
 
   // Filter: this wave's elements at or above the bound (never -inf, never
-  // NaN), compacted with ballots straight into the wave's sub-record.
+  // NaN), written straight into the wave's sub-record.  Only the lanes
+  // holding a hit run the inner code; an LDS counter hands out positions (the
+  // entry order is immaterial: the finalizer sorts them).
   const int nsp = ((nc * NWAVE + 63) >> 6) << 6;
   uint64_t* const rowrec = a.rec + (int64_t)row * SRECW * nsp;
   uint64_t* sub = rowrec + chunk * NWAVE + wave;
@@ -1520,20 +1526,18 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
     const float tf = (tk <= KEY_NEG_INF) ? -__FLT_MAX__ : keyf(tk);
 #pragma unroll
     for (int j = 0; j < SPC; j++) {
-      if (__ballot(gm[j] >= tf)) {
+      if (gm[j] >= tf) {
 #pragma unroll
         for (int e = 0; e < 4; e++) {
           const float x = q4(q[j], e);
-          const bool hit = x >= tf;
-          const uint64_t b = __ballot(hit);
-          if (b) {
-            const int pos = cnt + lanes_below(b);
-            if (hit && pos < CAPW) sub[(int64_t)(SHDR + pos) * nsp] = pack(fkey(x), (uint32_t)(base_id + j * SLOT + e));
-            cnt += __popcll(b);
+          if (x >= tf) {
+            const int pos = atomicAdd(&Lc.nhit[wave], 1);
+            if (pos < CAPW) sub[(int64_t)(SHDR + pos) * nsp] = pack(fkey(x), (uint32_t)(base_id + j * SLOT + e));
           }
         }
       }
     }
+    cnt = __hip_atomic_load(&Lc.nhit[wave], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     if (cnt > CAPW) cnt = wave_overflow<HAS_MASK>(rowp, mrow, s0, ns, enc, sub, nsp, kp, tk);
   }
 
@@ -1568,12 +1572,20 @@ __global__ __launch_bounds__(64 * FWAVES) void finalize_kernel(Args a) {
   const int nc = a.n_chunks, nsub = nc * NWAVE, nsp = ((nsub + 63) >> 6) << 6;
   for (int r = wave; r < span; r += nwaves) {
     const int row = seq * span + r;
-    const Cfg cfg = make_cfg(a.params[row], a.enc, a.n_top);
     const uint64_t* rowrec = a.rec + (int64_t)row * SRECW * nsp;
+    // One round of coalesced loads, issued before anything else: every header
+    // word and the first EPRE entries of every sub-record (common case).
+    uint64_t h[NHW], E[EPRE];
+    const bool live = lane < nsub;
+#pragma unroll
+    for (int i = 0; i < NHW; i++) h[i] = live ? rowrec[i * nsp + lane] : 0ull;
+#pragma unroll
+    for (int j = 0; j < EPRE; j++) E[j] = live ? rowrec[(SHDR + j) * nsp + lane] : 0ull;
+    const Cfg cfg = make_cfg(a.params[row], a.enc, a.n_top);
     const float* rowp = a.logits + (int64_t)row * a.ld;
     const uint32_t* mrow = HAS_MASK ? a.allowed + (int64_t)row * a.allowed_ld : nullptr;
     const bool done = nsub <= 64 && cfg.kp <= 64 && !cfg.bad &&
-                      fin_fast<HAS_MASK, WANT_LSE>(a, cfg, row, rowrec, nsp, nsub, Fw[wave]);
+                      fin_fast<HAS_MASK, WANT_LSE>(a, cfg, row, nsub, h, E, Fw[wave]);
     if (!done) fin_general<HAS_MASK, WANT_LSE>(a, cfg, row, rowrec, nsp, nsub, rowp, mrow, Fw[wave]);
   }
   (void)lane;

@@ -163,6 +163,28 @@ typedef struct {
 
 int xs_verify(xs_context* ctx, const xs_verify_args* args);
 
+/* ---------------------------------------------------------------------------
+ * Drafter confidence: argmax_probs_device / draft_argmax_probs
+ * (generate.rs:4059-4087).  For each row of logits [rows, ld] (all `width`
+ * columns: the reference reduces the raw lm_head row, with no encodable bound
+ * and no temperature), the first maximal id (candle's argmax convention,
+ * ties -> lower id) and p = 1 / sum_j exp(l_j - max), the sum taken in f64 and
+ * rounded once to f32.  A row holding a NaN or +inf gets p = NaN (as candle's
+ * exp(inf - inf) does), and a row holding a NaN or nothing above -inf gets
+ * id -1; keep_confident truncates at a NaN p, so such ids are never drafted.
+ * Outputs are device pointers [rows].  Rows are independent; the call runs on
+ * the context's stream like xs_sample. */
+typedef struct {
+  const float* logits;   /* [rows, ld] row-major f32; 16-byte aligned, ld % 4 == 0 */
+  int64_t rows;
+  int64_t ld;            /* row stride in floats (>= width) */
+  int64_t width;         /* columns reduced */
+  int32_t* ids;          /* [rows] argmax id (-1: see above) */
+  float* probs;          /* [rows] probability of the argmax */
+} xs_argmax_args;
+
+int xs_argmax_probs(xs_context* ctx, const xs_argmax_args* args);
+
 /* keep_confident (generate.rs:3898-3905), host memory: the length of the
  * longest prefix whose probabilities are all >= p_min (a NaN ends it). */
 int64_t xs_keep_confident(const float* probs, int64_t n, float p_min);

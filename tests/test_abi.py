@@ -16,7 +16,7 @@ def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     declared = _lib.declared_symbols()
     assert {"xs_create", "xs_destroy", "xs_set_stream", "xs_sample", "xs_verify",
-            "xs_keep_confident", "xs_version", "xs_test_exp"} <= set(declared)
+            "xs_argmax_probs", "xs_keep_confident", "xs_version", "xs_test_exp"} <= set(declared)
     for name in declared:
         assert hasattr(lib, name), name
     out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True,
@@ -40,11 +40,13 @@ int main(void) {
   printf("xs_row_params %zu\n", sizeof(xs_row_params));
   printf("xs_sample_args %zu\n", sizeof(xs_sample_args));
   printf("xs_verify_args %zu\n", sizeof(xs_verify_args));
+  printf("xs_argmax_args %zu\n", sizeof(xs_argmax_args));
   F(xs_row_params, top_k); F(xs_row_params, top_p);
   F(xs_sample_args, params); F(xs_sample_args, allowed); F(xs_sample_args, token);
   F(xs_sample_args, cand_ld); F(xs_sample_args, n_top); F(xs_sample_args, top_ld);
   F(xs_verify_args, drafts); F(xs_verify_args, n_eog); F(xs_verify_args, eog);
   F(xs_verify_args, row_token); F(xs_verify_args, seq_status);
+  F(xs_argmax_args, width); F(xs_argmax_args, ids); F(xs_argmax_args, probs);
   return 0;
 }
 ''')
@@ -60,8 +62,9 @@ def test_ctypes_structs_match_the_header(tmp_path):
     assert C.sizeof(_lib.RowParams) == c["xs_row_params"]
     assert C.sizeof(_lib.SampleArgs) == c["xs_sample_args"]
     assert C.sizeof(_lib.VerifyArgs) == c["xs_verify_args"]
+    assert C.sizeof(_lib.ArgmaxArgs) == c["xs_argmax_args"]
     for struct, cname in ((_lib.RowParams, "xs_row_params"), (_lib.SampleArgs, "xs_sample_args"),
-                          (_lib.VerifyArgs, "xs_verify_args")):
+                          (_lib.VerifyArgs, "xs_verify_args"), (_lib.ArgmaxArgs, "xs_argmax_args")):
         for field, _ in struct._fields_:
             key = f"{cname}.{field}"
             if key in c:

@@ -321,6 +321,11 @@ def test_infinities(ctx, oracle):
     for r in range(4):
         o = oracle_row(oracle, x[r], 4096, [0.0, 1.0, 1.0, 0.0][r], 20, 0.95, 0.5)
         assert o.status == d["status"][r]
+    # asking for the row statistics changes no draw: a +inf voids the
+    # statistics (held_row needs a finite max) but not the greedy argmax
+    s = run_sample(ctx, x, [0.0, 1.0, 1.0, 0.0], 20, 0.95, 0.5, n_top=4)
+    assert list(s["status"]) == list(d["status"]) and s["token"][0] == 7
+    assert np.isnan(s["row_lse"]).all()
     # with an allow-mask, a row left with no finite value is NO_FINITE
     allow = np.zeros((1, 4096), bool)
     allow[0, :16] = True

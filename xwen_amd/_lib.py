@@ -54,6 +54,11 @@ class VerifyArgs(C.Structure):
     ]
 
 
+class ArgmaxArgs(C.Structure):
+    _fields_ = [("logits", _vp), ("rows", _i64), ("ld", _i64), ("width", _i64),
+                ("ids", _vp), ("probs", _vp)]
+
+
 class XsError(RuntimeError):
     pass
 
@@ -79,6 +84,8 @@ def load() -> C.CDLL:
     L.xs_sample.argtypes = [_vp, C.POINTER(SampleArgs)]
     L.xs_verify.restype = C.c_int
     L.xs_verify.argtypes = [_vp, C.POINTER(VerifyArgs)]
+    L.xs_argmax_probs.restype = C.c_int
+    L.xs_argmax_probs.argtypes = [_vp, C.POINTER(ArgmaxArgs)]
     L.xs_keep_confident.restype = _i64
     L.xs_keep_confident.argtypes = [_vp, _i64, C.c_float]
     L.xs_version.restype = C.c_char_p

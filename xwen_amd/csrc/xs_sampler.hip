@@ -292,6 +292,17 @@ XS_DEV Cfg make_cfg(const xs_row_params& p, int64_t enc, int n_top) {
   return c;
 }
 
+XS_DEV Cfg greedy_cfg() {
+  Cfg c;
+  c.inv = 1.0f;
+  c.top_p = 1.0f;
+  c.k = 0;
+  c.kp = 1;
+  c.greedy = true;
+  c.scale = c.full = c.bad = false;
+  return c;
+}
+
 // ---------------------------------------------------------------------------
 // Workspace and launch arguments.
 //
@@ -330,6 +341,10 @@ struct Args {
   int32_t* committed;
   int32_t* n_committed;
   int32_t* seq_status;
+  // argmax_probs: every row greedy (params and uniforms unused), p_max[row] =
+  // 1 / sum exp(v - max) over the raw row
+  int32_t greedy_all;
+  float* p_max;
   // geometry + workspace
   int32_t n_chunks, nslots;
   uint64_t* rec;     // [rows, SRECW, nsp]: word i of sub-record s of a row at i * nsp + s
@@ -668,7 +683,7 @@ XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, int nsub, const uin
   const bool live = lane < nsub;
   const bool stoch = !cfg.greedy;
   const int kp = cfg.kp, k = cfg.k;
-  const float u_row = a.uniforms[row];
+  const float u_row = a.greedy_all ? 0.0f : a.uniforms[row];
   const double et = (&kExpT[0][0])[lane];
 
   const int cnt = live ? (int)min((uint32_t)h[4], (uint32_t)CAPW) : 0;  // clamped: never read past a sub-record
@@ -830,6 +845,7 @@ XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, int nsub, const uin
     if (WANT_LSE) {
       if (a.row_max) a.row_max[row] = m_v;
       if (a.row_lse) a.row_lse[row] = (!nan_seen && !__builtin_isinf(m_v)) ? (double)m_v + log(R_d) : __builtin_nan("");
+      if (a.p_max) a.p_max[row] = (!nan_seen && !__builtin_isinf(m_v)) ? (float)(1.0 / R_d) : __builtin_nanf("");
     }
   }
   if (want_cands && stoch && st == XS_ROW_OK) {
@@ -871,7 +887,7 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
   const bool stoch = !cfg.greedy && !cfg.bad;
   const uint64_t* rr = rowrec;
   const int G = (nsub + 63) >> 6;
-  const float u_row = a.uniforms[row];  // prefetched for the draw
+  const float u_row = a.greedy_all ? 0.0f : a.uniforms[row];  // prefetched for the draw
   const double et = (&kExpT[0][0])[lane];  // the exp table, staged into LDS below
   // Headers and entries are read from the workspace where they are used
   // (this path is rare; holding them in registers would cost the kernel's
@@ -1261,6 +1277,7 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
         const bool ok = !nan_seen && !__builtin_isinf(m_v);
         a.row_lse[row] = ok ? (double)m_v + log(R_d) : __builtin_nan("");
       }
+      if (a.p_max) a.p_max[row] = (!nan_seen && !__builtin_isinf(m_v)) ? (float)(1.0 / R_d) : __builtin_nanf("");
     }
   }
   if (want_cands && stoch && st == XS_ROW_OK) {
@@ -1328,7 +1345,7 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
   }
   // The row's parameters are read only now, so that round trip overlaps the
   // loads instead of delaying them.
-  const Cfg cfg = make_cfg(a.params[row], a.enc, a.n_top);
+  const Cfg cfg = a.greedy_all ? greedy_cfg() : make_cfg(a.params[row], a.enc, a.n_top);
   const bool stoch = !cfg.greedy && !cfg.bad;
   const int kp = cfg.kp;
 
@@ -1441,8 +1458,10 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
   }
   if (WANT_LSE) {
     // lanes to the wave max (the max's own lane by exactly exp2(0) = 1)
+    // (a NaN R needs no flag of its own: a NaN logit already sets bit 0, and
+    // a +inf one leaves the row max infinite, which voids the statistics but
+    // not a greedy draw: argmax returns the first +inf, sampler.rs:268-286)
     R = red_sumd((racc != 0.0) ? racc * (double)xexp2((rc - m_w) * LOG2E) : racc);
-    if (R != R) flags |= 1u;
   }
   const float c_r = m_w;
   if (HAS_MASK) {
@@ -1581,7 +1600,7 @@ __global__ __launch_bounds__(64 * FWAVES) void finalize_kernel(Args a) {
     for (int i = 0; i < NHW; i++) h[i] = live ? rowrec[i * nsp + lane] : 0ull;
 #pragma unroll
     for (int j = 0; j < EPRE; j++) E[j] = live ? rowrec[(SHDR + j) * nsp + lane] : 0ull;
-    const Cfg cfg = make_cfg(a.params[row], a.enc, a.n_top);
+    const Cfg cfg = a.greedy_all ? greedy_cfg() : make_cfg(a.params[row], a.enc, a.n_top);
     const float* rowp = a.logits + (int64_t)row * a.ld;
     const uint32_t* mrow = HAS_MASK ? a.allowed + (int64_t)row * a.allowed_ld : nullptr;
     const bool done = nsub <= 64 && cfg.kp <= 64 && !cfg.bad &&
@@ -1660,6 +1679,7 @@ struct xs_context {
   int32_t k_max;
   int32_t max_chunks;
   uint64_t* rec;
+  int32_t* row_status;  // [max_rows] statuses of calls whose caller takes none (xs_argmax_probs)
 };
 
 namespace {
@@ -1737,6 +1757,7 @@ int xs_create(int device, int64_t max_rows, int64_t vocab, int32_t k_max, xs_con
   const int64_t units = max_rows * nsp;
   bool ok = hipMalloc((void**)&c->rec, units * xs::SRECW * sizeof(uint64_t)) == hipSuccess;
   ok = ok && hipMemset(c->rec, 0, units * xs::SRECW * sizeof(uint64_t)) == hipSuccess;
+  ok = ok && hipMalloc((void**)&c->row_status, max_rows * sizeof(int32_t)) == hipSuccess;
   ok = ok && hipDeviceSynchronize() == hipSuccess;
   if (!ok) {
     xs_destroy(c);
@@ -1751,6 +1772,7 @@ int xs_destroy(xs_context* c) {
   (void)hipSetDevice(c->device);
   if (c->stream) (void)hipStreamSynchronize(c->stream); else (void)hipDeviceSynchronize();
   (void)hipFree(c->rec);
+  (void)hipFree(c->row_status);
   free(c);
   return XS_OK;
 }
@@ -1858,6 +1880,28 @@ int xs_verify(xs_context* ctx, const xs_verify_args* in) {
   a.nslots = (int32_t)slots_for(in->enc);
   a.rec = ctx->rec;
   return launch(ctx, a, rows, (int)in->span, in->allowed != nullptr, false);
+}
+
+int xs_argmax_probs(xs_context* ctx, const xs_argmax_args* in) {
+  if (!ctx || !in || !in->logits || !in->ids || !in->probs) return XS_ERR_ARG;
+  if (in->rows < 0 || in->width < 1 || in->ld < in->width) return XS_ERR_ARG;
+  if (in->rows > ctx->max_rows || in->width > ctx->vocab) return XS_ERR_CAPACITY;
+  if (in->ld % 4 != 0 || !aligned16(in->logits)) return XS_ERR_ARG;
+  if (chunks_for(in->width) > ctx->max_chunks) return XS_ERR_CAPACITY;
+  if (hipSetDevice(ctx->device) != hipSuccess) return XS_ERR_HIP;
+  xs::Args a;
+  memset(&a, 0, sizeof(a));
+  a.logits = in->logits;
+  a.ld = in->ld;
+  a.enc = in->width;  // the whole row: the reference reduces the raw lm_head output
+  a.token = in->ids;
+  a.status = ctx->row_status;
+  a.greedy_all = 1;
+  a.p_max = in->probs;
+  a.n_chunks = chunks_for(in->width);
+  a.nslots = (int32_t)slots_for(in->width);
+  a.rec = ctx->rec;
+  return launch(ctx, a, in->rows, 1, false, true);
 }
 
 int64_t xs_keep_confident(const float* probs, int64_t n, float p_min) {

@@ -319,6 +319,31 @@ class Sampler:
         return self.sample_controlled(logits, None, uniforms)
 
 
+def argmax_probs_device(ctx: Context, logits, *, width: int | None = None):
+    """argmax_probs_device (generate.rs:4059-4070) through xs_argmax_probs: per
+    row the first maximal id and 1 / sum exp(l - max), left on the device as
+    int32 / float32 [rows] tensors.  logits: float32 [rows, ld] CUDA tensor."""
+    torch = _torch()
+    rows, ld = logits.shape
+    width = ld if width is None else width
+    ids = torch.empty(rows, dtype=torch.int32, device=logits.device)
+    probs = torch.empty(rows, dtype=torch.float32, device=logits.device)
+    a = _lib.ArgmaxArgs()
+    a.logits = logits.data_ptr()
+    a.rows, a.ld, a.width = rows, ld, width
+    a.ids = ids.data_ptr()
+    a.probs = probs.data_ptr()
+    _lib.check(ctx.lib.xs_argmax_probs(ctx.h, C.byref(a)), "xs_argmax_probs")
+    return ids, probs
+
+
+def draft_argmax_probs(ctx: Context, logits, *, width: int | None = None):
+    """draft_argmax_probs (generate.rs:4075-4087): argmax_probs_device read back,
+    as numpy int64 ids and float32 probabilities."""
+    ids, probs = argmax_probs_device(ctx, logits, width=width)
+    return ids.cpu().numpy().astype(np.int64), probs.cpu().numpy()
+
+
 def keep_confident(ids, probs, p_min: float):
     """keep_confident (generate.rs:3898-3905) through the C ABI (host memory)."""
     lib = _lib.load()

@@ -11,11 +11,13 @@
  *   xs_create / xs_destroy      Sampler::new                   src/sampler.rs:130-149
  *   xs_sample                   Sampler::sample_controlled     src/sampler.rs:190-232
  *                               + Sampler::draw                src/sampler.rs:235-243
- *                               (allow-mask: SampleControl::allowed, src/sampler.rs:87-93,
- *                                apply_control src/sampler.rs:433-448)
+ *                               (SampleControl, src/sampler.rs:85-121, and
+ *                                apply_control src/sampler.rs:433-490)
  *                               + held_row / last_logprobs_for src/generate.rs:1871-1933
  *   xs_verify                   accept_drafts                  src/generate.rs:4020-4046
  *                               over the verify block          src/generate.rs:2410-2461
+ *   xs_argmax_probs             argmax_probs_device /
+ *                               draft_argmax_probs             src/generate.rs:4059-4087
  *   xs_keep_confident           keep_confident                 src/generate.rs:3898-3905
  *
  * Randomness: the reference draws from a seeded StdRng inside the sampler.  Here
@@ -48,11 +50,12 @@ extern "C" {
  *   XS_ROW_NO_FINITE   nothing finite left after the controls (:483-488), or no
  *                      logit above -inf on the greedy path (:285)
  *   XS_ROW_MASK_SHORT  allow-mask narrower than the encodable ids (:437-442)
- *   XS_ROW_FORCE_OOR   forced id outside the vocabulary (:472-477); reserved
+ *   XS_ROW_FORCE_OOR   forced id outside the vocabulary (:472-477)
  *   XS_ROW_ZERO_WEIGHT WeightedIndex saw no probability mass (:238-240)
  *   XS_ROW_NARROW      logit row narrower than the encodable bound (:196-200)
- *   XS_ROW_BAD_PARAM   top_k larger than the context's k_max (no reference
- *                      counterpart: the reference has no such limit)
+ *   XS_ROW_BAD_PARAM   top_k larger than the context's k_max, or a control list
+ *                      past XS_CTL_MAX entries (no reference counterpart: the
+ *                      reference has no such limits)
  *   XS_ROW_INTERNAL    the device-side hand-off between a row's workgroups
  *                      read an incomplete record (never expected; reported
  *                      instead of returning a token computed from it)      */
@@ -92,6 +95,35 @@ int xs_destroy(xs_context* ctx);
 /* Bind the hipStream_t the context's kernels run on (NULL = the null stream). */
 int xs_set_stream(xs_context* ctx, void* hip_stream);
 
+/* The rest of one row's SampleControl (sampler.rs:85-121) past the allow-mask:
+ * bans, additive biases, a pull and a force, applied after the mask in the
+ * reference's order (apply_control, sampler.rs:433-490):
+ *   banned  every listed id < enc goes to -inf (ids >= enc are skipped);
+ *   bias    v[id] += delta for every listed (id, delta) with id < enc, in list
+ *           order (a repeated id adds each delta in turn), f32 adds;
+ *   pull    (id, alpha): if v[id] is finite, v[id] += alpha * max(0, M - v[id])
+ *           with M the max over the row after the bans and biases (NaN
+ *           ignored); a non-finite or out-of-range target is left alone;
+ *   force   id: every other value goes to -inf and the target keeps its value
+ *           if finite, else 0; id >= enc is XS_ROW_FORCE_OOR.
+ * Without a force, a row left with no finite value is XS_ROW_NO_FINITE.  The
+ * id lists live in two device pools shared by a call's rows: banned ids are
+ * ctl_ids[ban_off .. ban_off + n_ban), bias entry i is (ctl_ids[bias_off + i],
+ * ctl_delta[bias_off + i]).  A row may list at most XS_CTL_MAX bans and
+ * biases together; more (or a negative count or offset) is
+ * XS_ROW_BAD_PARAM.  A row whose lists are empty and whose has_pull and
+ * has_force are 0 is uncontrolled. */
+#define XS_CTL_MAX 2048
+typedef struct {
+  int32_t ban_off, n_ban;
+  int32_t bias_off, n_bias;
+  int32_t has_pull;
+  uint32_t pull_id;
+  float pull_alpha;
+  int32_t has_force;
+  uint32_t force_id;
+} xs_row_control;
+
 /* One batched Sampler::sample_controlled + draw over `rows` independent rows.
  * All pointers are device pointers.  Required: logits, params, uniforms, token,
  * status.  Everything else may be NULL. */
@@ -127,6 +159,11 @@ typedef struct {
   int32_t* top_id;       /* [rows, top_ld] or NULL */
   float* top_logprob;    /* [rows, top_ld] or NULL */
   int64_t top_ld;
+  /* SampleControl's bans, biases, pull and force (see xs_row_control), or
+   * controls = NULL for none.  Not combinable with the held_row outputs. */
+  const xs_row_control* controls; /* [rows] */
+  const uint32_t* ctl_ids;        /* banned and bias ids of every row */
+  const float* ctl_delta;         /* bias deltas, indexed as ctl_ids */
 } xs_sample_args;
 
 int xs_sample(xs_context* ctx, const xs_sample_args* args);
@@ -159,6 +196,12 @@ typedef struct {
   int32_t* committed;    /* [seqs, span] committed ids (accepted drafts then the bonus) */
   int32_t* n_committed;  /* [seqs] */
   int32_t* seq_status;   /* [seqs] the first row error the walk reached, else XS_ROW_OK */
+  /* per-position controls [seqs * span] as in xs_sample_args, or NULL: row i
+   * of a sequence carries the bans and forces the caller derived for it
+   * (generate.rs:2426-2461) */
+  const xs_row_control* controls;
+  const uint32_t* ctl_ids;
+  const float* ctl_delta;
 } xs_verify_args;
 
 int xs_verify(xs_context* ctx, const xs_verify_args* args);

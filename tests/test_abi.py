@@ -41,12 +41,16 @@ int main(void) {
   printf("xs_sample_args %zu\n", sizeof(xs_sample_args));
   printf("xs_verify_args %zu\n", sizeof(xs_verify_args));
   printf("xs_argmax_args %zu\n", sizeof(xs_argmax_args));
+  printf("xs_row_control %zu\n", sizeof(xs_row_control));
   F(xs_row_params, top_k); F(xs_row_params, top_p);
   F(xs_sample_args, params); F(xs_sample_args, allowed); F(xs_sample_args, token);
   F(xs_sample_args, cand_ld); F(xs_sample_args, n_top); F(xs_sample_args, top_ld);
   F(xs_verify_args, drafts); F(xs_verify_args, n_eog); F(xs_verify_args, eog);
   F(xs_verify_args, row_token); F(xs_verify_args, seq_status);
   F(xs_argmax_args, width); F(xs_argmax_args, ids); F(xs_argmax_args, probs);
+  F(xs_row_control, n_bias); F(xs_row_control, pull_alpha); F(xs_row_control, force_id);
+  F(xs_sample_args, controls); F(xs_sample_args, ctl_delta);
+  F(xs_verify_args, controls); F(xs_verify_args, ctl_delta);
   return 0;
 }
 ''')
@@ -63,8 +67,10 @@ def test_ctypes_structs_match_the_header(tmp_path):
     assert C.sizeof(_lib.SampleArgs) == c["xs_sample_args"]
     assert C.sizeof(_lib.VerifyArgs) == c["xs_verify_args"]
     assert C.sizeof(_lib.ArgmaxArgs) == c["xs_argmax_args"]
+    assert C.sizeof(_lib.RowControl) == c["xs_row_control"]
     for struct, cname in ((_lib.RowParams, "xs_row_params"), (_lib.SampleArgs, "xs_sample_args"),
-                          (_lib.VerifyArgs, "xs_verify_args"), (_lib.ArgmaxArgs, "xs_argmax_args")):
+                          (_lib.VerifyArgs, "xs_verify_args"), (_lib.ArgmaxArgs, "xs_argmax_args"),
+                          (_lib.RowControl, "xs_row_control")):
         for field, _ in struct._fields_:
             key = f"{cname}.{field}"
             if key in c:

@@ -56,26 +56,35 @@ def dev(x):
 
 
 def run_sample(ctx, logits, T, K, P, U, *, enc=None, width=None, mask=None, mask_words=None,
-               cand_k=128, n_top=0):
+               cand_k=128, n_top=0, ctls=None):
+    """One xs_sample call; `ctls` is one SampleControl (sparse part) or None per row."""
     from xwen_amd import sampler as xsm
     rows = logits.shape[0]
     lg = dev(np.asarray(logits, np.float32))
     p = xsm.params_tensor(T, K, P, rows, "cuda")
     u = dev(np.broadcast_to(np.asarray(U, np.float32), (rows,)).copy())
     m = None if mask is None else dev(np.asarray(mask, np.uint32).view(np.int32))
+    controls = None if ctls is None else xsm.controls_tensor(ctls, "cuda")
     out = xsm.sample_batch(ctx, lg, p, u, enc=enc, width=width, allowed=m,
-                           allowed_words=mask_words, cand_k=cand_k, stats=True, n_top=n_top)
+                           allowed_words=mask_words, cand_k=cand_k, stats=True, n_top=n_top,
+                           controls=controls)
     torch.cuda.synchronize()
     return {k: (None if v is None else v.cpu().numpy()) for k, v in vars(out).items()}
 
 
-def oracle_row(oracle, row, enc, T, k, p, u, mask_row=None, **kw):
-    ctl = oracle.Ctl(allowed=mask_row) if mask_row is not None else None
-    return oracle.sample_controlled(row, enc, float(T), int(k), float(p), u=float(u), ctl=ctl, **kw)
+def oracle_row(oracle, row, enc, T, k, p, u, mask_row=None, ctl=None, **kw):
+    octl = None
+    if mask_row is not None or ctl is not None:
+        octl = oracle.Ctl(allowed=mask_row)
+        if ctl is not None:
+            octl.banned, octl.bias = tuple(ctl.banned), tuple(ctl.bias)
+            octl.pull, octl.force = ctl.pull, ctl.force
+    return oracle.sample_controlled(row, enc, float(T), int(k), float(p), u=float(u), ctl=octl,
+                                    **kw)
 
 
 def check_rows(oracle, logits, T, K, P, U, d, *, enc=None, mask=None, rows=None, margins=True,
-               label=""):
+               label="", ctls=None):
     """Compare device outputs `d` with the oracle row by row; returns the count of
     rows whose serial-f32 decision margin fell below MARGIN_EPS."""
     n_rows, width = logits.shape
@@ -87,16 +96,17 @@ def check_rows(oracle, logits, T, K, P, U, d, *, enc=None, mask=None, rows=None,
     thin = 0
     for r in (range(n_rows) if rows is None else rows):
         mrow = None if mask is None else mask[r]
+        kw = {} if ctls is None else {"ctl": ctls[r]}
         greedy = T[r] <= 0.0 or K[r] <= 1
         tag = f"{label} row {r} T={T[r]} k={K[r]} p={P[r]}"
         if greedy:
-            o = oracle_row(oracle, logits[r], enc, T[r], K[r], P[r], U[r], mrow)
+            o = oracle_row(oracle, logits[r], enc, T[r], K[r], P[r], U[r], mrow, **kw)
             assert (d["status"][r], d["token"][r] if o.status == 0 else -1) == \
                 (o.status, o.token if o.status == 0 else -1), tag
             continue
         S = np.float32(d["soft_sum"][r])
         o = oracle_row(oracle, logits[r], enc, T[r], K[r], P[r], U[r], mrow,
-                       sum_mode=oracle.SUM_GIVEN, s_given=S)
+                       sum_mode=oracle.SUM_GIVEN, s_given=S, **kw)
         assert d["status"][r] == o.status, (tag, d["status"][r], o.status)
         if o.status != 0:
             continue
@@ -112,13 +122,13 @@ def check_rows(oracle, logits, T, K, P, U, d, *, enc=None, mask=None, rows=None,
         assert np.float32(d["soft_max"][r]) == np.float32(o.smax), tag
         # the denominator against the exact sum of the same correctly rounded terms
         o64 = oracle_row(oracle, logits[r], enc, T[r], K[r], P[r], U[r], mrow,
-                         sum_mode=oracle.SUM_F64)
+                         sum_mode=oracle.SUM_F64, **kw)
         rel = abs(float(S) - float(o64.ssum)) / float(o64.ssum)
         WORST["denominator"] = max(WORST.get("denominator", 0.0), rel)
         assert rel <= DENOM_RTOL, (tag, float(S), o64.ssum, rel)
         if margins:
             oseq = oracle_row(oracle, logits[r], enc, T[r], K[r], P[r], U[r], mrow,
-                              sum_mode=oracle.SUM_SEQ_F32, margins=True)
+                              sum_mode=oracle.SUM_SEQ_F32, margins=True, **kw)
             margin = min(oseq.margin_order, oseq.margin_cut, oseq.margin_draw)
             if margin > MARGIN_EPS:
                 assert oseq.token == d["token"][r], (tag, "serial-f32 order", margin)
@@ -252,13 +262,19 @@ def _pad(values, ld=None):
 UNIFORMS = [0.0, 0.25, 0.5, 0.75, 1.0 - 2.0 ** -23, 0.123456789]
 
 
-def test_reference_cases_without_sparse_controls(ctx, golden):
+def test_reference_cases(ctx, golden):
+    """Every sampler known answer the reference's tests hold, controls included."""
+    from xwen_amd import sampler as xsm
     names = {"NAN": 1, "NO_FINITE": 2, "MASK_SHORT": 3, "FORCE_OOR": 4, "ZERO_WEIGHT": 5,
              "NARROW": 6}
     ran = 0
     for case in golden["sampler"]:
+        ctls = None
         if any(k in case for k in ("banned", "bias", "pull", "force")):
-            continue  # sparse SampleControl entries are not on the device path yet
+            ctls = [xsm.SampleControl(banned=case.get("banned", ()),
+                                      bias=[tuple(b) for b in case.get("bias", ())],
+                                      pull=tuple(case["pull"]) if "pull" in case else None,
+                                      force=case.get("force"))]
         vals = case["logits"]
         width = len(vals)
         enc = case["enc"]
@@ -269,7 +285,8 @@ def test_reference_cases_without_sparse_controls(ctx, golden):
         us = UNIFORMS if case.get("any_uniform") or "expect_in" in case else [0.5]
         for u in us:
             d = run_sample(ctx, row[None, :], case["T"], case["k"], case["p"], u, enc=enc,
-                           width=width, mask=mask, mask_words=None if mask is None else mask.shape[1])
+                           width=width, mask=mask, mask_words=None if mask is None else mask.shape[1],
+                           ctls=ctls)
             tag = (case["name"], u, int(d["status"][0]), int(d["token"][0]))
             if "expect_error" in case:
                 assert d["status"][0] == names[case["expect_error"]], tag
@@ -278,7 +295,7 @@ def test_reference_cases_without_sparse_controls(ctx, golden):
             else:
                 assert d["status"][0] == 0 and d["token"][0] in case["expect_in"], tag
         ran += 1
-    assert ran >= 10
+    assert ran >= 28
 
 
 def test_wide_nan_errors_on_both_paths(ctx, golden):

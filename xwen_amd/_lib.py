@@ -19,6 +19,7 @@ ROW_OK, ROW_NAN, ROW_NO_FINITE, ROW_MASK_SHORT, ROW_FORCE_OOR, ROW_ZERO_WEIGHT, 
     ROW_BAD_PARAM, ROW_INTERNAL = range(9)
 K_MAX = 127
 TOP_MAX = 128
+CTL_MAX = 2048
 
 _vp = C.c_void_p
 _i64 = C.c_int64
@@ -31,6 +32,14 @@ class RowParams(C.Structure):
     _fields_ = [("temperature", C.c_double), ("top_k", _i32), ("top_p", C.c_float)]
 
 
+class RowControl(C.Structure):
+    """xs_row_control: SampleControl's bans, biases, pull and force (sampler.rs:85-121)."""
+
+    _fields_ = [("ban_off", _i32), ("n_ban", _i32), ("bias_off", _i32), ("n_bias", _i32),
+                ("has_pull", _i32), ("pull_id", C.c_uint32), ("pull_alpha", C.c_float),
+                ("has_force", _i32), ("force_id", C.c_uint32)]
+
+
 class SampleArgs(C.Structure):
     _fields_ = [
         ("logits", _vp), ("rows", _i64), ("ld", _i64), ("width", _i64), ("enc", _i64),
@@ -40,6 +49,7 @@ class SampleArgs(C.Structure):
         ("cand_ld", _i64), ("soft_max", _vp), ("soft_sum", _vp),
         ("row_max", _vp), ("row_lse", _vp), ("n_top", _i32), ("top_id", _vp),
         ("top_logprob", _vp), ("top_ld", _i64),
+        ("controls", _vp), ("ctl_ids", _vp), ("ctl_delta", _vp),
     ]
 
 
@@ -51,6 +61,7 @@ class VerifyArgs(C.Structure):
         ("drafts", _vp), ("budget", _vp), ("n_eog", _i32), ("eog", _i32 * 8),
         ("row_token", _vp), ("row_status", _vp), ("accepted", _vp), ("committed", _vp),
         ("n_committed", _vp), ("seq_status", _vp),
+        ("controls", _vp), ("ctl_ids", _vp), ("ctl_delta", _vp),
     ]
 
 

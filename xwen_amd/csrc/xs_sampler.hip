@@ -310,6 +310,20 @@ XS_DEV Cfg greedy_cfg() {
 // finalize_kernel, launched after it on the same stream, reads them.  The
 // kernel boundary is the hand-off: no atomics, no flags, no fences.
 
+// What control_kernel leaves for the other kernels about one row's sparse
+// controls (the bans and biases themselves become the row's patch list).
+struct CtlRow {
+  int32_t active;     // the row has a ban, bias, pull or force
+  int32_t status;     // XS_ROW_OK, XS_ROW_FORCE_OOR or XS_ROW_BAD_PARAM
+  int32_t n_patch;    // entries of the row's patch list
+  int32_t pull_id;    // the pulled id with its new value, or -1
+  float pull_val;
+  int32_t force_id;   // the forced id with its final value, or -1
+  float force_val;
+  int32_t pad;
+};
+constexpr int CTL_MAX = XS_CTL_MAX;
+
 struct Args {
   const float* logits;
   int64_t ld, enc;
@@ -345,6 +359,16 @@ struct Args {
   // 1 / sum exp(v - max) over the raw row
   int32_t greedy_all;
   float* p_max;
+  // sparse controls (controls == nullptr: none) and what control_kernel makes
+  // of them: per row a patch list of (id << 32 | final value bits) sorted by id,
+  // CTL_MAX entries apart, and the first patch of every chunk (n_chunks + 1
+  // offsets per row)
+  const xs_row_control* controls;
+  const uint32_t* ctl_ids;
+  const float* ctl_delta;
+  uint64_t* patch;
+  CtlRow* ctl_row;
+  int32_t* ctl_chunk;
   // geometry + workspace
   int32_t n_chunks, nslots;
   uint64_t* rec;     // [rows, SRECW, nsp]: word i of sub-record s of a row at i * nsp + s
@@ -879,9 +903,10 @@ XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, int nsub, const uin
 // EPRE, and the id-ordered scan for probability ties at the top-k boundary.
 // Lane l handles sub-records l + 64g.  Out of line: it is rare, and inlined
 // it would cost the streaming path registers.
-template <bool HAS_MASK, bool WANT_LSE>
+template <bool HAS_MASK, bool WANT_LSE, bool HAS_CTL>
 XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* rowrec,
-                        int nsp, int nsub, const float* rowp, const uint32_t* mrow, FinLds& F) {
+                        int nsp, int nsub, const float* rowp, const uint32_t* mrow, const CtlRow& cr,
+                        FinLds& F) {
   const int lane = lane_id();
   const int kp = cfg.kp, enc = (int)a.enc;
   const bool stoch = !cfg.greedy && !cfg.bad;
@@ -933,9 +958,13 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
   const bool nan_seen = fl & 1u;
   const bool finite_seen = fl & 2u;
 
+  // A controlled row (mask or sparse controls) errors when nothing finite is
+  // left (sampler.rs:483-488); a forced row always keeps its target.
+  const bool ctl_on = HAS_CTL && cr.active;
   int st = XS_ROW_OK;
-  if (cfg.bad) st = XS_ROW_BAD_PARAM;
-  else if (HAS_MASK && !finite_seen) st = XS_ROW_NO_FINITE;
+  if (ctl_on && cr.status != XS_ROW_OK) st = cr.status;
+  else if (cfg.bad) st = XS_ROW_BAD_PARAM;
+  else if ((HAS_MASK || ctl_on) && !finite_seen) st = XS_ROW_NO_FINITE;
   else if (cfg.greedy) st = nan_seen ? XS_ROW_NAN : (m_v == -INFINITY ? XS_ROW_NO_FINITE : XS_ROW_OK);
   else if (nan_seen || __builtin_isinf(m_s)) st = XS_ROW_NAN;
 
@@ -1137,18 +1166,47 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
         const float x_lo = elo > 0x1p-100 ? (float)(log(elo) - 0x1p-8) : -INFINITY;
         const float x_hi = (float)(log(ehi) + 0x1p-8);
         int need = k - g, have = g;
+        int sc = 0;  // next patch (the list is sorted by id, as the scan runs)
+        const uint64_t* pl = HAS_CTL ? a.patch + (int64_t)row * CTL_MAX : nullptr;
         for (int base = 0; base < enc && need > 0; base += 256) {
           const int f = base / 4 + lane;
           float4 qv = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
           if (4 * f < enc) qv = reinterpret_cast<const float4*>(rowp)[f];
-          const float xv[4] = {qv.x, qv.y, qv.z, qv.w};
+          float xv[4] = {qv.x, qv.y, qv.z, qv.w};
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const int id = 4 * f + e;
+            if (HAS_MASK && id < enc && !((mrow[id >> 5] >> (id & 31)) & 1u)) xv[e] = -INFINITY;
+          }
+          if (ctl_on) {  // the controlled values, as chunk_kernel saw them
+            if (cr.force_id >= 0) {
+#pragma unroll
+              for (int e = 0; e < 4; e++) xv[e] = (4 * f + e == cr.force_id) ? cr.force_val : -INFINITY;
+            } else {
+              while (sc < cr.n_patch) {
+                const uint64_t pe = pl[sc];
+                const int off = (int)(uint32_t)(pe >> 32) - base;
+                if (off >= 256) break;
+                if ((off >> 2) == lane) {
+                  const float pv = __uint_as_float((uint32_t)pe);
+#pragma unroll
+                  for (int e = 0; e < 4; e++) xv[e] = ((off & 3) == e) ? pv : xv[e];
+                }
+                sc++;
+              }
+              const int pt = cr.pull_id - base;
+              if (pt >= 0 && pt < 256 && (pt >> 2) == lane) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) xv[e] = ((pt & 3) == e) ? cr.pull_val : xv[e];
+              }
+            }
+          }
           bool hit[4];
           int c = 0;
 #pragma unroll
           for (int e = 0; e < 4; e++) {
             const int id = 4 * f + e;
-            float x = xv[e];
-            if (HAS_MASK && id < enc && !((mrow[id >> 5] >> (id & 31)) & 1u)) x = -INFINITY;
+            const float x = xv[e];
             hit[e] = false;
             if (id < enc) {
               const float sx = cfg.scale ? x * cfg.inv : x;
@@ -1315,7 +1373,7 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
 // the chunk and publishes it as one sub-record; the row's last wave (atomic
 // ticket over all of the row's waves) finalizes the row.
 
-template <bool HAS_MASK, bool WANT_LSE>
+template <bool HAS_MASK, bool WANT_LSE, bool HAS_CTL>
 __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) void chunk_kernel(Args a) {
   __shared__ ChunkLds Lc;
   const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
@@ -1348,6 +1406,21 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
   const Cfg cfg = a.greedy_all ? greedy_cfg() : make_cfg(a.params[row], a.enc, a.n_top);
   const bool stoch = !cfg.greedy && !cfg.bad;
   const int kp = cfg.kp;
+  // Sparse controls: the chunk's patches (final values written by
+  // control_kernel), the pulled id, or the forced id.
+  int pc = 0, phi = 0, ctl_pull = -1, ctl_force = -1;
+  float ctl_pval = 0.0f, ctl_fval = 0.0f;
+  const uint64_t* pl = nullptr;
+  if (HAS_CTL) {
+    const CtlRow cr = a.ctl_row[row];
+    pc = a.ctl_chunk[(int64_t)row * (nc + 1) + chunk];
+    phi = a.ctl_chunk[(int64_t)row * (nc + 1) + chunk + 1];
+    pl = a.patch + (int64_t)row * CTL_MAX;
+    ctl_pull = cr.pull_id;
+    ctl_pval = cr.pull_val;
+    ctl_force = cr.force_id;
+    ctl_fval = cr.force_val;
+  }
 
   // Online reduction, one float4 at a time, branch-free.  The softmax partial
   // is summed in the reference's scaled domain, s = v * inv rounded to f32 as
@@ -1385,6 +1458,31 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
 #pragma unroll
       for (int e = 0; e < 4; e++)
         if (j >= ns || id0 + e >= enc) x[e] = -INFINITY;
+    }
+    if (HAS_CTL) {
+      const int sb = (s0 + j) * SLOT;
+      if (ctl_force >= 0) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) x[e] = (sb + 4 * tid + e == ctl_force) ? ctl_fval : -INFINITY;
+      } else {
+        // this slot's patches: the next ones in the sorted list
+        while (pc < phi) {
+          const uint64_t pe = pl[pc];
+          const int off = (int)(uint32_t)(pe >> 32) - sb;
+          if (off >= SLOT) break;
+          if ((off >> 2) == tid) {
+            const float pv = __uint_as_float((uint32_t)pe);
+#pragma unroll
+            for (int e = 0; e < 4; e++) x[e] = ((off & 3) == e) ? pv : x[e];
+          }
+          pc++;
+        }
+        const int pt = ctl_pull - sb;
+        if (pt >= 0 && pt < SLOT && (pt >> 2) == tid) {
+#pragma unroll
+          for (int e = 0; e < 4; e++) x[e] = ((pt & 3) == e) ? ctl_pval : x[e];
+        }
+      }
     }
     q[j] = v4f{x[0], x[1], x[2], x[3]};
     gm[j] = vmax(vmax3(x[0], x[1], x[2]), x[3]);
@@ -1464,7 +1562,7 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
     R = red_sumd((racc != 0.0) ? racc * (double)xexp2((rc - m_w) * LOG2E) : racc);
   }
   const float c_r = m_w;
-  if (HAS_MASK) {
+  if (HAS_MASK || HAS_CTL) {
     if (__builtin_isfinite(m_w)) {
       flags |= 2u;
     } else if (m_w == INFINITY) {
@@ -1581,7 +1679,7 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
 // speculative block the workgroup then walks its sequence (accept_drafts).
 constexpr int FWAVES = 8;
 
-template <bool HAS_MASK, bool WANT_LSE>
+template <bool HAS_MASK, bool WANT_LSE, bool HAS_CTL>
 __global__ __launch_bounds__(64 * FWAVES) void finalize_kernel(Args a) {
   __shared__ FinLds Fw[FWAVES];
   const int lane = lane_id(), wave = wave_id();
@@ -1603,9 +1701,11 @@ __global__ __launch_bounds__(64 * FWAVES) void finalize_kernel(Args a) {
     const Cfg cfg = a.greedy_all ? greedy_cfg() : make_cfg(a.params[row], a.enc, a.n_top);
     const float* rowp = a.logits + (int64_t)row * a.ld;
     const uint32_t* mrow = HAS_MASK ? a.allowed + (int64_t)row * a.allowed_ld : nullptr;
-    const bool done = nsub <= 64 && cfg.kp <= 64 && !cfg.bad &&
+    CtlRow cr{};
+    if (HAS_CTL) cr = a.ctl_row[row];
+    const bool done = !(HAS_CTL && cr.active) && nsub <= 64 && cfg.kp <= 64 && !cfg.bad &&
                       fin_fast<HAS_MASK, WANT_LSE>(a, cfg, row, nsub, h, E, Fw[wave]);
-    if (!done) fin_general<HAS_MASK, WANT_LSE>(a, cfg, row, rowrec, nsp, nsub, rowp, mrow, Fw[wave]);
+    if (!done) fin_general<HAS_MASK, WANT_LSE, HAS_CTL>(a, cfg, row, rowrec, nsp, nsub, rowp, mrow, cr, Fw[wave]);
   }
   (void)lane;
 
@@ -1636,6 +1736,162 @@ __global__ __launch_bounds__(64 * FWAVES) void finalize_kernel(Args a) {
       a.seq_status[seq] = sst;
     }
   }
+}
+
+// ---------------------------------------------------------------------------
+// Sparse controls (apply_control, sampler.rs:433-490): one workgroup per row,
+// launched before chunk_kernel when a call carries controls.  The row's bans
+// and biases become its patch list: every distinct listed id < enc with its
+// value after the mask, the bans (sampler.rs:450-454) and then the biases in
+// list order (:455-459).  A pull needs the row max after those (:460-470): the
+// workgroup reads the row once for it, and only for a finite target, and keeps
+// the target's new value.  A force keeps the target's final value (:471-482).
+// chunk_kernel overwrites exactly these elements before anything reads them.
+template <bool HAS_MASK>
+__global__ __launch_bounds__(BLOCK) void control_kernel(Args a) {
+  __shared__ uint64_t keys[CTL_MAX];  // (id << 32 | list position), sorted
+  __shared__ uint64_t pl[CTL_MAX];    // the patch list
+  __shared__ int s4[NWAVE];
+  __shared__ float wmax[NWAVE];
+  const int row = blockIdx.x, tid = threadIdx.x, lane = lane_id(), wave = wave_id();
+  const xs_row_control c = a.controls[row];
+  const int enc = (int)a.enc, nc = a.n_chunks;
+  const float* rowp = a.logits + (int64_t)row * a.ld;
+  const uint32_t* mrow = HAS_MASK ? a.allowed + (int64_t)row * a.allowed_ld : nullptr;
+  int32_t* cb = a.ctl_chunk + (int64_t)row * (nc + 1);
+  uint64_t* patch = a.patch + (int64_t)row * CTL_MAX;
+  auto allowed = [&](int id) __attribute__((always_inline)) {
+    return !HAS_MASK || ((mrow[id >> 5] >> (id & 31)) & 1u);
+  };
+  const bool active = c.n_ban != 0 || c.n_bias != 0 || c.has_pull != 0 || c.has_force != 0;
+  const int64_t n64 = (int64_t)c.n_ban + (int64_t)c.n_bias;
+  int status = XS_ROW_OK;
+  if (c.n_ban < 0 || c.n_bias < 0 || c.ban_off < 0 || c.bias_off < 0 || n64 > CTL_MAX ||
+      (n64 > 0 && !a.ctl_ids) || (c.n_bias > 0 && !a.ctl_delta))
+    status = XS_ROW_BAD_PARAM;
+  if (!active || status != XS_ROW_OK) {
+    for (int i = tid; i <= nc; i += BLOCK) cb[i] = 0;
+    if (tid == 0) a.ctl_row[row] = CtlRow{active ? 1 : 0, status, 0, -1, 0.0f, -1, 0.0f, 0};
+    return;
+  }
+
+  // Sort the listed ids, each tagged with its list position (bans first).
+  const int n = (int)n64;
+  int np2 = 1;
+  while (np2 < n) np2 <<= 1;
+  for (int i = tid; i < np2; i += BLOCK) {
+    uint64_t k = ~0ull;
+    if (i < n) {
+      const uint32_t id = i < c.n_ban ? a.ctl_ids[c.ban_off + i] : a.ctl_ids[c.bias_off + (i - c.n_ban)];
+      k = ((uint64_t)id << 32) | (uint32_t)i;
+    }
+    keys[i] = k;
+  }
+  __syncthreads();
+  for (int size = 2; size <= np2; size <<= 1) {  // bitonic, ascending
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = tid; i < np2 / 2; i += BLOCK) {
+        const int lo = 2 * i - (i & (stride - 1)), hi = lo + stride;
+        const bool asc = (lo & size) == 0;
+        const uint64_t x = keys[lo], y = keys[hi];
+        if ((x > y) == asc) {
+          keys[lo] = y;
+          keys[hi] = x;
+        }
+      }
+      __syncthreads();
+    }
+  }
+
+  // One patch per distinct id < enc: the run of its entries holds its bans
+  // (lower positions) and then its biases in list order.
+  const int seg = (n + BLOCK - 1) / BLOCK;
+  const int b0 = min(n, tid * seg), b1 = min(n, b0 + seg);
+  auto starts = [&](int i) __attribute__((always_inline)) {
+    const uint32_t id = (uint32_t)(keys[i] >> 32);
+    return id < (uint32_t)enc && (i == 0 || (uint32_t)(keys[i - 1] >> 32) != id);
+  };
+  int cnt = 0;
+  for (int i = b0; i < b1; i++) cnt += starts(i) ? 1 : 0;
+  int total;
+  int p = block_excl_scan(cnt, s4, &total);
+  for (int i = b0; i < b1; i++) {
+    if (!starts(i)) continue;
+    const uint32_t id = (uint32_t)(keys[i] >> 32);
+    float x = allowed((int)id) ? rowp[id] : -INFINITY;
+    for (int j = i; j < n && (uint32_t)(keys[j] >> 32) == id; j++) {
+      const int o = (int)(uint32_t)keys[j];
+      if (o < c.n_ban) x = -INFINITY;
+      else x = x + a.ctl_delta[c.bias_off + (o - c.n_ban)];
+    }
+    pl[p++] = ((uint64_t)id << 32) | __float_as_uint(x);
+  }
+  __syncthreads();
+  auto lower = [&](uint32_t v) __attribute__((always_inline)) {  // first patch with id >= v
+    int lo = 0, hi = total;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if ((uint32_t)(pl[mid] >> 32) < v) lo = mid + 1;
+      else hi = mid;
+    }
+    return lo;
+  };
+  auto patched = [&](int id) __attribute__((always_inline)) {
+    const int q = lower((uint32_t)id);
+    return q < total && (uint32_t)(pl[q] >> 32) == (uint32_t)id;
+  };
+  for (int i = tid; i < total; i += BLOCK) patch[i] = pl[i];
+  for (int i = tid; i <= nc; i += BLOCK) cb[i] = (i == nc) ? total : lower((uint32_t)(i * SPC * SLOT));
+
+  // pull: the max M over the row after the bans and biases (f32::max folds
+  // skip NaN; so does every `>` test here), then v += alpha * max(0, M - v)
+  int pull_id = -1;
+  float pull_val = 0.0f;
+  if (c.has_pull && c.pull_id < (uint32_t)enc) {
+    const int t = (int)c.pull_id;
+    const float vt = patched(t) ? __uint_as_float((uint32_t)pl[lower((uint32_t)t)])
+                                : (allowed(t) ? rowp[t] : -INFINITY);
+    if (__builtin_isfinite(vt)) {
+      float best = -INFINITY;
+      const v4f* r4 = reinterpret_cast<const v4f*>(rowp);
+      for (int f = tid; 4 * f < enc; f += BLOCK) {
+        const v4f q = r4[f];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const int id = 4 * f + e;
+          const float x = q4(q, e);
+          if (id < enc && x > best && allowed(id) && !patched(id)) best = x;
+        }
+      }
+      for (int i = tid; i < total; i += BLOCK) {
+        const float v = __uint_as_float((uint32_t)pl[i]);
+        if (v > best) best = v;
+      }
+      best = wave_maxf(best);
+      if (lane == 0) wmax[wave] = best;
+      __syncthreads();
+      float M = wmax[0];
+      for (int w = 1; w < NWAVE; w++) M = wmax[w] > M ? wmax[w] : M;
+      pull_val = vt + c.pull_alpha * fmaxf(M - vt, 0.0f);
+      pull_id = t;
+    }
+  }
+  // force: the target keeps its final value if finite, else 0
+  int force_id = -1;
+  float force_val = 0.0f;
+  if (c.has_force) {
+    if (c.force_id >= (uint32_t)enc) {
+      status = XS_ROW_FORCE_OOR;
+    } else {
+      const int t = (int)c.force_id;
+      const float v = t == pull_id ? pull_val
+                                   : (patched(t) ? __uint_as_float((uint32_t)pl[lower((uint32_t)t)])
+                                                 : (allowed(t) ? rowp[t] : -INFINITY));
+      force_val = __builtin_isfinite(v) ? v : 0.0f;
+      force_id = t;
+    }
+  }
+  if (tid == 0) a.ctl_row[row] = CtlRow{1, status, total, pull_id, pull_val, force_id, force_val, 0};
 }
 
 // Fills every row's status with one data error (a call-level condition such as
@@ -1680,6 +1936,9 @@ struct xs_context {
   int32_t max_chunks;
   uint64_t* rec;
   int32_t* row_status;  // [max_rows] statuses of calls whose caller takes none (xs_argmax_probs)
+  uint64_t* ctl_patch;  // [max_rows, CTL_MAX] patch lists of controlled calls
+  xs::CtlRow* ctl_row;  // [max_rows]
+  int32_t* ctl_chunk;   // [max_rows, max_chunks + 1]
 };
 
 namespace {
@@ -1714,22 +1973,30 @@ int check_common(xs_context* ctx, const Call& c) {
 }
 
 // chunk_kernel over rows x n_chunks workgroups, then finalize_kernel with one
-// workgroup per sequence of `span` rows (span 1: a plain batch).
-template <bool M, bool S>
-void launch2(xs_context* ctx, xs::Args& a, dim3 g1, dim3 g2, dim3 b2) {
-  hipLaunchKernelGGL((xs::chunk_kernel<M, S>), g1, dim3(xs::BLOCK), 0, ctx->stream, a);
-  hipLaunchKernelGGL((xs::finalize_kernel<M, S>), g2, b2, 0, ctx->stream, a);
+// workgroup per sequence of `span` rows (span 1: a plain batch); a call with
+// sparse controls runs control_kernel (one workgroup per row) first.
+template <bool M, bool S, bool C>
+void launch2(xs_context* ctx, xs::Args& a, int64_t rows, dim3 g1, dim3 g2, dim3 b2) {
+  if (C) hipLaunchKernelGGL((xs::control_kernel<M>), dim3((unsigned)rows), dim3(xs::BLOCK), 0, ctx->stream, a);
+  hipLaunchKernelGGL((xs::chunk_kernel<M, S, C>), g1, dim3(xs::BLOCK), 0, ctx->stream, a);
+  hipLaunchKernelGGL((xs::finalize_kernel<M, S, C>), g2, b2, 0, ctx->stream, a);
 }
 
 int launch(xs_context* ctx, xs::Args& a, int64_t rows, int span, bool mask, bool lse) {
+  const bool ctl = a.controls != nullptr;
   const int64_t grid = rows * (int64_t)a.n_chunks;
   if (grid == 0) return XS_OK;
   if (grid > 0x7FFFFFFF || span < 1) return XS_ERR_CAPACITY;
-  if (mask && lse) return XS_ERR_ARG;
+  if ((mask || ctl) && lse) return XS_ERR_ARG;
+  a.patch = ctx->ctl_patch;
+  a.ctl_row = ctx->ctl_row;
+  a.ctl_chunk = ctx->ctl_chunk;
   const dim3 g1((unsigned)grid), g2((unsigned)(rows / span)), b2(64 * (unsigned)std::min(span, xs::FWAVES));
-  if (mask) launch2<true, false>(ctx, a, g1, g2, b2);
-  else if (lse) launch2<false, true>(ctx, a, g1, g2, b2);
-  else launch2<false, false>(ctx, a, g1, g2, b2);
+  if (ctl && mask) launch2<true, false, true>(ctx, a, rows, g1, g2, b2);
+  else if (ctl) launch2<false, false, true>(ctx, a, rows, g1, g2, b2);
+  else if (mask) launch2<true, false, false>(ctx, a, rows, g1, g2, b2);
+  else if (lse) launch2<false, true, false>(ctx, a, rows, g1, g2, b2);
+  else launch2<false, false, false>(ctx, a, rows, g1, g2, b2);
   return hipGetLastError() == hipSuccess ? XS_OK : XS_ERR_HIP;
 }
 
@@ -1758,6 +2025,9 @@ int xs_create(int device, int64_t max_rows, int64_t vocab, int32_t k_max, xs_con
   bool ok = hipMalloc((void**)&c->rec, units * xs::SRECW * sizeof(uint64_t)) == hipSuccess;
   ok = ok && hipMemset(c->rec, 0, units * xs::SRECW * sizeof(uint64_t)) == hipSuccess;
   ok = ok && hipMalloc((void**)&c->row_status, max_rows * sizeof(int32_t)) == hipSuccess;
+  ok = ok && hipMalloc((void**)&c->ctl_patch, max_rows * xs::CTL_MAX * sizeof(uint64_t)) == hipSuccess;
+  ok = ok && hipMalloc((void**)&c->ctl_row, max_rows * sizeof(xs::CtlRow)) == hipSuccess;
+  ok = ok && hipMalloc((void**)&c->ctl_chunk, max_rows * (mc + 1) * sizeof(int32_t)) == hipSuccess;
   ok = ok && hipDeviceSynchronize() == hipSuccess;
   if (!ok) {
     xs_destroy(c);
@@ -1773,6 +2043,9 @@ int xs_destroy(xs_context* c) {
   if (c->stream) (void)hipStreamSynchronize(c->stream); else (void)hipDeviceSynchronize();
   (void)hipFree(c->rec);
   (void)hipFree(c->row_status);
+  (void)hipFree(c->ctl_patch);
+  (void)hipFree(c->ctl_row);
+  (void)hipFree(c->ctl_chunk);
   free(c);
   return XS_OK;
 }
@@ -1793,7 +2066,7 @@ int xs_sample(xs_context* ctx, const xs_sample_args* in) {
   if (in->n_top < 0 || in->n_top > XS_TOP_MAX) return XS_ERR_ARG;
   if ((in->top_id || in->top_logprob) && in->top_ld < in->n_top) return XS_ERR_ARG;
   const bool lse = in->row_max || in->row_lse || in->top_id || in->top_logprob;
-  if (lse && in->allowed) return XS_ERR_ARG;
+  if (lse && (in->allowed || in->controls)) return XS_ERR_ARG;
   if (hipSetDevice(ctx->device) != hipSuccess) return XS_ERR_HIP;
   int32_t data_err = XS_ROW_OK;
   if (in->width < in->enc) data_err = XS_ROW_NARROW;
@@ -1828,6 +2101,9 @@ int xs_sample(xs_context* ctx, const xs_sample_args* in) {
   a.top_id = in->top_id;
   a.top_logprob = in->top_logprob;
   a.top_ld = in->top_ld;
+  a.controls = in->controls;
+  a.ctl_ids = in->ctl_ids;
+  a.ctl_delta = in->ctl_delta;
   a.span = 0;
   a.n_chunks = chunks_for(in->enc);
   a.nslots = (int32_t)slots_for(in->enc);
@@ -1876,6 +2152,9 @@ int xs_verify(xs_context* ctx, const xs_verify_args* in) {
   a.committed = in->committed;
   a.n_committed = in->n_committed;
   a.seq_status = in->seq_status;
+  a.controls = in->controls;
+  a.ctl_ids = in->ctl_ids;
+  a.ctl_delta = in->ctl_delta;
   a.n_chunks = chunks_for(in->enc);
   a.nslots = (int32_t)slots_for(in->enc);
   a.rec = ctx->rec;

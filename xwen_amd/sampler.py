@@ -3,7 +3,9 @@
 Names, argument meaning and error behaviour follow the reference:
 
   SamplerOptions / recommended      src/sampler.rs:36-71
-  SampleControl (allowed mask)      src/sampler.rs:85-121
+  SampleControl (mask, bans, bias,
+  pull, force)                      src/sampler.rs:85-121, :433-490
+  draft_argmax_probs                src/generate.rs:4059-4087
   Sampler.new / sample /
   sample_masked / sample_controlled src/sampler.rs:123-232
   Sampler.is_eog / eog_ids /
@@ -42,7 +44,8 @@ ROW_STATUS_NAMES = {
     _lib.ROW_FORCE_OOR: "forced token id is outside the vocabulary",
     _lib.ROW_ZERO_WEIGHT: "no candidate carries any probability mass after top-k/top-p filtering",
     _lib.ROW_NARROW: "logit row is narrower than the encodable ids the sampler draws over",
-    _lib.ROW_BAD_PARAM: "top_k exceeds the sampler context's k_max",
+    _lib.ROW_BAD_PARAM: "top_k exceeds the sampler context's k_max, or a control list "
+                        "holds more than XS_CTL_MAX entries",
     _lib.ROW_INTERNAL: "device hand-off read an incomplete record (internal error)",
 }
 
@@ -79,10 +82,64 @@ class SamplerOptions:
 
 @dataclass
 class SampleControl:
-    """SampleControl (sampler.rs:85-121).  `allowed` is a packed u32 allow-mask per
-    row on the GPU ([rows, words], bit t%32 of word t/32), or None."""
+    """SampleControl (sampler.rs:85-121), applied in the reference's order:
+    allowed -> banned -> bias -> pull -> force (apply_control, sampler.rs:433-490).
+
+    `allowed` is a packed u32 allow-mask per row on the GPU ([rows, words], bit
+    t%32 of word t/32), or None.  `banned` is a list of ids, `bias` a list of
+    (id, delta), `pull` an (id, alpha) pair or None, `force` an id or None; the
+    same sparse controls apply to every row of the call."""
 
     allowed: object = None
+    banned: tuple = ()
+    bias: tuple = ()
+    pull: object = None
+    force: object = None
+
+    def is_noop(self) -> bool:
+        return (self.allowed is None and not self.banned and not self.bias
+                and self.pull is None and self.force is None)
+
+    def has_sparse(self) -> bool:
+        return bool(self.banned) or bool(self.bias) or self.pull is not None \
+            or self.force is not None
+
+
+@dataclass
+class Controls:
+    """Device form of per-row sparse controls: xs_row_control [rows] plus the id
+    and delta pools its offsets index."""
+
+    rows: object
+    ids: object
+    delta: object
+
+
+def controls_tensor(per_row, device) -> Controls:
+    """Pack one SampleControl-like object (or None) per row into the xs_row_control
+    array and the shared id / delta pools (device tensors)."""
+    torch = _torch()
+    n = len(per_row)
+    arr = (_lib.RowControl * max(n, 1))()
+    ids, delta = [], []
+    for r, c in enumerate(per_row):
+        if c is None:
+            continue
+        rc = arr[r]
+        rc.ban_off, rc.n_ban = len(ids), len(c.banned)
+        ids += [int(i) for i in c.banned]
+        delta += [0.0] * len(c.banned)
+        rc.bias_off, rc.n_bias = len(ids), len(c.bias)
+        ids += [int(i) for i, _ in c.bias]
+        delta += [float(d) for _, d in c.bias]
+        if c.pull is not None:
+            rc.has_pull, rc.pull_id, rc.pull_alpha = 1, int(c.pull[0]), float(c.pull[1])
+        if c.force is not None:
+            rc.has_force, rc.force_id = 1, int(c.force)
+    raw = np.frombuffer(bytes(arr), dtype=np.uint8)[: n * C.sizeof(_lib.RowControl)].copy()
+    ids_t = torch.from_numpy(np.asarray(ids + [0], np.uint32).view(np.int32)).to(device)
+    delta_t = torch.from_numpy(np.asarray(delta + [0.0], np.float32)).to(device)
+    return Controls(rows=torch.from_numpy(raw).to(device), ids=ids_t, delta=delta_t)
 
 
 def _torch():
@@ -155,7 +212,7 @@ class Draws:
 def sample_batch(ctx: Context, logits, params, uniforms, *, enc: int | None = None,
                  width: int | None = None, allowed=None, allowed_words: int | None = None,
                  cand_k: int = 0, stats: bool = False, n_top: int = 0, out: Draws | None = None,
-                 check: bool = True) -> Draws:
+                 controls: Controls | None = None, check: bool = True) -> Draws:
     """One xs_sample call.  logits: float32 [rows, ld] CUDA tensor (ld % 4 == 0);
     params: the uint8 tensor from params_tensor; uniforms: float32 [rows]."""
     torch = _torch()
@@ -204,6 +261,10 @@ def sample_batch(ctx: Context, logits, params, uniforms, *, enc: int | None = No
         a.top_id = out.top_id.data_ptr()
         a.top_logprob = out.top_logprob.data_ptr()
         a.top_ld = out.top_id.shape[1]
+    if controls is not None:
+        a.controls = controls.rows.data_ptr()
+        a.ctl_ids = controls.ids.data_ptr()
+        a.ctl_delta = controls.delta.data_ptr()
     rc = ctx.lib.xs_sample(ctx.h, C.byref(a))
     if check:
         _lib.check(rc, "xs_sample")
@@ -222,7 +283,7 @@ class Verdict:
 
 def verify_batch(ctx: Context, logits, seqs: int, span: int, params, uniforms, drafts, *,
                  budget=None, eog=(), enc: int | None = None, allowed=None,
-                 out: Verdict | None = None) -> Verdict:
+                 controls: Controls | None = None, out: Verdict | None = None) -> Verdict:
     """One xs_verify call over logits [seqs*span, ld]; drafts int32 [seqs, span-1]."""
     torch = _torch()
     rows, ld = logits.shape
@@ -256,6 +317,10 @@ def verify_batch(ctx: Context, logits, seqs: int, span: int, params, uniforms, d
     a.committed = out.committed.data_ptr()
     a.n_committed = out.n_committed.data_ptr()
     a.seq_status = out.seq_status.data_ptr()
+    if controls is not None:
+        a.controls = controls.rows.data_ptr()
+        a.ctl_ids = controls.ids.data_ptr()
+        a.ctl_delta = controls.delta.data_ptr()
     _lib.check(ctx.lib.xs_verify(ctx.h, C.byref(a)), "xs_verify")
     return out
 
@@ -307,9 +372,12 @@ class Sampler:
         p = params_tensor(self.opts.temperature, self.opts.top_k, self.opts.top_p, rows,
                           logits.device)
         allowed = None if ctl is None else ctl.allowed
+        controls = None
+        if ctl is not None and ctl.has_sparse():
+            controls = controls_tensor([ctl] * rows, logits.device)
         self.ctx.bind_current_stream()
         out = sample_batch(self.ctx, logits, p, u, enc=self.encodable_, width=width,
-                           allowed=allowed)
+                           allowed=allowed, controls=controls)
         st = out.status.cpu().numpy()
         if st.any():
             raise SampleError(st)

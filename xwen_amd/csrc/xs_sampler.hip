@@ -306,9 +306,9 @@ XS_DEV Cfg greedy_cfg() {
 // ---------------------------------------------------------------------------
 // Workspace and launch arguments.
 //
-// chunk_kernel writes one sub-record per wave into the workspace;
-// finalize_kernel, launched after it on the same stream, reads them.  The
-// kernel boundary is the hand-off: no atomics, no flags, no fences.
+// chunk_kernel writes one sub-record per wave into the workspace with
+// agent-scope stores; the row's last workgroup (arrival ticket) reads them
+// back with agent-scope loads and finalizes the row in the same launch.
 
 // What control_kernel leaves for the other kernels about one row's sparse
 // controls (the bans and biases themselves become the row's patch list).
@@ -370,11 +370,31 @@ struct Args {
   CtlRow* ctl_row;
   int32_t* ctl_chunk;
   // geometry + workspace
+  int32_t* row_ticket;  // [rows] workgroups of the row that have published (0 between calls)
+  int32_t* seq_ticket;  // [seqs] rows of the sequence that are finalized (0 between calls)
   int32_t n_chunks, nslots;
   uint64_t* rec;     // [rows, SRECW, nsp]: word i of sub-record s of a row at i * nsp + s
 };
 
 
+
+// Agent-scope (sc1) stores and loads: coherent across the XCDs' L2 caches
+// without the whole-L2 writeback / invalidate a __threadfence() costs.  A
+// workgroup hands its sub-records to the row's finalizing wave through them:
+// it waits for its stores to be acknowledged (drain) before it takes the
+// row's arrival ticket, and the wave that takes the last ticket reads the
+// sub-records back with agent-scope loads.
+XS_DEV void st_agent(uint64_t* p, uint64_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+XS_DEV void st_agent(int32_t* p, int32_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+XS_DEV uint64_t ld_agent(const uint64_t* p) { return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+XS_DEV int32_t ld_agent(const int32_t* p) { return __hip_atomic_load(const_cast<int32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+
+// Wait until every memory operation this wave issued has completed.
+XS_DEV void drain() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
 
 // Order this wave's LDS writes before its later LDS reads by other lanes.
 XS_DEV void wave_lds_sync() {
@@ -518,7 +538,7 @@ constexpr double LN2D = 0.693147180559945309417;
 struct ChunkLds {
   uint32_t groupmax[BLOCK / 4];     // maxima of 4-lane groups
   uint32_t lanemax[BLOCK];          // lane maxima
-  int32_t nhit[NWAVE];              // each wave's entry count (filter)
+  int32_t last;                     // this workgroup took the row's last ticket
 };
 struct FinLds {
   uint64_t list[SURV];              // gathered survivors
@@ -617,7 +637,7 @@ XS_DEV int wave_overflow(const float* rowp, const uint32_t* mrow, int s0, int ns
       const bool hit = valid(x) && fkey(x) > eq;
       const uint64_t b = __ballot(hit);
       const int pos = n + lanes_below(b);
-      if (hit && pos < CAPW) sub[(int64_t)(SHDR + pos) * nsp] = pack(fkey(x), (uint32_t)((s0 + j) * SLOT + 4 * tid + e));
+      if (hit && pos < CAPW) st_agent(&sub[(int64_t)(SHDR + pos) * nsp], pack(fkey(x), (uint32_t)((s0 + j) * SLOT + 4 * tid + e)));
       n += __popcll(b);
     }
   n = min(n, CAPW);
@@ -638,7 +658,7 @@ XS_DEV int wave_overflow(const float* rowp, const uint32_t* mrow, int s0, int ns
 #pragma unroll
     for (int e = 0; e < 4; e++)
       if (t[e]) {
-        if (pos < need && n + pos < CAPW) sub[(int64_t)(SHDR + n + pos) * nsp] = pack(eq, (uint32_t)((s0 + j) * SLOT + 4 * tid + e));
+        if (pos < need && n + pos < CAPW) st_agent(&sub[(int64_t)(SHDR + n + pos) * nsp], pack(eq, (uint32_t)((s0 + j) * SLOT + 4 * tid + e)));
         pos++;
       }
     const int tot = (int)rdl((uint32_t)incl, 63);
@@ -702,7 +722,7 @@ XS_DEV double red_sumd(double v) {
 // does the row.  Same arithmetic, in the same order, as the general path.
 template <bool HAS_MASK, bool WANT_LSE>
 XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, int nsub, const uint64_t (&h)[NHW],
-                     const uint64_t (&E)[EPRE], FinLds& F) {
+                     const uint64_t (&E)[EPRE], const uint64_t* rowrec, int nsp, FinLds& F) {
   const int lane = lane_id();
   const bool live = lane < nsub;
   const bool stoch = !cfg.greedy;
@@ -713,7 +733,7 @@ XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, int nsub, const uin
   const int cnt = live ? (int)min((uint32_t)h[4], (uint32_t)CAPW) : 0;  // clamped: never read past a sub-record
   const float m_v = red_maxf(live ? __uint_as_float((uint32_t)h[3]) : -INFINITY);
   const uint32_t fl = red_or(live ? (uint32_t)(h[3] >> 32) : 0u);
-  if (red_maxi(cnt) > EPRE) return false;
+  const int maxc = red_maxi(cnt);
   const float m_s = cfg.scale ? m_v * cfg.inv : m_v;
   double part = 0.0, rpart = 0.0;
   if (live) {
@@ -745,15 +765,24 @@ XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, int nsub, const uin
   // position is the number of survivors above it ((key, ~id) are distinct).
   const uint64_t floor_e = (uint64_t)tau << 32;
   int M = 0;
-#pragma unroll
-  for (int j = 0; j < EPRE; j++) {
-    const bool ok = j < cnt && E[j] >= floor_e;
+  auto put = [&](uint64_t e, bool ok) __attribute__((always_inline)) {
     const uint64_t b = __ballot(ok);
     if (b) {
       const int pos = M + lanes_below(b);
-      if (ok && pos < 64) F.list[pos] = E[j];
+      if (ok && pos < 64) F.list[pos] = e;
       M += __popcll(b);
     }
+  };
+#pragma unroll
+  for (int j = 0; j < EPRE; j++) put(E[j], j < cnt && E[j] >= floor_e);
+  // entries past the preloaded ones (a sub-record holding more than EPRE)
+#pragma unroll 1
+  for (int j0 = EPRE; j0 < maxc; j0 += 4) {
+    uint64_t e[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) e[u] = (j0 + u < cnt) ? ld_agent(rowrec + (int64_t)(SHDR + j0 + u) * nsp + lane) : 0ull;
+#pragma unroll
+    for (int u = 0; u < 4; u++) put(e[u], j0 + u < cnt && e[u] >= floor_e);
   }
   if (M > 64) return false;
   F.expt[lane] = et;
@@ -861,8 +890,8 @@ XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, int nsub, const uin
 
   // Outputs.
   if (lane == 0) {
-    a.token[row] = st == XS_ROW_OK ? tok : -1;
-    a.status[row] = st;
+    st_agent(&a.token[row], st == XS_ROW_OK ? tok : -1);
+    st_agent(&a.status[row], st);
     if (a.n_cand) a.n_cand[row] = (stoch && st == XS_ROW_OK) ? k : 0;
     if (a.soft_max) a.soft_max[row] = m_s;
     if (a.soft_sum) a.soft_sum[row] = S;
@@ -919,7 +948,7 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
   // common path its register budget).
   auto has = [&](int g) __attribute__((always_inline)) { return g < G && g * 64 + lane < nsub; };
   auto hdr = [&](int g, int i) __attribute__((always_inline)) -> uint64_t {
-    return has(g) ? rr[i * nsp + g * 64 + lane] : 0ull;
+    return has(g) ? ld_agent(&rr[i * nsp + g * 64 + lane]) : 0ull;
   };
 
   float mv = -INFINITY;
@@ -1032,7 +1061,7 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
     for (int j = j0; j < maxc; j += 4) {
       uint64_t e[4];
 #pragma unroll
-      for (int u = 0; u < 4; u++) e[u] = (j + u < c) ? *(rr + (int64_t)(SHDR + j + u) * nsp + s) : 0ull;
+      for (int u = 0; u < 4; u++) e[u] = (j + u < c) ? ld_agent(rr + (int64_t)(SHDR + j + u) * nsp + s) : 0ull;
 #pragma unroll
       for (int u = 0; u < 4; u++) put(e[u], j + u < c && e[u] >= fl_e);
     }
@@ -1058,7 +1087,7 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
       for (int g = 0; g < GMAX; g++) {
         const int s = g * 64 + lane;
         const int n = has(g) ? (int)min((uint32_t)hdr(g, 4), (uint32_t)CAPW) : 0;
-        for (int j = 0; j < n; j++) c += *(rr + (int64_t)(SHDR + j) * nsp + s) >= cnd ? 1 : 0;
+        for (int j = 0; j < n; j++) c += ld_agent(rr + (int64_t)(SHDR + j) * nsp + s) >= cnd ? 1 : 0;
       }
       if (wave_sumi(c) >= kp) ans = cnd;
     }
@@ -1324,8 +1353,8 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
 
   // Outputs.
   if (lane == 0) {
-    a.token[row] = st == XS_ROW_OK ? tok : -1;
-    a.status[row] = st;
+    st_agent(&a.token[row], st == XS_ROW_OK ? tok : -1);
+    st_agent(&a.status[row], st);
     if (a.n_cand) a.n_cand[row] = (stoch && st == XS_ROW_OK) ? k : 0;
     if (a.soft_max) a.soft_max[row] = m_s;
     if (a.soft_sum) a.soft_sum[row] = S;
@@ -1368,14 +1397,75 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
 }
 
 // ---------------------------------------------------------------------------
+// Row finalize, run by the first wave of the row's last workgroup: one round
+// of coalesced agent-scope loads (every header word and the first EPRE
+// entries of every sub-record), then fin_fast, or fin_general when the row
+// falls outside the common case.  For a speculative block the row then takes
+// its sequence's ticket, and the sequence's last finalized row walks it
+// (accept_drafts).
+template <bool HAS_MASK, bool WANT_LSE, bool HAS_CTL>
+XS_DEV void finalize_row(const Args& a, const Cfg& cfg, int row, const uint64_t* rowrec, int nsp,
+                         int nsub, const float* rowp, const uint32_t* mrow, FinLds& F) {
+  const int lane = lane_id();
+  uint64_t h[NHW], E[EPRE];
+  const bool live = lane < nsub;
+#pragma unroll
+  for (int i = 0; i < NHW; i++) h[i] = live ? ld_agent(&rowrec[i * nsp + lane]) : 0ull;
+#pragma unroll
+  for (int j = 0; j < EPRE; j++) E[j] = live ? ld_agent(&rowrec[(SHDR + j) * nsp + lane]) : 0ull;
+  CtlRow cr{};
+  if (HAS_CTL) cr = a.ctl_row[row];
+  const bool done = !(HAS_CTL && cr.active) && nsub <= 64 && cfg.kp <= 64 && !cfg.bad &&
+                    fin_fast<HAS_MASK, WANT_LSE>(a, cfg, row, nsub, h, E, rowrec, nsp, F);
+  if (!done) fin_general<HAS_MASK, WANT_LSE, HAS_CTL>(a, cfg, row, rowrec, nsp, nsub, rowp, mrow, cr, F);
+
+  if (a.span > 0) {
+    drain();  // this row's token and status are acknowledged
+    const int seq = row / a.span;
+    int t = 0;
+    if (lane == 0) t = __hip_atomic_fetch_add(&a.seq_ticket[seq], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    t = __builtin_amdgcn_readfirstlane(t);
+    if (t == a.span - 1 && lane == 0) {
+      st_agent(&a.seq_ticket[seq], 0);
+      // accept_drafts (generate.rs:4020-4046) over the sequence's rows
+      const int span = a.span, D = span - 1;
+      const int64_t r0 = (int64_t)seq * span;
+      const int bud = a.budget ? a.budget[seq] : 0x7FFFFFFF;
+      int mcount = 0, ncom = 0, sst = XS_ROW_OK;
+      for (int i = 0; i < span; i++) {
+        if (ncom >= bud) break;
+        const int rs = ld_agent(&a.status[r0 + i]);
+        if (rs != XS_ROW_OK) {
+          sst = rs;
+          break;
+        }
+        const int s = ld_agent(&a.token[r0 + i]);
+        const bool matched = i < D && s == a.drafts[(int64_t)seq * D + i];
+        a.committed[(int64_t)seq * span + ncom] = s;
+        ncom++;
+        if (matched) mcount++;
+        bool eog = false;
+        for (int e = 0; e < a.n_eog; e++) eog |= (s == a.eog[e]);
+        if (!matched || eog) break;
+      }
+      for (int i = ncom; i < span; i++) a.committed[(int64_t)seq * span + i] = -1;
+      a.accepted[seq] = mcount;
+      a.n_committed[seq] = ncom;
+      a.seq_status[seq] = sst;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // The kernel.  Grid: rows x n_chunks workgroups of BLOCK lanes; chunk c of a
 // row covers slots [c*SPC, c*SPC + SPC).  Every wave reduces its own share of
-// the chunk and publishes it as one sub-record; the row's last wave (atomic
-// ticket over all of the row's waves) finalizes the row.
+// the chunk and publishes it as one sub-record; the row's last workgroup to
+// arrive (an atomic ticket per row) finalizes the row with its first wave.
 
 template <bool HAS_MASK, bool WANT_LSE, bool HAS_CTL>
 __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) void chunk_kernel(Args a) {
   __shared__ ChunkLds Lc;
+  __shared__ FinLds Fl;
   const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
   const int nc = a.n_chunks;
   const int row = blockIdx.x / nc;
@@ -1587,7 +1677,6 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
     g = max(g, xor_u32(g, 2));
     if ((lane & 3) == 0) Lc.groupmax[wave * 16 + (lane >> 2)] = g;
     Lc.lanemax[tid] = km;
-    if (lane == 0) Lc.nhit[wave] = 0;
   }
   __syncthreads();
   uint32_t tk = 0;
@@ -1631,9 +1720,8 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
   }
 
   // Filter: this wave's elements at or above the bound (never -inf, never
-  // NaN), written straight into the wave's sub-record.  Only the lanes
-  // holding a hit run the inner code; an LDS counter hands out positions (the
-  // entry order is immaterial: the finalizer sorts them).
+  // NaN), written straight into the wave's sub-record, in slot order, at
+  // positions a ballot prefix hands out.
   const int nsp = ((nc * NWAVE + 63) >> 6) << 6;
   uint64_t* const rowrec = a.rec + (int64_t)row * SRECW * nsp;
   uint64_t* sub = rowrec + chunk * NWAVE + wave;
@@ -1643,99 +1731,47 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
     const float tf = (tk <= KEY_NEG_INF) ? -__FLT_MAX__ : keyf(tk);
 #pragma unroll
     for (int j = 0; j < SPC; j++) {
-      if (gm[j] >= tf) {
+      if (__ballot(gm[j] >= tf)) {
 #pragma unroll
         for (int e = 0; e < 4; e++) {
           const float x = q4(q[j], e);
-          if (x >= tf) {
-            const int pos = atomicAdd(&Lc.nhit[wave], 1);
-            if (pos < CAPW) sub[(int64_t)(SHDR + pos) * nsp] = pack(fkey(x), (uint32_t)(base_id + j * SLOT + e));
+          const bool hit = x >= tf;
+          const uint64_t b = __ballot(hit);
+          if (b) {
+            const int pos = cnt + lanes_below(b);
+            if (hit && pos < CAPW) st_agent(&sub[(int64_t)(SHDR + pos) * nsp], pack(fkey(x), (uint32_t)(base_id + j * SLOT + e)));
+            cnt += __popcll(b);
           }
         }
       }
     }
-    cnt = __hip_atomic_load(&Lc.nhit[wave], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     if (cnt > CAPW) cnt = wave_overflow<HAS_MASK>(rowp, mrow, s0, ns, enc, sub, nsp, kp, tk);
   }
 
-  // Publish the sub-record header.  The finalize kernel, launched after this
-  // one on the same stream, reads all of it.
+  // Publish the sub-record header.
   if (lane == 0) {
-    sub[0 * nsp] = (uint64_t)__double_as_longlong(P);
-    sub[1 * nsp] = ((uint64_t)__float_as_uint(c_r) << 32) | __float_as_uint(c_w);
-    sub[2 * nsp] = (uint64_t)__double_as_longlong(R);
-    sub[3 * nsp] = ((uint64_t)flags << 32) | __float_as_uint(m_w);
-    sub[4 * nsp] = (uint64_t)(uint32_t)cnt;
-    sub[5 * nsp] = ((uint64_t)pub[1] << 32) | pub[0];
-    sub[6 * nsp] = ((uint64_t)pub[3] << 32) | pub[2];
+    st_agent(&sub[0 * nsp], (uint64_t)__double_as_longlong(P));
+    st_agent(&sub[1 * nsp], ((uint64_t)__float_as_uint(c_r) << 32) | __float_as_uint(c_w));
+    st_agent(&sub[2 * nsp], (uint64_t)__double_as_longlong(R));
+    st_agent(&sub[3 * nsp], ((uint64_t)flags << 32) | __float_as_uint(m_w));
+    st_agent(&sub[4 * nsp], (uint64_t)(uint32_t)cnt);
+    st_agent(&sub[5 * nsp], ((uint64_t)pub[1] << 32) | pub[0]);
+    st_agent(&sub[6 * nsp], ((uint64_t)pub[3] << 32) | pub[2]);
   }
-}
 
-// ---------------------------------------------------------------------------
-// The finalize kernel, launched after chunk_kernel on the same stream: one
-// workgroup per sequence (per row for a plain batch), one wave per row of it
-// (a wave takes every FWAVES-th row when the sequence has more).  A row takes
-// fin_fast, or fin_general when it falls outside the common case.  For a
-// speculative block the workgroup then walks its sequence (accept_drafts).
-constexpr int FWAVES = 8;
-
-template <bool HAS_MASK, bool WANT_LSE, bool HAS_CTL>
-__global__ __launch_bounds__(64 * FWAVES) void finalize_kernel(Args a) {
-  __shared__ FinLds Fw[FWAVES];
-  const int lane = lane_id(), wave = wave_id();
-  const int nwaves = (int)(blockDim.x >> 6);
-  const int span = a.span > 0 ? a.span : 1;
-  const int seq = blockIdx.x;
-  const int nc = a.n_chunks, nsub = nc * NWAVE, nsp = ((nsub + 63) >> 6) << 6;
-  for (int r = wave; r < span; r += nwaves) {
-    const int row = seq * span + r;
-    const uint64_t* rowrec = a.rec + (int64_t)row * SRECW * nsp;
-    // One round of coalesced loads, issued before anything else: every header
-    // word and the first EPRE entries of every sub-record (common case).
-    uint64_t h[NHW], E[EPRE];
-    const bool live = lane < nsub;
-#pragma unroll
-    for (int i = 0; i < NHW; i++) h[i] = live ? rowrec[i * nsp + lane] : 0ull;
-#pragma unroll
-    for (int j = 0; j < EPRE; j++) E[j] = live ? rowrec[(SHDR + j) * nsp + lane] : 0ull;
-    const Cfg cfg = a.greedy_all ? greedy_cfg() : make_cfg(a.params[row], a.enc, a.n_top);
-    const float* rowp = a.logits + (int64_t)row * a.ld;
-    const uint32_t* mrow = HAS_MASK ? a.allowed + (int64_t)row * a.allowed_ld : nullptr;
-    CtlRow cr{};
-    if (HAS_CTL) cr = a.ctl_row[row];
-    const bool done = !(HAS_CTL && cr.active) && nsub <= 64 && cfg.kp <= 64 && !cfg.bad &&
-                      fin_fast<HAS_MASK, WANT_LSE>(a, cfg, row, nsub, h, E, Fw[wave]);
-    if (!done) fin_general<HAS_MASK, WANT_LSE, HAS_CTL>(a, cfg, row, rowrec, nsp, nsub, rowp, mrow, cr, Fw[wave]);
+  // Hand-off: every wave's stores acknowledged, the workgroup takes the row's
+  // arrival ticket; the last of the row's workgroups resets it for the next
+  // call and its first wave finalizes the row.
+  drain();
+  __syncthreads();
+  if (tid == 0) {
+    const int t = __hip_atomic_fetch_add(&a.row_ticket[row], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    Lc.last = (t == nc - 1) ? 1 : 0;
+    if (t == nc - 1) st_agent(&a.row_ticket[row], 0);
   }
-  (void)lane;
-
-  // Speculative verify: accept_drafts over the sequence's sampled rows.
-  if (a.span > 0) {
-    __syncthreads();  // every row of the sequence has its token and status
-    if (threadIdx.x == 0) {
-      const int D = span - 1;
-      const int64_t r0 = (int64_t)seq * span;
-      const int bud = a.budget ? a.budget[seq] : 0x7FFFFFFF;
-      int mcount = 0, ncom = 0, sst = XS_ROW_OK;
-      for (int i = 0; i < span; i++) {
-        if (ncom >= bud) break;
-        const int rs = a.status[r0 + i];
-        if (rs != XS_ROW_OK) { sst = rs; break; }
-        const int s = a.token[r0 + i];
-        const bool matched = i < D && s == a.drafts[(int64_t)seq * D + i];
-        a.committed[(int64_t)seq * span + ncom] = s;
-        ncom++;
-        if (matched) mcount++;
-        bool eog = false;
-        for (int e = 0; e < a.n_eog; e++) eog |= (s == a.eog[e]);
-        if (!matched || eog) break;
-      }
-      for (int i = ncom; i < span; i++) a.committed[(int64_t)seq * span + i] = -1;
-      a.accepted[seq] = mcount;
-      a.n_committed[seq] = ncom;
-      a.seq_status[seq] = sst;
-    }
-  }
+  __syncthreads();
+  if (!Lc.last || wave != 0) return;
+  finalize_row<HAS_MASK, WANT_LSE, HAS_CTL>(a, cfg, row, rowrec, nsp, nc * NWAVE, rowp, mrow, Fl);
 }
 
 // ---------------------------------------------------------------------------
@@ -1939,6 +1975,8 @@ struct xs_context {
   uint64_t* ctl_patch;  // [max_rows, CTL_MAX] patch lists of controlled calls
   xs::CtlRow* ctl_row;  // [max_rows]
   int32_t* ctl_chunk;   // [max_rows, max_chunks + 1]
+  int32_t* row_ticket;  // [max_rows] arrival tickets, zero between calls
+  int32_t* seq_ticket;  // [max_rows]
 };
 
 namespace {
@@ -1972,14 +2010,13 @@ int check_common(xs_context* ctx, const Call& c) {
   return XS_OK;
 }
 
-// chunk_kernel over rows x n_chunks workgroups, then finalize_kernel with one
-// workgroup per sequence of `span` rows (span 1: a plain batch); a call with
-// sparse controls runs control_kernel (one workgroup per row) first.
+// One chunk_kernel launch over rows x n_chunks workgroups (it finalizes the
+// rows itself); a call with sparse controls runs control_kernel (one
+// workgroup per row) first.
 template <bool M, bool S, bool C>
-void launch2(xs_context* ctx, xs::Args& a, int64_t rows, dim3 g1, dim3 g2, dim3 b2) {
+void launch2(xs_context* ctx, xs::Args& a, int64_t rows, dim3 g1) {
   if (C) hipLaunchKernelGGL((xs::control_kernel<M>), dim3((unsigned)rows), dim3(xs::BLOCK), 0, ctx->stream, a);
   hipLaunchKernelGGL((xs::chunk_kernel<M, S, C>), g1, dim3(xs::BLOCK), 0, ctx->stream, a);
-  hipLaunchKernelGGL((xs::finalize_kernel<M, S, C>), g2, b2, 0, ctx->stream, a);
 }
 
 int launch(xs_context* ctx, xs::Args& a, int64_t rows, int span, bool mask, bool lse) {
@@ -1991,12 +2028,14 @@ int launch(xs_context* ctx, xs::Args& a, int64_t rows, int span, bool mask, bool
   a.patch = ctx->ctl_patch;
   a.ctl_row = ctx->ctl_row;
   a.ctl_chunk = ctx->ctl_chunk;
-  const dim3 g1((unsigned)grid), g2((unsigned)(rows / span)), b2(64 * (unsigned)std::min(span, xs::FWAVES));
-  if (ctl && mask) launch2<true, false, true>(ctx, a, rows, g1, g2, b2);
-  else if (ctl) launch2<false, false, true>(ctx, a, rows, g1, g2, b2);
-  else if (mask) launch2<true, false, false>(ctx, a, rows, g1, g2, b2);
-  else if (lse) launch2<false, true, false>(ctx, a, rows, g1, g2, b2);
-  else launch2<false, false, false>(ctx, a, rows, g1, g2, b2);
+  a.row_ticket = ctx->row_ticket;
+  a.seq_ticket = ctx->seq_ticket;
+  const dim3 g1((unsigned)grid);
+  if (ctl && mask) launch2<true, false, true>(ctx, a, rows, g1);
+  else if (ctl) launch2<false, false, true>(ctx, a, rows, g1);
+  else if (mask) launch2<true, false, false>(ctx, a, rows, g1);
+  else if (lse) launch2<false, true, false>(ctx, a, rows, g1);
+  else launch2<false, false, false>(ctx, a, rows, g1);
   return hipGetLastError() == hipSuccess ? XS_OK : XS_ERR_HIP;
 }
 
@@ -2028,6 +2067,10 @@ int xs_create(int device, int64_t max_rows, int64_t vocab, int32_t k_max, xs_con
   ok = ok && hipMalloc((void**)&c->ctl_patch, max_rows * xs::CTL_MAX * sizeof(uint64_t)) == hipSuccess;
   ok = ok && hipMalloc((void**)&c->ctl_row, max_rows * sizeof(xs::CtlRow)) == hipSuccess;
   ok = ok && hipMalloc((void**)&c->ctl_chunk, max_rows * (mc + 1) * sizeof(int32_t)) == hipSuccess;
+  ok = ok && hipMalloc((void**)&c->row_ticket, max_rows * sizeof(int32_t)) == hipSuccess;
+  ok = ok && hipMalloc((void**)&c->seq_ticket, max_rows * sizeof(int32_t)) == hipSuccess;
+  ok = ok && hipMemset(c->row_ticket, 0, max_rows * sizeof(int32_t)) == hipSuccess;
+  ok = ok && hipMemset(c->seq_ticket, 0, max_rows * sizeof(int32_t)) == hipSuccess;
   ok = ok && hipDeviceSynchronize() == hipSuccess;
   if (!ok) {
     xs_destroy(c);
@@ -2046,6 +2089,8 @@ int xs_destroy(xs_context* c) {
   (void)hipFree(c->ctl_patch);
   (void)hipFree(c->ctl_row);
   (void)hipFree(c->ctl_chunk);
+  (void)hipFree(c->row_ticket);
+  (void)hipFree(c->seq_ticket);
   free(c);
   return XS_OK;
 }

@@ -789,13 +789,8 @@ XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, int nsub, const uin
   wave_lds_sync();
   const uint64_t xv = lane < M ? F.list[lane] : 0ull;
   int rank = 0;
-  for (int j0 = 0; j0 < M; j0 += 8) {
-#pragma unroll
-    for (int u = 0; u < 8; u++) {
-      const uint64_t y = rdl64(xv, (j0 + u) & 63);
-      rank += (j0 + u < M && y > xv) ? 1 : 0;
-    }
-  }
+#pragma unroll 8
+  for (int j = 0; j < M; j++) rank += (F.list[j] > xv) ? 1 : 0;  // LDS broadcast reads
   if (lane < M) F.psel[rank] = xv;
   wave_lds_sync();
   const uint64_t sel = lane < M ? F.psel[lane] : 0ull;
@@ -844,8 +839,11 @@ XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, int nsub, const uin
     // The draw (truncate_top_p, then WeightedIndex), serial f32: lane i
     // ends each chain with the serial prefix sum through weight i.
     w = lane < k ? __uint_as_float((uint32_t)(pk >> 32)) : 0.0f;
-    auto chain = [&](float init) __attribute__((always_inline)) -> float {
-      float acc = init;
+    // Every lane adds the same weights (uniform, from scalar registers) in
+    // order; lane j keeps the running value after weight j.  The weights past
+    // k are +0.0 and leave the sums unchanged.
+    auto chain = [&](float init, float& at_lane) __attribute__((always_inline)) -> float {
+      float acc = init, mine = 0.0f;
 #pragma unroll
       for (int b0 = 0; b0 < 64; b0 += 8) {
         if (b0 < k) {
@@ -853,21 +851,27 @@ XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, int nsub, const uin
 #pragma unroll
           for (int u = 0; u < 8; u++) q[u] = rdlf(w, b0 + u);
 #pragma unroll
-          for (int u = 0; u < 8; u++) acc = acc + ((lane >= b0 + u) ? q[u] : 0.0f);
+          for (int u = 0; u < 8; u++) {
+            acc = acc + q[u];
+            mine = (lane == b0 + u) ? acc : mine;
+          }
         }
       }
+      at_lane = mine;
       return acc;
     };
     bool zero = false;
     if (!(cfg.top_p >= 1.0f)) {
-      const float sum = rdlf(chain(-0.0f), k - 1);  // folds from -0.0 as Rust's f32 Sum does
+      float unused;
+      const float sum = chain(-0.0f, unused);  // folds from -0.0 as Rust's f32 Sum does
       if (!(sum > 0.0f)) zero = true;  // all weights zero: returned unchanged
       else w = __fdiv_rn(w, sum);
     }
     if (zero) {
       st = XS_ROW_ZERO_WEIGHT;
     } else {
-      const float c = chain(0.0f);
+      float c;
+      (void)chain(0.0f, c);
       int keep = k;
       if (!(cfg.top_p >= 1.0f)) {
         const uint64_t bm = __ballot(lane < k && c >= cfg.top_p);
@@ -1684,13 +1688,10 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
   // (K' <= 64), or the chunk's lane maxima of rank wave + 4r (K' > 64).
   uint32_t pub[4] = {fkey(m_w), 0u, 0u, 0u};
   if (!cfg.bad) {
-    if (kp <= 64) {
-      const uint32_t gv = Lc.groupmax[lane];
-#pragma unroll
-      for (int bit = 31; bit >= 0; bit--) {
-        const uint32_t c = tk | (1u << bit);
-        if ((int)__popcll(__ballot(gv >= c)) >= kp) tk = c;
-      }
+    if (kp <= 64) {  // the kp-th largest group max: a DPP bitonic sort of the 64
+      uint32_t gv[1] = {Lc.groupmax[lane]};
+      wave_sort_desc<1, true>(gv);
+      tk = rdl(gv[0], kp - 1);
     }
     if (kp > 64) {
       uint32_t all[4];

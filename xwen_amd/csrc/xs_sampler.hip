@@ -306,7 +306,7 @@ XS_DEV Cfg greedy_cfg() {
 // ---------------------------------------------------------------------------
 // Workspace and launch arguments.
 //
-// chunk_kernel writes one sub-record per wave into the workspace with
+// sample_kernel writes one sub-record per wave into the workspace with
 // agent-scope stores; the row's last workgroup (arrival ticket) reads them
 // back with agent-scope loads and finalizes the row in the same launch.
 
@@ -732,8 +732,10 @@ XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, int nsub, const uin
 
   const int cnt = live ? (int)min((uint32_t)h[4], (uint32_t)CAPW) : 0;  // clamped: never read past a sub-record
   const float m_v = red_maxf(live ? __uint_as_float((uint32_t)h[3]) : -INFINITY);
-  const uint32_t fl = red_or(live ? (uint32_t)(h[3] >> 32) : 0u);
-  const int maxc = red_maxi(cnt);
+  const uint32_t hf = live ? (uint32_t)(h[3] >> 32) : 0u;
+  const bool nan_seen = __ballot(hf & 1u) != 0;
+  const bool finite_seen = __ballot(hf & 2u) != 0;
+  const int maxc = __ballot(cnt > EPRE) ? red_maxi(cnt) : EPRE;
   const float m_s = cfg.scale ? m_v * cfg.inv : m_v;
   double part = 0.0, rpart = 0.0;
   if (live) {
@@ -747,8 +749,6 @@ XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, int nsub, const uin
   const double S_d = red_sumd(part);
   const double R_d = WANT_LSE ? red_sumd(rpart) : 0.0;
   const float S = (float)S_d;
-  const bool nan_seen = fl & 1u;
-  const bool finite_seen = fl & 2u;
   int st = XS_ROW_OK;
   if (HAS_MASK && !finite_seen) st = XS_ROW_NO_FINITE;
   else if (cfg.greedy) st = nan_seen ? XS_ROW_NAN : (m_v == -INFINITY ? XS_ROW_NO_FINITE : XS_ROW_OK);
@@ -773,8 +773,25 @@ XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, int nsub, const uin
       M += __popcll(b);
     }
   };
+  {
+    // the preloaded entries: each lane's survivors go after those of the
+    // lanes below it (an exclusive scan of the per-lane counts)
+    bool ok[EPRE];
+    int c = 0;
 #pragma unroll
-  for (int j = 0; j < EPRE; j++) put(E[j], j < cnt && E[j] >= floor_e);
+    for (int j = 0; j < EPRE; j++) {
+      ok[j] = j < cnt && E[j] >= floor_e;
+      c += ok[j] ? 1 : 0;
+    }
+    const int incl = wave_incl_scan(c);
+    int pos = incl - c;
+#pragma unroll
+    for (int j = 0; j < EPRE; j++) {
+      if (ok[j] && pos < 64) F.list[pos] = E[j];
+      pos += ok[j] ? 1 : 0;
+    }
+    M = (int)rdl((uint32_t)incl, 63);
+  }
   // entries past the preloaded ones (a sub-record holding more than EPRE)
 #pragma unroll 1
   for (int j0 = EPRE; j0 < maxc; j0 += 4) {
@@ -1211,7 +1228,7 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
             const int id = 4 * f + e;
             if (HAS_MASK && id < enc && !((mrow[id >> 5] >> (id & 31)) & 1u)) xv[e] = -INFINITY;
           }
-          if (ctl_on) {  // the controlled values, as chunk_kernel saw them
+          if (ctl_on) {  // the controlled values, as sample_kernel saw them
             if (cr.force_id >= 0) {
 #pragma unroll
               for (int e = 0; e < 4; e++) xv[e] = (4 * f + e == cr.force_id) ? cr.force_val : -INFINITY;
@@ -1467,7 +1484,7 @@ XS_DEV void finalize_row(const Args& a, const Cfg& cfg, int row, const uint64_t*
 // arrive (an atomic ticket per row) finalizes the row with its first wave.
 
 template <bool HAS_MASK, bool WANT_LSE, bool HAS_CTL>
-__global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) void chunk_kernel(Args a) {
+__global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) void sample_kernel(Args a) {
   __shared__ ChunkLds Lc;
   __shared__ FinLds Fl;
   const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
@@ -1777,13 +1794,13 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
 
 // ---------------------------------------------------------------------------
 // Sparse controls (apply_control, sampler.rs:433-490): one workgroup per row,
-// launched before chunk_kernel when a call carries controls.  The row's bans
+// launched before sample_kernel when a call carries controls.  The row's bans
 // and biases become its patch list: every distinct listed id < enc with its
 // value after the mask, the bans (sampler.rs:450-454) and then the biases in
 // list order (:455-459).  A pull needs the row max after those (:460-470): the
 // workgroup reads the row once for it, and only for a finite target, and keeps
 // the target's new value.  A force keeps the target's final value (:471-482).
-// chunk_kernel overwrites exactly these elements before anything reads them.
+// sample_kernel overwrites exactly these elements before anything reads them.
 template <bool HAS_MASK>
 __global__ __launch_bounds__(BLOCK) void control_kernel(Args a) {
   __shared__ uint64_t keys[CTL_MAX];  // (id << 32 | list position), sorted
@@ -2011,13 +2028,13 @@ int check_common(xs_context* ctx, const Call& c) {
   return XS_OK;
 }
 
-// One chunk_kernel launch over rows x n_chunks workgroups (it finalizes the
+// One sample_kernel launch over rows x n_chunks workgroups (it finalizes the
 // rows itself); a call with sparse controls runs control_kernel (one
 // workgroup per row) first.
 template <bool M, bool S, bool C>
 void launch2(xs_context* ctx, xs::Args& a, int64_t rows, dim3 g1) {
   if (C) hipLaunchKernelGGL((xs::control_kernel<M>), dim3((unsigned)rows), dim3(xs::BLOCK), 0, ctx->stream, a);
-  hipLaunchKernelGGL((xs::chunk_kernel<M, S, C>), g1, dim3(xs::BLOCK), 0, ctx->stream, a);
+  hipLaunchKernelGGL((xs::sample_kernel<M, S, C>), g1, dim3(xs::BLOCK), 0, ctx->stream, a);
 }
 
 int launch(xs_context* ctx, xs::Args& a, int64_t rows, int span, bool mask, bool lse) {

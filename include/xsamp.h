@@ -19,6 +19,7 @@
  *   xs_argmax_probs             argmax_probs_device /
  *                               draft_argmax_probs             src/generate.rs:4059-4087
  *   xs_keep_confident           keep_confident                 src/generate.rs:3898-3905
+ *   xs_select_option            select_option                  src/batch.rs:1545-1588
  *
  * Randomness: the reference draws from a seeded StdRng inside the sampler.  Here
  * the caller supplies one uniform per sampled row, u = j * 2^-23 with j in
@@ -227,6 +228,21 @@ typedef struct {
 } xs_argmax_args;
 
 int xs_argmax_probs(xs_context* ctx, const xs_argmax_args* args);
+
+/* Scored selection: select_option (batch.rs:1545-1588), host memory.  Over n
+ * option scores (f64 sums of log-probs, e.g. from xs_sample's held_row
+ * outputs): greedy (temperature <= 0 or top_k <= 1) returns the first maximal
+ * score (argmax_index, batch.rs:1683-1693).  Otherwise the scores are
+ * renormalized at the temperature (f64, batch.rs:1674-1680), ranked by
+ * probability (desc, f64 total order) with ties to the lower index, cut to
+ * top_k and then to the nucleus measured over the survivors' own mass (the
+ * crossing option kept; none cut at top_p >= 1, truncate_nucleus,
+ * batch.rs:1562-1588), and drawn with WeightedIndex<f64> from the uniform
+ * u = j * 2^-52 (rand 0.9's f64 UniformFloat from 52 random bits).  Returns
+ * XS_ROW_OK with *index set, XS_ROW_ZERO_WEIGHT when no option carries mass
+ * (the reference's error), or XS_ERR_ARG. */
+int32_t xs_select_option(const double* scores, int64_t n, double temperature, int64_t top_k,
+                         double top_p, double u, int64_t* index);
 
 /* keep_confident (generate.rs:3898-3905), host memory: the length of the
  * longest prefix whose probabilities are all >= p_min (a NaN ends it). */

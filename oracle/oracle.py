@@ -21,6 +21,7 @@ OK, NAN, NO_FINITE, MASK_SHORT, FORCE_OOR, ZERO_WEIGHT, NARROW = range(7)
 SUM_SEQ_F32, SUM_F64, SUM_GIVEN = 0, 1, 2
 
 _f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+_f64p = np.ctypeslib.ndpointer(np.float64, flags="C_CONTIGUOUS")
 _u32p = np.ctypeslib.ndpointer(np.uint32, flags="C_CONTIGUOUS")
 
 
@@ -92,6 +93,11 @@ def lib():
                                        C.POINTER(C.c_int64), C.POINTER(C.c_int64)]
         L.xo_draft_argmax_probs.restype = C.c_int32
         L.xo_draft_argmax_probs.argtypes = [_f32p, C.c_int64, C.c_int64, _u32p, _f32p]
+        L.xo_truncate_nucleus.restype = C.c_int64
+        L.xo_truncate_nucleus.argtypes = [_f64p, C.c_int64, C.c_double]
+        L.xo_select_option.restype = C.c_int32
+        L.xo_select_option.argtypes = [_f64p, C.c_int64, C.c_double, C.c_int64, C.c_double,
+                                       C.c_double, C.POINTER(C.c_int64)]
         L.xo_keep_confident.restype = C.c_int64
         L.xo_keep_confident.argtypes = [_u32p, _f32p, C.c_int64, C.c_float]
         L.xo_held_row.restype = C.c_int32
@@ -282,6 +288,21 @@ def draft_argmax_probs(logits: np.ndarray):
     pr = np.zeros(n, np.float32)
     lib().xo_draft_argmax_probs(x, n, v, ids, pr)
     return ids, pr
+
+
+def truncate_nucleus(probs, top_p: float) -> int:
+    """xo_truncate_nucleus: how many of the ranked probabilities the cut keeps."""
+    p = np.ascontiguousarray(probs, np.float64)
+    return int(lib().xo_truncate_nucleus(p, p.size, float(top_p)))
+
+
+def select_option(scores, temperature: float, top_k: int, top_p: float, u: float = 0.0):
+    """xo_select_option: (status, index) of batch.rs's select_option for uniform u."""
+    s = np.ascontiguousarray(scores, np.float64)
+    idx = C.c_int64(-1)
+    st = lib().xo_select_option(s, s.size, float(temperature), int(top_k), float(top_p),
+                                float(u), C.byref(idx))
+    return int(st), int(idx.value)
 
 
 def keep_confident(ids, probs, p_min: float):

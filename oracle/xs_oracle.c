@@ -593,3 +593,89 @@ void xo_det_logits(int64_t n, uint64_t seed, float scale, float* out) {
     out[i] = (u - 0.5f) * 2.0f * scale;
   }
 }
+
+/* truncate_nucleus -- batch.rs:1562-1588: over probabilities already ranked
+ * (desc), the number kept: all at top_p >= 1 or a total <= 0, else up to and
+ * including the first whose running sum of p / total reaches top_p. */
+int64_t xo_truncate_nucleus(const double* prob, int64_t n, double top_p) {
+  if (top_p >= 1.0) return n;
+  double total = -0.0;
+  for (int64_t i = 0; i < n; i++) total += prob[i];
+  if (total <= 0.0) return n;
+  double cum = 0.0;
+  for (int64_t i = 0; i < n; i++) {
+    cum += prob[i] / total;
+    if (cum >= top_p) return i + 1;
+  }
+  return n;
+}
+
+/* f64::total_cmp order as an unsigned key. */
+static uint64_t total_key64(double d) {
+  uint64_t b;
+  memcpy(&b, &d, 8);
+  return (b >> 63) ? ~b : (b | 0x8000000000000000ull);
+}
+
+/* select_option -- batch.rs:1545-1560, with renormalize (:1674-1680) and
+ * argmax_index (:1683-1693): greedy on T <= 0 or top_k <= 1; else softmax at
+ * T in f64 (libm exp), rank by (p desc by total_cmp, index asc), keep top_k,
+ * cut the nucleus, and draw with WeightedIndex<f64> from u = j * 2^-52. */
+int32_t xo_select_option(const double* scores, int64_t n, double temperature, int64_t top_k,
+                         double top_p, double u, int64_t* index) {
+  if (n < 1) return XO_ZERO_WEIGHT;
+  if (temperature <= 0.0 || top_k <= 1) {
+    double best = -INFINITY;
+    int64_t at = 0;
+    for (int64_t i = 0; i < n; i++)
+      if (scores[i] > best) { best = scores[i]; at = i; }
+    *index = at;
+    return XO_OK;
+  }
+  double* p = (double*)malloc((size_t)n * sizeof(double));
+  int64_t* rank = (int64_t*)malloc((size_t)n * sizeof(int64_t));
+  double* w = (double*)malloc((size_t)n * sizeof(double));
+  double mx = -INFINITY;
+  for (int64_t i = 0; i < n; i++) {
+    const double s = scores[i] / temperature;
+    p[i] = s;
+    if (s > mx) mx = s;  /* the f64::max fold from -inf: a NaN never replaces it */
+  }
+  double total = -0.0;
+  for (int64_t i = 0; i < n; i++) {
+    p[i] = exp(p[i] - mx);
+    total += p[i];
+  }
+  for (int64_t i = 0; i < n; i++) p[i] = p[i] / total;
+  /* insertion sort: stable, by total_cmp key desc */
+  for (int64_t i = 0; i < n; i++) {
+    int64_t j = i;
+    while (j > 0 && total_key64(p[rank[j - 1]]) < total_key64(p[i])) { rank[j] = rank[j - 1]; j--; }
+    rank[j] = i;
+  }
+  int64_t m = top_k < n ? top_k : n;
+  for (int64_t i = 0; i < m; i++) w[i] = p[rank[i]];
+  m = xo_truncate_nucleus(w, m, top_p);
+  /* WeightedIndex<f64>::new + sample */
+  int32_t st = XO_OK;
+  double tw = w[0];
+  if (!(tw >= 0.0)) st = XO_ZERO_WEIGHT;
+  double* cum = (double*)malloc((size_t)(m > 1 ? m - 1 : 1) * sizeof(double));
+  for (int64_t i = 1; i < m && st == XO_OK; i++) {
+    if (!(w[i] >= 0.0)) { st = XO_ZERO_WEIGHT; break; }
+    cum[i - 1] = tw;
+    tw += w[i];
+  }
+  if (st == XO_OK && (tw == 0.0 || !isfinite(tw))) st = XO_ZERO_WEIGHT;
+  if (st == XO_OK) {
+    const double x = u * tw + 0.0;
+    int64_t c = 0;
+    while (c < m - 1 && cum[c] <= x) c++;
+    *index = rank[c];
+  }
+  free(cum);
+  free(w);
+  free(rank);
+  free(p);
+  return st;
+}

@@ -33,6 +33,12 @@
  *   xo_draft_argmax_probs generate.rs:5520-5552 (f64 scalar, 1e-5).
  *   xo_keep_confident    generate.rs:5560-5597.
  *   xo_held_row          f64 brute force (decimal) on small rows.
+ *   xo_select_option /
+ *   xo_truncate_nucleus  batch.rs:2970-3016 (greedy on both conditions, a
+ *                        top_k of 2 never reaching the third option, a tight
+ *                        nucleus keeping the leader, an open draw reaching the
+ *                        tail, the three nucleus cuts); the f64 uniform->index
+ *                        map is restated from rand 0.9 as for f32.
  *   xo_det_logits        sampler.rs:903-914 generator, checked by the KATs
  *                        that consume it (top_p_of_zero, llama.cpp matrix).
  */
@@ -130,6 +136,9 @@ int64_t xo_keep_confident(const uint32_t* ids, const float* probs, int64_t n, fl
 int32_t xo_held_row(const float* row, int64_t width, int64_t enc, float* max_out,
                     double* lse_out);
 void xo_det_logits(int64_t n, uint64_t seed, float scale, float* out);
+int64_t xo_truncate_nucleus(const double* prob, int64_t n, double top_p);
+int32_t xo_select_option(const double* scores, int64_t n, double temperature, int64_t top_k,
+                         double top_p, double u, int64_t* index);
 
 #ifdef __cplusplus
 }

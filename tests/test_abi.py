@@ -115,3 +115,28 @@ def test_mask_packing_round_trips():
     # the reference's own example: mask 0b0101 allows ids 0 and 2 (sampler.rs:819-833)
     w = workloads.pack_mask(np.array([[True, False, True, False]]))
     assert w[0, 0] == 0b0101
+
+
+def test_select_option_through_the_abi(golden, oracle):
+    """xs_select_option (host code in the library) against the oracle's
+    restatement, index for index, and on the reference's own cases."""
+    from xwen_amd import sampler as xsm
+    rng = np.random.default_rng(6)
+    for trial in range(400):
+        n = int(rng.integers(1, 12))
+        scores = rng.normal(0, 3, n)
+        if trial % 5 == 0:
+            scores[rng.integers(0, n)] = scores.max()  # a tie at the top
+        T = float(rng.choice([0.0, 0.5, 1.0, 2.5]))
+        k = int(rng.choice([1, 2, 3, 20]))
+        p = float(rng.choice([0.3, 0.8, 0.95, 1.0]))
+        u = float(rng.integers(0, 1 << 52)) * 2.0 ** -52
+        st, idx = oracle.select_option(scores, T, k, p, u)
+        assert st == 0
+        got = xsm.select_option(scores, xsm.SamplerOptions(temperature=T, top_k=k, top_p=p), u)
+        assert got == idx, (trial, scores, T, k, p, u)
+    c = golden["select_option"]
+    T, k, p = c["tight"]
+    assert xsm.select_option(c["scores"], xsm.SamplerOptions(T, k, p), 0.99) == c["tight_expect"]
+    with pytest.raises(xsm.SampleError):
+        xsm.select_option([0.0, float("nan")], xsm.SamplerOptions(1.0, 20, 0.9), 0.5)

@@ -361,3 +361,49 @@ def test_exp_table_constants_against_decimal():
     krows = re.findall(r"\{(0x[0-9a-fp.+-]+), (-?0x[0-9a-fp.+-]+)\}", kernel)
     assert [tuple(map(float.fromhex, r)) for r in krows] == \
         [tuple(map(float.fromhex, r)) for r in rows]
+
+
+# --- select_option (batch.rs:1545-1588) ----------------------------------------
+
+def test_select_option_known_answers(golden, oracle):
+    c = golden["select_option"]
+    sc = c["scores"]
+    us = [j / 997 for j in range(997)]  # a grid over [0, 1) in place of the seeded draws
+    for T, k, p in c["greedy"]:
+        for u in us[:8]:
+            assert oracle.select_option(sc, T, k, p, u) == (0, c["greedy_expect"])
+    T, k, p = c["narrow"]
+    assert all(oracle.select_option(sc, T, k, p, u)[1] < c["narrow_below"] for u in us)
+    T, k, p = c["tight"]
+    assert all(oracle.select_option(sc, T, k, p, u) == (0, c["tight_expect"]) for u in us)
+    T, k, p = c["open"]
+    assert any(oracle.select_option(sc, T, k, p, u)[1] >= c["open_reaches"] for u in us)
+
+
+def test_truncate_nucleus_known_answers(golden, oracle):
+    c = golden["truncate_nucleus"]
+    for top_p, want in c["cases"]:
+        assert oracle.truncate_nucleus(c["ranked"], top_p) == want
+
+
+def test_select_option_draws_the_renormalized_mass(oracle):
+    """With no cut, the share of a uniform grid that maps to option i is the
+    softmax probability of its score at T (a closed form), to the grid step."""
+    rng = np.random.default_rng(5)
+    scores = rng.normal(0, 2, 7)
+    T, N = 1.7, 20000
+    got = np.bincount([oracle.select_option(scores, T, 50, 1.0, j / N)[1] for j in range(N)],
+                      minlength=7) / N
+    z = scores / T
+    want = np.exp(z - z.max()) / np.exp(z - z.max()).sum()
+    assert np.abs(got - want).max() <= 2.0 / N
+
+
+def test_select_option_ties_and_errors(oracle):
+    # equal scores rank by index: top_k = 2 never reaches the third
+    assert all(oracle.select_option([1.0, 1.0, 1.0], 1.0, 2, 1.0, j / 64)[1] < 2 for j in range(64))
+    # greedy ties go to the first listed option, NaN never wins
+    assert oracle.select_option([float("nan"), 2.0, 2.0], 0.0, 20, 1.0) == (0, 1)
+    # no mass: a NaN score makes every probability NaN (WeightedIndex refuses it)
+    assert oracle.select_option([0.0, float("nan")], 1.0, 20, 0.9, 0.5)[0] == 5
+    assert oracle.select_option([-np.inf, -np.inf], 1.0, 20, 0.9, 0.5)[0] == 5

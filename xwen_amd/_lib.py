@@ -97,6 +97,9 @@ def load() -> C.CDLL:
     L.xs_verify.argtypes = [_vp, C.POINTER(VerifyArgs)]
     L.xs_argmax_probs.restype = C.c_int
     L.xs_argmax_probs.argtypes = [_vp, C.POINTER(ArgmaxArgs)]
+    L.xs_select_option.restype = _i32
+    L.xs_select_option.argtypes = [_vp, _i64, C.c_double, _i64, C.c_double, C.c_double,
+                                   C.POINTER(_i64)]
     L.xs_keep_confident.restype = _i64
     L.xs_keep_confident.argtypes = [_vp, _i64, C.c_float]
     L.xs_version.restype = C.c_char_p

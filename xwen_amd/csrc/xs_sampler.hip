@@ -37,6 +37,9 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <vector>
 #include <math.h>
 #include <stdint.h>
 #include <stdlib.h>
@@ -2244,6 +2247,77 @@ int xs_argmax_probs(xs_context* ctx, const xs_argmax_args* in) {
   a.nslots = (int32_t)slots_for(in->width);
   a.rec = ctx->rec;
   return launch(ctx, a, in->rows, 1, false, true);
+}
+
+int32_t xs_select_option(const double* scores, int64_t n, double temperature, int64_t top_k,
+                         double top_p, double u, int64_t* index) {
+  if (!scores || !index || n < 1) return XS_ERR_ARG;
+  if (temperature <= 0.0 || top_k <= 1) {  // argmax_index: the first maximal score
+    double best = -INFINITY;
+    int64_t at = 0;
+    for (int64_t i = 0; i < n; i++)
+      if (scores[i] > best) {
+        best = scores[i];
+        at = i;
+      }
+    *index = at;
+    return XS_ROW_OK;
+  }
+  // renormalize at the temperature: f64 softmax (the f64::max fold skips NaN)
+  std::vector<double> p((size_t)n);
+  double mx = -INFINITY;
+  for (int64_t i = 0; i < n; i++) {
+    p[i] = scores[i] / temperature;
+    if (p[i] > mx) mx = p[i];
+  }
+  double total = -0.0;
+  for (double& v : p) {
+    v = std::exp(v - mx);
+    total += v;
+  }
+  for (double& v : p) v = v / total;
+  // rank by probability (f64::total_cmp, descending), ties to the lower index
+  auto key = [](double d) {
+    uint64_t b;
+    memcpy(&b, &d, 8);
+    return (b >> 63) ? ~b : (b | 0x8000000000000000ull);
+  };
+  std::vector<int64_t> order((size_t)n);
+  for (int64_t i = 0; i < n; i++) order[i] = i;
+  std::stable_sort(order.begin(), order.end(), [&](int64_t x, int64_t y) { return key(p[x]) > key(p[y]); });
+  const int64_t kept_k = std::min(top_k, n);
+  // the nucleus over the survivors' own mass; the crossing option stays
+  int64_t keep = kept_k;
+  if (!(top_p >= 1.0)) {
+    double mass = -0.0;
+    for (int64_t i = 0; i < kept_k; i++) mass += p[order[i]];
+    if (!(mass <= 0.0)) {
+      double run = 0.0;
+      for (int64_t i = 0; i < kept_k; i++) {
+        run += p[order[i]] / mass;
+        if (run >= top_p) {
+          keep = i + 1;
+          break;
+        }
+      }
+    }
+  }
+  // WeightedIndex<f64> (rand 0.9): cumulative weights before each later
+  // weight, the draw x = u * total, the count of cumulative weights <= x
+  double acc = p[order[0]];
+  if (!(acc >= 0.0)) return XS_ROW_ZERO_WEIGHT;
+  std::vector<double> cum;
+  for (int64_t i = 1; i < keep; i++) {
+    const double w = p[order[i]];
+    if (!(w >= 0.0)) return XS_ROW_ZERO_WEIGHT;
+    cum.push_back(acc);
+    acc += w;
+  }
+  if (acc == 0.0 || !std::isfinite(acc)) return XS_ROW_ZERO_WEIGHT;
+  const double x = u * acc + 0.0;
+  const int64_t c = std::upper_bound(cum.begin(), cum.end(), x) - cum.begin();
+  *index = order[c];
+  return XS_ROW_OK;
 }
 
 int64_t xs_keep_confident(const float* probs, int64_t n, float p_min) {

@@ -12,6 +12,7 @@ Names, argument meaning and error behaviour follow the reference:
   encodable                         src/sampler.rs:127-128, :245-253
   verify_batch (accept_drafts)      src/generate.rs:4020-4046
   keep_confident                    src/generate.rs:3898-3905
+  select_option                     src/batch.rs:1545-1588
   held-row log-probs                src/generate.rs:1871-1933
 
 Differences, all forced by the batched device design:
@@ -410,6 +411,25 @@ def draft_argmax_probs(ctx: Context, logits, *, width: int | None = None):
     as numpy int64 ids and float32 probabilities."""
     ids, probs = argmax_probs_device(ctx, logits, width=width)
     return ids.cpu().numpy().astype(np.int64), probs.cpu().numpy()
+
+
+def select_option(scores, sampling: SamplerOptions, u: float = 0.0) -> int:
+    """select_option (batch.rs:1545-1588) through the C ABI (host memory): the
+    option index drawn from f64 `scores` under `sampling`, with the uniform
+    u = j * 2^-52 (ignored when greedy).  Raises SampleError when no option
+    carries any mass, as the reference's call fails."""
+    lib = _lib.load()
+    s = np.ascontiguousarray(np.asarray(scores, np.float64))
+    if s.size == 0:
+        raise ValueError("select_option needs at least one option")
+    idx = C.c_int64(-1)
+    st = lib.xs_select_option(s.ctypes.data, s.size, float(sampling.temperature),
+                              int(sampling.top_k), float(sampling.top_p), float(u), C.byref(idx))
+    if st < 0:
+        _lib.check(st, "xs_select_option")
+    if st != _lib.ROW_OK:
+        raise SampleError([st])
+    return int(idx.value)
 
 
 def keep_confident(ids, probs, p_min: float):

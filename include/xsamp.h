@@ -203,6 +203,12 @@ typedef struct {
   const xs_row_control* controls;
   const uint32_t* ctl_ids;
   const float* ctl_delta;
+  /* [seqs * span] or NULL: nonzero at position i when committing drafts[i]
+   * completes the grammar, which ends the walk like an EOG id
+   * (generate.rs:2452-2459).  Row i+1 is reached only if draft i was
+   * accepted, so the caller computes these, with the per-position masks,
+   * by stepping a copy of its grammar state along the drafts. */
+  const uint8_t* done_after;
 } xs_verify_args;
 
 int xs_verify(xs_context* ctx, const xs_verify_args* args);

@@ -50,7 +50,7 @@ int main(void) {
   F(xs_argmax_args, width); F(xs_argmax_args, ids); F(xs_argmax_args, probs);
   F(xs_row_control, n_bias); F(xs_row_control, pull_alpha); F(xs_row_control, force_id);
   F(xs_sample_args, controls); F(xs_sample_args, ctl_delta);
-  F(xs_verify_args, controls); F(xs_verify_args, ctl_delta);
+  F(xs_verify_args, controls); F(xs_verify_args, ctl_delta); F(xs_verify_args, done_after);
   return 0;
 }
 ''')

@@ -61,7 +61,7 @@ class VerifyArgs(C.Structure):
         ("drafts", _vp), ("budget", _vp), ("n_eog", _i32), ("eog", _i32 * 8),
         ("row_token", _vp), ("row_status", _vp), ("accepted", _vp), ("committed", _vp),
         ("n_committed", _vp), ("seq_status", _vp),
-        ("controls", _vp), ("ctl_ids", _vp), ("ctl_delta", _vp),
+        ("controls", _vp), ("ctl_ids", _vp), ("ctl_delta", _vp), ("done_after", _vp),
     ]
 
 

@@ -352,6 +352,7 @@ struct Args {
   int32_t span;
   const int32_t* drafts;
   const int32_t* budget;
+  const uint8_t* done_after;  // [seqs * span] or null: committing this draft completes the grammar
   int32_t n_eog;
   int32_t eog[8];
   int32_t* accepted;
@@ -1470,6 +1471,9 @@ XS_DEV void finalize_row(const Args& a, const Cfg& cfg, int row, const uint64_t*
         if (matched) mcount++;
         bool eog = false;
         for (int e = 0; e < a.n_eog; e++) eog |= (s == a.eog[e]);
+        // a draft that completes the grammar ends the walk like an EOG
+        // (generate.rs:2452-2459): the caller computed it along the drafts
+        if (matched && a.done_after && a.done_after[r0 + i]) eog = true;
         if (!matched || eog) break;
       }
       for (int i = ncom; i < span; i++) a.committed[(int64_t)seq * span + i] = -1;
@@ -2218,6 +2222,7 @@ int xs_verify(xs_context* ctx, const xs_verify_args* in) {
   a.committed = in->committed;
   a.n_committed = in->n_committed;
   a.seq_status = in->seq_status;
+  a.done_after = in->done_after;
   a.controls = in->controls;
   a.ctl_ids = in->ctl_ids;
   a.ctl_delta = in->ctl_delta;

@@ -11,6 +11,7 @@ Names, argument meaning and error behaviour follow the reference:
   Sampler.is_eog / eog_ids /
   encodable                         src/sampler.rs:127-128, :245-253
   verify_batch (accept_drafts)      src/generate.rs:4020-4046
+  masks_along_drafts                src/generate.rs:2434-2459
   keep_confident                    src/generate.rs:3898-3905
   select_option                     src/batch.rs:1545-1588
   held-row log-probs                src/generate.rs:1871-1933
@@ -284,8 +285,10 @@ class Verdict:
 
 def verify_batch(ctx: Context, logits, seqs: int, span: int, params, uniforms, drafts, *,
                  budget=None, eog=(), enc: int | None = None, allowed=None,
-                 controls: Controls | None = None, out: Verdict | None = None) -> Verdict:
-    """One xs_verify call over logits [seqs*span, ld]; drafts int32 [seqs, span-1]."""
+                 controls: Controls | None = None, done_after=None,
+                 out: Verdict | None = None) -> Verdict:
+    """One xs_verify call over logits [seqs*span, ld]; drafts int32 [seqs, span-1].
+    `allowed` / `done_after` per position come from masks_along_drafts."""
     torch = _torch()
     rows, ld = logits.shape
     assert rows == seqs * span
@@ -322,8 +325,44 @@ def verify_batch(ctx: Context, logits, seqs: int, span: int, params, uniforms, d
         a.controls = controls.rows.data_ptr()
         a.ctl_ids = controls.ids.data_ptr()
         a.ctl_delta = controls.delta.data_ptr()
+    if done_after is not None:
+        a.done_after = done_after.data_ptr()
     _lib.check(ctx.lib.xs_verify(ctx.h, C.byref(a)), "xs_verify")
     return out
+
+
+def masks_along_drafts(grammar, drafts, words: int):
+    """The verify block's per-position allow-masks, computed before the launch
+    (generate.rs:2434-2459).  The reference advances its grammar at sample
+    time, so row i's mask is the grammar state after the tokens committed at
+    rows 0..i-1; row i is reached only if those were drafts[0..i), so a copy
+    of the state stepped along the drafts gives every reachable row's mask.
+
+    `grammar` is GrammarState-like (constrain.rs:192-230): mask_words() ->
+    LSB-first u32 words or None (dormant: every id allowed), on_committed(id),
+    is_done(), and fork() -> an independent copy.  Returns (masks uint32
+    [span, words], done_after uint8 [span]): done_after[i] is 1 when
+    committing drafts[i] completes the grammar, which ends the walk like an
+    EOG.  Rows past a draft the grammar disallows (the sample there cannot
+    match it) or past completion are unreachable and get an all-ones mask."""
+    g = grammar.fork()
+    span = len(drafts) + 1
+    masks = np.full((span, words), 0xFFFFFFFF, np.uint32)
+    done = np.zeros(span, np.uint8)
+    for i in range(span):
+        m = g.mask_words()
+        if m is not None:
+            masks[i] = np.asarray(m, np.uint32)[:words]
+        if i == len(drafts):
+            break
+        t = int(drafts[i])
+        if m is not None and not (int(masks[i][t >> 5]) >> (t & 31)) & 1:
+            break  # the row's sample cannot equal this draft: the walk ends here
+        g.on_committed(t)
+        if g.is_done():
+            done[i] = 1
+            break
+    return masks, done
 
 
 class Sampler:

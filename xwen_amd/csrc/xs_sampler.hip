@@ -326,6 +326,7 @@ struct CtlRow {
   int32_t pad;
 };
 constexpr int CTL_MAX = XS_CTL_MAX;
+constexpr int TSTRIDE = 32;  // one arrival ticket per 128-byte line: tickets of different rows never share one
 
 struct Args {
   const float* logits;
@@ -374,8 +375,8 @@ struct Args {
   CtlRow* ctl_row;
   int32_t* ctl_chunk;
   // geometry + workspace
-  int32_t* row_ticket;  // [rows] workgroups of the row that have published (0 between calls)
-  int32_t* seq_ticket;  // [seqs] rows of the sequence that are finalized (0 between calls)
+  int32_t* row_ticket;  // [rows * TSTRIDE] workgroups of the row that have published (0 between calls)
+  int32_t* seq_ticket;  // [seqs * TSTRIDE] rows of the sequence that are finalized (0 between calls)
   int32_t n_chunks, nslots;
   uint64_t* rec;     // [rows, SRECW, nsp]: word i of sub-record s of a row at i * nsp + s
 };
@@ -1448,10 +1449,10 @@ XS_DEV void finalize_row(const Args& a, const Cfg& cfg, int row, const uint64_t*
     drain();  // this row's token and status are acknowledged
     const int seq = row / a.span;
     int t = 0;
-    if (lane == 0) t = __hip_atomic_fetch_add(&a.seq_ticket[seq], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (lane == 0) t = __hip_atomic_fetch_add(&a.seq_ticket[seq * TSTRIDE], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     t = __builtin_amdgcn_readfirstlane(t);
     if (t == a.span - 1 && lane == 0) {
-      st_agent(&a.seq_ticket[seq], 0);
+      st_agent(&a.seq_ticket[seq * TSTRIDE], 0);
       // accept_drafts (generate.rs:4020-4046) over the sequence's rows
       const int span = a.span, D = span - 1;
       const int64_t r0 = (int64_t)seq * span;
@@ -1790,9 +1791,9 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
   drain();
   __syncthreads();
   if (tid == 0) {
-    const int t = __hip_atomic_fetch_add(&a.row_ticket[row], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int t = __hip_atomic_fetch_add(&a.row_ticket[row * TSTRIDE], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     Lc.last = (t == nc - 1) ? 1 : 0;
-    if (t == nc - 1) st_agent(&a.row_ticket[row], 0);
+    if (t == nc - 1) st_agent(&a.row_ticket[row * TSTRIDE], 0);
   }
   __syncthreads();
   if (!Lc.last || wave != 0) return;
@@ -2000,8 +2001,8 @@ struct xs_context {
   uint64_t* ctl_patch;  // [max_rows, CTL_MAX] patch lists of controlled calls
   xs::CtlRow* ctl_row;  // [max_rows]
   int32_t* ctl_chunk;   // [max_rows, max_chunks + 1]
-  int32_t* row_ticket;  // [max_rows] arrival tickets, zero between calls
-  int32_t* seq_ticket;  // [max_rows]
+  int32_t* row_ticket;  // [max_rows * TSTRIDE] arrival tickets, zero between calls
+  int32_t* seq_ticket;  // [max_rows * TSTRIDE]
 };
 
 namespace {
@@ -2092,10 +2093,11 @@ int xs_create(int device, int64_t max_rows, int64_t vocab, int32_t k_max, xs_con
   ok = ok && hipMalloc((void**)&c->ctl_patch, max_rows * xs::CTL_MAX * sizeof(uint64_t)) == hipSuccess;
   ok = ok && hipMalloc((void**)&c->ctl_row, max_rows * sizeof(xs::CtlRow)) == hipSuccess;
   ok = ok && hipMalloc((void**)&c->ctl_chunk, max_rows * (mc + 1) * sizeof(int32_t)) == hipSuccess;
-  ok = ok && hipMalloc((void**)&c->row_ticket, max_rows * sizeof(int32_t)) == hipSuccess;
-  ok = ok && hipMalloc((void**)&c->seq_ticket, max_rows * sizeof(int32_t)) == hipSuccess;
-  ok = ok && hipMemset(c->row_ticket, 0, max_rows * sizeof(int32_t)) == hipSuccess;
-  ok = ok && hipMemset(c->seq_ticket, 0, max_rows * sizeof(int32_t)) == hipSuccess;
+  const size_t tbytes = (size_t)max_rows * xs::TSTRIDE * sizeof(int32_t);
+  ok = ok && hipMalloc((void**)&c->row_ticket, tbytes) == hipSuccess;
+  ok = ok && hipMalloc((void**)&c->seq_ticket, tbytes) == hipSuccess;
+  ok = ok && hipMemset(c->row_ticket, 0, tbytes) == hipSuccess;
+  ok = ok && hipMemset(c->seq_ticket, 0, tbytes) == hipSuccess;
   ok = ok && hipDeviceSynchronize() == hipSuccess;
   if (!ok) {
     xs_destroy(c);

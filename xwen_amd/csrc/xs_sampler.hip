@@ -1755,6 +1755,7 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
   int cnt = 0;
   if (!cfg.bad) {
     const float tf = (tk <= KEY_NEG_INF) ? -__FLT_MAX__ : keyf(tk);
+    uint64_t* const ent = sub + SHDR * nsp;  // entry p at ent[p * nsp]
 #pragma unroll
     for (int j = 0; j < SPC; j++) {
       if (__ballot(gm[j] >= tf)) {
@@ -1764,8 +1765,8 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
           const bool hit = x >= tf;
           const uint64_t b = __ballot(hit);
           if (b) {
-            const int pos = cnt + lanes_below(b);
-            if (hit && pos < CAPW) st_agent(&sub[(int64_t)(SHDR + pos) * nsp], pack(fkey(x), (uint32_t)(base_id + j * SLOT + e)));
+            const uint32_t pos = (uint32_t)cnt + (uint32_t)lanes_below(b);
+            if (hit && pos < (uint32_t)CAPW) st_agent(ent + pos * (uint32_t)nsp, pack(fkey(x), (uint32_t)(base_id + j * SLOT + e)));
             cnt += __popcll(b);
           }
         }

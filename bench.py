@@ -15,6 +15,11 @@ Prints one JSON line (rank 0, N = 1):
   cpu_baseline  the CPU oracle's restatement of the reference sampler (serial
              f32 softmax with libm expf, streaming top-k, top-p, WeightedIndex),
              one thread, on a bounded sample of the same rows
+
+`--workload c3|c4|c5` times the other measured configurations the same way
+(masked rows, a speculative verify block through xs_verify, a heterogeneous
+256-row batch with held_row statistics); their lines carry no cpu_baseline and
+no traffic figure.  The default (c2) is the headline line.
 """
 from __future__ import annotations
 
@@ -88,6 +93,103 @@ def calibrate_copy(nbytes: int, reps: int) -> None:
                       "launches": reps}), flush=True)
 
 
+def setup(name, nbuf, dev, torch, workloads, xsm, _lib, lib) -> dict:
+    """Build one workload's inputs (resident in HBM, `nbuf` rotating copies)
+    and its launch.  c2 is the headline configuration; c3-c5 are the other
+    measured configurations of the path."""
+    import ctypes as C
+    import numpy as np
+
+    log(f"generating the {name} workload")
+    wl = {"c2": workloads.c2_batch, "c3": workloads.c3_masked, "c4": workloads.c4_verify,
+          "c5": workloads.c5_heterogeneous}[name]()
+    rows, V = wl.logits.shape
+    ctx = xsm.Context(max_rows=rows, vocab=V)
+    base = torch.as_tensor(wl.logits).to(dev)
+    bufs = [base if i == 0 else base.clone() for i in range(nbuf)]
+    params = xsm.params_tensor(wl.temperature, wl.top_k, wl.top_p, rows, dev)
+    u = torch.as_tensor(wl.u).to(dev)
+    i32 = dict(dtype=torch.int32, device=dev)
+    row_bytes = ROW_BYTES
+    if name == "c4":
+        drafts = torch.as_tensor(wl.drafts).to(dev)
+        outs = [xsm.Verdict(row_token=torch.empty(rows, **i32), row_status=torch.empty(rows, **i32),
+                            accepted=torch.empty(wl.seqs, **i32),
+                            committed=torch.empty((wl.seqs, wl.span), **i32),
+                            n_committed=torch.empty(wl.seqs, **i32),
+                            seq_status=torch.empty(wl.seqs, **i32)) for _ in range(nbuf)]
+        argv = []
+        for i in range(nbuf):
+            a = _lib.VerifyArgs()
+            a.logits = bufs[i].data_ptr()
+            a.seqs, a.span, a.ld, a.width, a.enc = wl.seqs, wl.span, V, V, V
+            a.params, a.uniforms, a.drafts = params.data_ptr(), u.data_ptr(), drafts.data_ptr()
+            a.row_token, a.row_status = outs[i].row_token.data_ptr(), outs[i].row_status.data_ptr()
+            a.accepted, a.committed = outs[i].accepted.data_ptr(), outs[i].committed.data_ptr()
+            a.n_committed, a.seq_status = outs[i].n_committed.data_ptr(), outs[i].seq_status.data_ptr()
+            argv.append(a)
+        call = lib.xs_verify
+        token_of = lambda o: o.row_token
+    else:
+        outs = [xsm.Draws(token=torch.empty(rows, **i32), status=torch.empty(rows, **i32))
+                for _ in range(nbuf)]
+        extra = {}
+        if name == "c3":
+            extra["mask"] = torch.as_tensor(wl.mask.view(np.int32)).to(dev)
+            row_bytes += 4 * wl.mask.shape[1]
+        if name == "c5":
+            for o in outs:
+                o.row_max = torch.empty(rows, dtype=torch.float32, device=dev)
+                o.row_lse = torch.empty(rows, dtype=torch.float64, device=dev)
+                o.top_id = torch.empty((rows, wl.n_top), **i32)
+                o.top_logprob = torch.empty((rows, wl.n_top), dtype=torch.float32, device=dev)
+        argv = []
+        for i in range(nbuf):
+            a = _lib.SampleArgs()
+            a.logits = bufs[i].data_ptr()
+            a.rows, a.ld, a.width, a.enc = rows, V, V, V
+            a.params, a.uniforms = params.data_ptr(), u.data_ptr()
+            a.token, a.status = outs[i].token.data_ptr(), outs[i].status.data_ptr()
+            if "mask" in extra:
+                a.allowed = extra["mask"].data_ptr()
+                a.allowed_words = a.allowed_ld = wl.mask.shape[1]
+            if outs[i].top_id is not None:
+                a.row_max, a.row_lse = outs[i].row_max.data_ptr(), outs[i].row_lse.data_ptr()
+                a.n_top, a.top_ld = wl.n_top, wl.n_top
+                a.top_id, a.top_logprob = outs[i].top_id.data_ptr(), outs[i].top_logprob.data_ptr()
+            argv.append(a)
+        call = lib.xs_sample
+        token_of = lambda o: o.token
+    refs = [C.byref(a) for a in argv]
+    h = ctx.h
+
+    def step(i):
+        rc = call(h, refs[i % nbuf])
+        if rc:
+            raise RuntimeError(f"launch failed: {rc}")
+
+    status_of = (lambda o: o.row_status) if name == "c4" else (lambda o: o.status)
+    S = dict(wl=wl, rows=rows, ctx=ctx, step=step, outs=outs, alg_bytes=rows * row_bytes,
+             token_of=token_of, status_of=status_of, bufs=bufs, keep=(params, u, argv))
+    if name == "c4":
+        S["keep"] += (drafts,)
+    elif name == "c3":
+        S["keep"] += (extra["mask"],)
+    return S
+
+
+WORKLOAD_TEXT = {
+    "c2": "C2 batched sampling: 64 rows x V=248,320 fp32, T 0.7 / top_k 20 / top_p 0.80, "
+          "one uniform per row",
+    "c3": "C3 grammar-constrained sampling: 32 rows x V=248,320 fp32 + packed u32 allow-masks "
+          "(1% / 10% / 50% dense, one one-hot), T 1.0 / top_k 20 / top_p 0.95",
+    "c4": "C4 speculative verify: 16 sequences x 16 positions x V=248,320 fp32, 15 drafts each, "
+          "top_k 20 / top_p 0.95 / T 1.0, accept_drafts on the device",
+    "c5": "C5 heterogeneous batch: 256 rows x V=248,320 fp32 Student-t(3)x2, per-row T/k/p, "
+          "held_row max / logsumexp / top-20 log-probs",
+}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -98,6 +200,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES")
+    ap.add_argument("--workload", choices=["c2", "c3", "c4", "c5"], default="c2",
+                    help="c2 (default) is the headline configuration")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path "
@@ -116,40 +220,11 @@ def main() -> int:
     from xwen_amd import _lib
     from xwen_amd import sampler as xsm
 
-    log("generating the batch-64 workload")
-    wl = workloads.c2_batch()
-    rows, V = wl.logits.shape
     dev = torch.device("cuda:0")
-    ctx = xsm.Context(max_rows=rows, vocab=V)
-    bufs = []
-    base = torch.as_tensor(wl.logits).to(dev)
-    for i in range(args.nbuf):
-        bufs.append(base if i == 0 else base.clone())
-    params = xsm.params_tensor(wl.temperature, wl.top_k, wl.top_p, rows, dev)
-    u = torch.as_tensor(wl.u).to(dev)
-    outs = [xsm.Draws(token=torch.empty(rows, dtype=torch.int32, device=dev),
-                      status=torch.empty(rows, dtype=torch.int32, device=dev))
-            for _ in range(args.nbuf)]
     lib = _lib.load()
-
-    def make_args(i):
-        a = _lib.SampleArgs()
-        a.logits = bufs[i].data_ptr()
-        a.rows, a.ld, a.width, a.enc = rows, V, V, V
-        a.params = params.data_ptr()
-        a.uniforms = u.data_ptr()
-        a.token = outs[i].token.data_ptr()
-        a.status = outs[i].status.data_ptr()
-        return a
-
-    argv = [make_args(i) for i in range(args.nbuf)]
-    refs = [C.byref(a) for a in argv]
-    h = ctx.h
-
-    def step(i):
-        rc = lib.xs_sample(h, refs[i % args.nbuf])
-        if rc:
-            raise RuntimeError(f"xs_sample failed: {rc}")
+    S = setup(args.workload, args.nbuf, dev, torch, workloads, xsm, _lib, lib)
+    wl, rows, ctx, step, outs, alg_bytes = S["wl"], S["rows"], S["ctx"], S["step"], S["outs"], S["alg_bytes"]
+    V = wl.logits.shape[1]
 
     stream = torch.cuda.current_stream(dev)
     ctx.bind_current_stream()
@@ -157,7 +232,7 @@ def main() -> int:
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
-    st = outs[0].status.cpu().numpy()
+    st = S["status_of"](outs[0]).cpu().numpy()
     if st.any():
         raise RuntimeError(f"row errors in the warm-up batch: {st}")
 
@@ -208,17 +283,23 @@ def main() -> int:
     ms_total = t_start.elapsed_time(t_end)
     ms_step = ms_total / steps
     rows_per_s = rows / (ms_step / 1e3)
-    alg_bytes = rows * ROW_BYTES
     achieved = alg_bytes / (ms_step / 1e3) / 1e9
     log(f"{ms_step * 1e3:.2f} us/step, {rows_per_s / 1e6:.3f} M rows/s, {achieved:.0f} GB/s")
 
     # parity spot check of the timed outputs against the first warm-up batch
-    tok0 = outs[0].token.cpu().numpy()
+    tok0 = S["token_of"](outs[0]).cpu().numpy()
     for o in outs[1:]:
-        assert (o.token.cpu().numpy() == tok0).all(), "rotating buffers disagree"
+        assert (S["token_of"](o).cpu().numpy() == tok0).all(), "rotating buffers disagree"
 
+    headline = args.workload == "c2"
+    config = {"workload": WORKLOAD_TEXT[args.workload], "rows": rows, "vocab": V}
+    if headline:
+        config.update({"temperature": 0.7, "top_k": 20, "top_p": 0.8})
+    config.update({"launch": "hipGraph" if graph is not None else "eager",
+                   "rotating_buffers": args.nbuf, "buffer_bytes_total": args.nbuf * alg_bytes})
     result = {
-        "metric": "sampled rows/sec at V=248,320 batch 64 (1 GPU); achieved HBM GB/s vs peak",
+        "metric": ("sampled rows/sec at V=248,320 batch 64 (1 GPU); achieved HBM GB/s vs peak"
+                   if headline else f"sampled rows/sec at V=248,320, {args.workload.upper()} (1 GPU)"),
         "value": round(rows_per_s, 1),
         "unit": "rows/s",
         "n_gpus": 1,
@@ -229,22 +310,19 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp32",
-        "data": "synthetic (seeded numpy PCG64: N(0,2.5^2) + 8 spikes U(8,14) per row)",
-        "config": {"workload": "C2 batched sampling: 64 rows x V=248,320 fp32, T 0.7 / "
-                               "top_k 20 / top_p 0.80, one uniform per row",
-                   "rows": rows, "vocab": V, "temperature": 0.7, "top_k": 20, "top_p": 0.8,
-                   "launch": "hipGraph" if graph is not None else "eager",
-                   "rotating_buffers": args.nbuf,
-                   "buffer_bytes_total": args.nbuf * alg_bytes},
+        "data": ("synthetic (seeded numpy PCG64: N(0,2.5^2) + 8 spikes U(8,14) per row)"
+                 if headline else "synthetic (seeded numpy PCG64, tests/workloads.py)"),
+        "config": config,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic()},
+                     "traffic": measured_traffic() if headline else None},
     }
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and headline:
         log(f"CPU baseline (~{args.cpu_seconds:.0f} s)")
         result["cpu_baseline"] = cpu_baseline(wl, args.cpu_seconds)
     else:
         result["cpu_baseline"] = None
+    del S
     ctx.close()
     print(json.dumps(result), flush=True)
     del np

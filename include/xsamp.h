@@ -57,9 +57,7 @@ extern "C" {
  *   XS_ROW_BAD_PARAM   top_k larger than the context's k_max, or a control list
  *                      past XS_CTL_MAX entries (no reference counterpart: the
  *                      reference has no such limits)
- *   XS_ROW_INTERNAL    the device-side hand-off between a row's workgroups
- *                      read an incomplete record (never expected; reported
- *                      instead of returning a token computed from it)      */
+ *   XS_ROW_INTERNAL    reserved; this build never reports it               */
 #define XS_ROW_OK 0
 #define XS_ROW_NAN 1
 #define XS_ROW_NO_FINITE 2

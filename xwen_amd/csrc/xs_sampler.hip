@@ -6,14 +6,16 @@
 //
 //   chunk pass   every workgroup streams one chunk of one row from HBM exactly
 //                once (16-byte loads, one slot = 256 lanes x float4), applies
-//                the allow-mask, and reduces the chunk: max, NaN/finite flags,
-//                the softmax partial sum, the held_row f64 partial sum, and a
-//                candidate list that provably holds the chunk's K' best
-//                (logit desc, id asc) entries.  The candidate bound is the K'-th
-//                largest lane maximum of the block (lane maxima are distinct
-//                elements, so at least K' elements lie at or above it).
-//   finalize     the last workgroup of a row (atomic ticket) merges the chunk
-//                summaries and candidate lists, recomputes the exact f32
+//                the allow-mask and the sparse controls, and each wave reduces
+//                its share into a sub-record: max, NaN/finite flags, the
+//                softmax partial sum, the held_row f64 partial sum, and a
+//                candidate list that provably holds every element of the row's
+//                K' best (logit desc, id asc) that lies in the chunk.  The
+//                candidate bound is the K'-th largest maximum of the chunk's 64
+//                four-lane groups (distinct elements, so at least K' elements
+//                of the chunk lie at or above it).
+//   finalize     the last workgroup of a row (atomic arrival ticket) merges the
+//                sub-records, recomputes the exact f32
 //                probability of the K' = top_k + 1 survivors with a correctly
 //                rounded exp, orders them by (p desc, id asc) -- the
 //                reference's top_k_desc order -- proves the k-th boundary is
@@ -22,6 +24,10 @@
 //                reference's serial f32 top-p cut and WeightedIndex draw.
 //   verify       for a speculative block, the last row finalizer of a
 //                sequence runs accept_drafts over the sequence's rows.
+//   controls     a call with sparse controls first runs control_kernel (one
+//                workgroup per row), which turns the row's bans and biases into
+//                a sorted list of final values, and keeps the pulled and the
+//                forced values, for the chunk pass to apply.
 //
 // Exactness: every value that decides a token is computed with the reference's
 // own f32 operations in the reference's order (scale by (float)(1/T), subtract
@@ -552,11 +558,6 @@ struct FinLds {
   double expt[64];                  // kExpT, flattened
   uint32_t keys[GMAX * 64 * 4];     // published bound keys (more than 64 sub-records)
 };
-union Lds {
-  ChunkLds c;
-  FinLds f;
-};
-
 // p = rn(e / S) of one controlled logit v (the reference's softmax_in_place:
 // v *= inv unless T == 1, then exp(v - max), then / sum; sampler.rs:289-310).
 // T: the 2^(j/32) table (kExpT flattened), here the finalizer's LDS copy.
@@ -1756,18 +1757,25 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
   if (!cfg.bad) {
     const float tf = (tk <= KEY_NEG_INF) ? -__FLT_MAX__ : keyf(tk);
     uint64_t* const ent = sub + SHDR * nsp;  // entry p at ent[p * nsp]
+    // every slot's ballot first, so the branches below test values already in
+    // scalar registers instead of waiting on each compare
+    uint64_t sb[SPC];
+#pragma unroll
+    for (int j = 0; j < SPC; j++) sb[j] = __ballot(gm[j] >= tf);
 #pragma unroll
     for (int j = 0; j < SPC; j++) {
-      if (__ballot(gm[j] >= tf)) {
+      if (sb[j]) {
+        uint64_t eb[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) eb[e] = __ballot(q4(q[j], e) >= tf);
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-          const float x = q4(q[j], e);
-          const bool hit = x >= tf;
-          const uint64_t b = __ballot(hit);
-          if (b) {
-            const uint32_t pos = (uint32_t)cnt + (uint32_t)lanes_below(b);
+          if (eb[e]) {
+            const float x = q4(q[j], e);
+            const bool hit = (eb[e] >> lane) & 1ull;
+            const uint32_t pos = (uint32_t)cnt + (uint32_t)lanes_below(eb[e]);
             if (hit && pos < (uint32_t)CAPW) st_agent(ent + pos * (uint32_t)nsp, pack(fkey(x), (uint32_t)(base_id + j * SLOT + e)));
-            cnt += __popcll(b);
+            cnt += __popcll(eb[e]);
           }
         }
       }

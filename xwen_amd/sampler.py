@@ -48,7 +48,7 @@ ROW_STATUS_NAMES = {
     _lib.ROW_NARROW: "logit row is narrower than the encodable ids the sampler draws over",
     _lib.ROW_BAD_PARAM: "top_k exceeds the sampler context's k_max, or a control list "
                         "holds more than XS_CTL_MAX entries",
-    _lib.ROW_INTERNAL: "device hand-off read an incomplete record (internal error)",
+    _lib.ROW_INTERNAL: "internal error (reserved)",
 }
 
 

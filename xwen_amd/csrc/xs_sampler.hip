@@ -558,6 +558,13 @@ struct FinLds {
   double expt[64];                  // kExpT, flattened
   uint32_t keys[GMAX * 64 * 4];     // published bound keys (more than 64 sub-records)
 };
+// The chunk pass stages each wave's entries here before it publishes them;
+// after the hand-off only the row's last workgroup uses the memory again, as
+// its finalizer's.
+union TailLds {
+  uint64_t stage[NWAVE][CAPW];
+  FinLds fin;
+};
 // p = rn(e / S) of one controlled logit v (the reference's softmax_in_place:
 // v *= inv unless T == 1, then exp(v - max), then / sum; sampler.rs:289-310).
 // T: the 2^(j/32) table (kExpT flattened), here the finalizer's LDS copy.
@@ -1495,7 +1502,7 @@ XS_DEV void finalize_row(const Args& a, const Cfg& cfg, int row, const uint64_t*
 template <bool HAS_MASK, bool WANT_LSE, bool HAS_CTL>
 __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) void sample_kernel(Args a) {
   __shared__ ChunkLds Lc;
-  __shared__ FinLds Fl;
+  __shared__ TailLds Tl;
   const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
   const int nc = a.n_chunks;
   const int row = blockIdx.x / nc;
@@ -1754,9 +1761,10 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
   uint64_t* sub = rowrec + chunk * NWAVE + wave;
   const int base_id = s0 * SLOT + 4 * tid;
   int cnt = 0;
+  bool ovf = false;
+  uint64_t* const stg = Tl.stage[wave];
   if (!cfg.bad) {
     const float tf = (tk <= KEY_NEG_INF) ? -__FLT_MAX__ : keyf(tk);
-    uint64_t* const ent = sub + SHDR * nsp;  // entry p at ent[p * nsp]
     // every slot's ballot first, so the branches below test values already in
     // scalar registers instead of waiting on each compare
     uint64_t sb[SPC];
@@ -1774,24 +1782,41 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
             const float x = q4(q[j], e);
             const bool hit = (eb[e] >> lane) & 1ull;
             const uint32_t pos = (uint32_t)cnt + (uint32_t)lanes_below(eb[e]);
-            if (hit && pos < (uint32_t)CAPW) st_agent(ent + pos * (uint32_t)nsp, pack(fkey(x), (uint32_t)(base_id + j * SLOT + e)));
+            if (hit && pos < (uint32_t)CAPW) stg[pos] = pack(fkey(x), (uint32_t)(base_id + j * SLOT + e));
             cnt += __popcll(eb[e]);
           }
         }
       }
     }
-    if (cnt > CAPW) cnt = wave_overflow<HAS_MASK>(rowp, mrow, s0, ns, enc, sub, nsp, kp, tk);
+    if (cnt > CAPW) {  // the exact re-scan writes its entries straight to the sub-record
+      cnt = wave_overflow<HAS_MASK>(rowp, mrow, s0, ns, enc, sub, nsp, kp, tk);
+      ovf = true;
+    }
   }
 
-  // Publish the sub-record header.
-  if (lane == 0) {
-    st_agent(&sub[0 * nsp], (uint64_t)__double_as_longlong(P));
-    st_agent(&sub[1 * nsp], ((uint64_t)__float_as_uint(c_r) << 32) | __float_as_uint(c_w));
-    st_agent(&sub[2 * nsp], (uint64_t)__double_as_longlong(R));
-    st_agent(&sub[3 * nsp], ((uint64_t)flags << 32) | __float_as_uint(m_w));
-    st_agent(&sub[4 * nsp], (uint64_t)(uint32_t)cnt);
-    st_agent(&sub[5 * nsp], ((uint64_t)pub[1] << 32) | pub[0]);
-    st_agent(&sub[6 * nsp], ((uint64_t)pub[3] << 32) | pub[2]);
+  // Publish the sub-record: header word i and staged entry p go to words i
+  // and SHDR + p, one word per lane (an overflow wrote its entries itself).
+  {
+    const uint64_t w0 = (uint64_t)__double_as_longlong(P);
+    const uint64_t w1 = ((uint64_t)__float_as_uint(c_r) << 32) | __float_as_uint(c_w);
+    const uint64_t w2 = (uint64_t)__double_as_longlong(R);
+    const uint64_t w3 = ((uint64_t)flags << 32) | __float_as_uint(m_w);
+    const uint64_t w4 = (uint64_t)(uint32_t)cnt;
+    const uint64_t w5 = ((uint64_t)pub[1] << 32) | pub[0];
+    const uint64_t w6 = ((uint64_t)pub[3] << 32) | pub[2];
+    const int staged = ovf ? 0 : cnt;
+    wave_lds_sync();
+    for (int i = lane; i < SHDR + staged; i += 64) {
+      uint64_t v = w0;
+      v = i == 1 ? w1 : v;
+      v = i == 2 ? w2 : v;
+      v = i == 3 ? w3 : v;
+      v = i == 4 ? w4 : v;
+      v = i == 5 ? w5 : v;
+      v = i == 6 ? w6 : v;
+      if (i >= SHDR) v = stg[i - SHDR];
+      if (i != SHDR - 1) st_agent(sub + (uint32_t)i * (uint32_t)nsp, v);
+    }
   }
 
   // Hand-off: every wave's stores acknowledged, the workgroup takes the row's
@@ -1806,7 +1831,7 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
   }
   __syncthreads();
   if (!Lc.last || wave != 0) return;
-  finalize_row<HAS_MASK, WANT_LSE, HAS_CTL>(a, cfg, row, rowrec, nsp, nc * NWAVE, rowp, mrow, Fl);
+  finalize_row<HAS_MASK, WANT_LSE, HAS_CTL>(a, cfg, row, rowrec, nsp, nc * NWAVE, rowp, mrow, Tl.fin);
 }
 
 // ---------------------------------------------------------------------------

@@ -1,0 +1,97 @@
+"""One context across calls of different shapes, and xs_sample captured in a
+HIP graph and replayed: the arrival tickets are reset by each row's last
+workgroup inside the launch, so no call depends on memory a host-side fill
+would have to clear, and every replay must equal the eager call."""
+import numpy as np
+import pytest
+
+from tests import workloads
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+V = workloads.V
+
+
+def _call(ctx, x, T, K, P, U, **kw):
+    from xwen_amd import sampler as xsm
+    rows = x.shape[0]
+    lg = torch.as_tensor(x).cuda()
+    p = xsm.params_tensor(T, K, P, rows, "cuda")
+    u = torch.as_tensor(np.broadcast_to(np.float32(U), (rows,)).copy()).cuda()
+    out = xsm.sample_batch(ctx, lg, p, u, cand_k=20, stats=True, **kw)
+    torch.cuda.synchronize()
+    return {k: (None if v is None else v.cpu().numpy()) for k, v in vars(out).items()}
+
+
+def test_shapes_change_between_calls_on_one_context():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from xwen_amd import sampler as xsm
+    rng = np.random.default_rng(61)
+    shapes = [(64, V), (3, 1000), (17, 100_000), (1, 4), (64, V), (40, 65_536)]
+    batches = []
+    for rows, width in shapes:
+        x = rng.normal(0, 3, (rows, width)).astype(np.float32)
+        x[:, rng.integers(0, width, 3)] += np.float32(6.0)
+        batches.append(x)
+    shared = xsm.Context(max_rows=64, vocab=V)
+    shared.bind_current_stream()
+    got = [_call(shared, x, 0.8, 20, 0.9, 0.37) for x in batches]
+    shared.close()
+    for x, g in zip(batches, got):
+        fresh = xsm.Context(max_rows=64, vocab=V)
+        fresh.bind_current_stream()
+        want = _call(fresh, x, 0.8, 20, 0.9, 0.37)
+        fresh.close()
+        assert (g["status"] == 0).all()
+        for k in ("token", "status", "cand_id", "n_cand"):
+            assert (g[k] == want[k]).all(), k
+        assert (g["cand_w"].view(np.uint32) == want["cand_w"].view(np.uint32)).all()
+
+
+def test_graph_replays_match_the_eager_call():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from xwen_amd import sampler as xsm
+    wl = workloads.c2_batch(rows=32)
+    rows = wl.logits.shape[0]
+    ctx = xsm.Context(max_rows=64, vocab=V)
+    lg = torch.as_tensor(wl.logits).cuda()
+    p = xsm.params_tensor(wl.temperature, wl.top_k, wl.top_p, rows, "cuda")
+    u = torch.as_tensor(wl.u).cuda()
+    out = xsm.Draws(token=torch.empty(rows, dtype=torch.int32, device="cuda"),
+                    status=torch.empty(rows, dtype=torch.int32, device="cuda"),
+                    soft_sum=torch.empty(rows, dtype=torch.float32, device="cuda"),
+                    soft_max=torch.empty(rows, dtype=torch.float32, device="cuda"))
+    ctx.bind_current_stream()
+    xsm.sample_batch(ctx, lg, p, u, stats=True, out=out)
+    torch.cuda.synchronize()
+    want_tok = out.token.cpu().numpy().copy()
+    want_sum = out.soft_sum.cpu().numpy().copy()
+    assert (out.status.cpu().numpy() == 0).all()
+
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        ctx.bind_current_stream()
+        with torch.cuda.graph(g, stream=side):
+            ctx.bind_current_stream()
+            xsm.sample_batch(ctx, lg, p, u, stats=True, out=out)
+    ctx.bind_current_stream()
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(62)
+    for rep in range(5):
+        out.token.fill_(-7)
+        out.soft_sum.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert (out.token.cpu().numpy() == want_tok).all(), rep
+        assert (out.soft_sum.cpu().numpy().view(np.uint32) == want_sum.view(np.uint32)).all(), rep
+        # eager work of another shape on the same context between replays
+        x = rng.normal(0, 2, (5, 50_000)).astype(np.float32)
+        other = _call(ctx, x, 1.0, 20, 0.95, 0.5)
+        assert (other["status"] == 0).all()
+    ctx.close()

@@ -1,0 +1,91 @@
+"""The row's survivor bound and the finalizer's survivor sort across row shapes
+that stress them, against the CPU oracle: allow-masks of a few contiguous
+ranges (few sub-records hold a finite value, so the bound comes from each
+chunk's top group maxima rather than one key per sub-record), masks with
+fewer finite ids than K', and dense rows at K' = 64 and 65, whose survivors can
+outnumber one wave's lanes."""
+import numpy as np
+import pytest
+
+from tests import workloads
+from tests.test_gpu_sampler import check_rows, run_sample
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+V = workloads.V
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from xwen_amd import sampler as xsm
+    c = xsm.Context(max_rows=64, vocab=V)
+    c.bind_current_stream()
+    yield c
+    c.close()
+
+
+def _uniforms(rng, n):
+    return rng.integers(0, 1 << 23, n).astype(np.float32) * np.float32(2.0 ** -23)
+
+
+def test_range_masks(ctx, oracle):
+    rng = np.random.default_rng(81)
+    rows = 24
+    x = rng.standard_normal((rows, V), dtype=np.float32) * np.float32(3.0)
+    allow = np.zeros((rows, V), bool)
+    for r in range(rows):
+        n_ranges, width = [(1, 40), (2, 300), (4, V // 400), (8, 2000)][r % 4]
+        for _ in range(n_ranges):
+            s = int(rng.integers(0, V - width))
+            allow[r, s:s + width] = True
+    mask = workloads.pack_mask(allow)
+    K = np.array([20, 50, 63, 1, 40, 64] * 4)
+    T = np.array([1.0, 0.7, 1.3, 1.0] * 6)
+    P = np.array([0.95, 1.0, 0.9, 0.5, 1.0, 0.8] * 4)
+    U = _uniforms(rng, rows)
+    d = run_sample(ctx, x, T, K, P, U, mask=mask, cand_k=128)
+    assert (d["status"] == 0).all(), d["status"]
+    check_rows(oracle, x, T, K, P, U, d, mask=mask, margins=False, label="range masks")
+    for r in range(rows):
+        assert allow[r, d["token"][r]]
+
+
+def test_fewer_finite_ids_than_k(ctx, oracle):
+    """10 to 60 allowed ids scattered over the whole row, K' up to 64."""
+    rng = np.random.default_rng(82)
+    rows = 12
+    x = rng.standard_normal((rows, V), dtype=np.float32) * np.float32(3.0)
+    allow = np.zeros((rows, V), bool)
+    for r in range(rows):
+        allow[r, rng.choice(V, 10 + 5 * r, replace=False)] = True
+    mask = workloads.pack_mask(allow)
+    K = np.array([63, 20, 40, 64] * 3)
+    T = np.array([1.0] * 6 + [0.6] * 6)
+    P = np.array([1.0, 0.95, 0.9] * 4)
+    U = _uniforms(rng, rows)
+    d = run_sample(ctx, x, T, K, P, U, mask=mask, cand_k=128)
+    assert (d["status"] == 0).all(), d["status"]
+    check_rows(oracle, x, T, K, P, U, d, mask=mask, margins=False, label="sparse ids")
+
+
+def test_dense_rows_at_k64(ctx, oracle):
+    """K' = 64 (top_k 63) and 65 over N(0, s^2) rows of several spreads, and rows whose top
+    hundreds of logits sit in a narrow band: many survivors per row."""
+    rng = np.random.default_rng(83)
+    rows = 32
+    x = np.empty((rows, V), np.float32)
+    for r in range(rows):
+        x[r] = rng.standard_normal(V, dtype=np.float32) * np.float32([0.5, 1.0, 3.0, 8.0][r % 4])
+        if r % 8 == 7:  # a plateau: 300 ids within 1e-3 of each other at the top
+            ids = rng.choice(V, 300, replace=False)
+            x[r, ids] = np.float32(40.0) + rng.uniform(0, 1e-3, 300).astype(np.float32)
+    K = np.array([63, 63, 63, 64] * 8)
+    T = np.array([1.0, 0.8, 1.5, 1.0] * 8)
+    P = np.array([1.0, 0.99, 0.9, 1.0] * 8)
+    U = _uniforms(rng, rows)
+    d = run_sample(ctx, x, T, K, P, U, cand_k=128)
+    assert (d["status"] == 0).all(), d["status"]
+    check_rows(oracle, x, T, K, P, U, d, margins=False, label="dense k64")

@@ -729,7 +729,7 @@ XS_DEV double red_sumd(double v) {
 
 // ---------------------------------------------------------------------------
 // Row finalize, common case: at most 64 sub-records (one per lane), K' <= 64,
-// at most EPRE entries per sub-record, at most 64 survivors, and no boundary
+// at most SURV survivors, and no boundary
 // tie that needs the id-ordered row scan.  Returns false (having written
 // nothing) when the row is outside that case; the general finalizer then
 // does the row.  Same arithmetic, in the same order, as the general path.
@@ -767,12 +767,23 @@ XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, int nsub, const uin
   else if (cfg.greedy) st = nan_seen ? XS_ROW_NAN : (m_v == -INFINITY ? XS_ROW_NO_FINITE : XS_ROW_OK);
   else if (nan_seen || __builtin_isinf(m_s)) st = XS_ROW_NAN;
 
-  // Survivor bound: the K'-th largest published wave max.
+  // Survivor bound: the K'-th largest of the sub-records' first published
+  // keys; of all four when fewer than 2K' of the first are finite (a sparse
+  // mask), which would leave the first bound weak or absent.
   uint32_t tau = 0;
-  if (nsub >= kp) {
+  const int nfin = __popcll(__ballot(live && (uint32_t)h[5] > KEY_NEG_INF));
+  if (nfin >= 2 * kp) {
     uint32_t x[1] = {live ? (uint32_t)h[5] : 0u};
     wave_sort_desc<1>(x);
     tau = rdl(x[0], kp - 1);
+  } else if (4 * nsub >= kp) {
+    uint32_t x[4] = {live ? (uint32_t)h[5] : 0u, live ? (uint32_t)(h[5] >> 32) : 0u,
+                     live ? (uint32_t)h[6] : 0u, live ? (uint32_t)(h[6] >> 32) : 0u};
+    wave_sort_desc<4>(x);
+    const int i = kp - 1;
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+      if ((i >> 6) == r) tau = rdl(x[r], i & 63);
   }
   // Gather the survivors into LDS, then order them by rank: a survivor's
   // position is the number of survivors above it ((key, ~id) are distinct).
@@ -782,7 +793,7 @@ XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, int nsub, const uin
     const uint64_t b = __ballot(ok);
     if (b) {
       const int pos = M + lanes_below(b);
-      if (ok && pos < 64) F.list[pos] = e;
+      if (ok && pos < SURV) F.list[pos] = e;
       M += __popcll(b);
     }
   };
@@ -800,7 +811,7 @@ XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, int nsub, const uin
     int pos = incl - c;
 #pragma unroll
     for (int j = 0; j < EPRE; j++) {
-      if (ok[j] && pos < 64) F.list[pos] = E[j];
+      if (ok[j] && pos < SURV) F.list[pos] = E[j];
       pos += ok[j] ? 1 : 0;
     }
     M = (int)rdl((uint32_t)incl, 63);
@@ -814,16 +825,23 @@ XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, int nsub, const uin
 #pragma unroll
     for (int u = 0; u < 4; u++) put(e[u], j0 + u < cnt && e[u] >= floor_e);
   }
-  if (M > 64) return false;
+  if (M > SURV) return false;
   F.expt[lane] = et;
   wave_lds_sync();
-  const uint64_t xv = lane < M ? F.list[lane] : 0ull;
-  int rank = 0;
+  // rank by counting the survivors above, LDS broadcast reads
+  uint64_t sel;
+  if (M <= 64) {
+    const uint64_t xv = lane < M ? F.list[lane] : 0ull;
+    int rank = 0;
 #pragma unroll 8
-  for (int j = 0; j < M; j++) rank += (F.list[j] > xv) ? 1 : 0;  // LDS broadcast reads
-  if (lane < M) F.psel[rank] = xv;
-  wave_lds_sync();
-  const uint64_t sel = lane < M ? F.psel[lane] : 0ull;
+    for (int j = 0; j < M; j++) rank += (F.list[j] > xv) ? 1 : 0;
+    if (lane < M) F.srt[rank] = xv;
+    wave_lds_sync();
+    sel = lane < M ? F.srt[lane] : 0ull;
+  } else {
+    rank_sort_lds(F.list, F.srt, M);
+    sel = F.srt[lane];
+  }
   const int nsel = min(M, kp);
 
   // Probabilities of the selection (lanes < nsel) and, on lane nsel, of the
@@ -1032,11 +1050,11 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
   else if (nan_seen || __builtin_isinf(m_s)) st = XS_ROW_NAN;
 
   // Survivor bound: the K'-th largest of the published keys (distinct
-  // elements: wave maxima, or the chunks' top lane maxima when K' > 64).
+  // elements: each chunk's top group or lane maxima), as many per sub-record
+  // as one four-register sort holds.
   uint32_t tau_row = 0;
   {
-    int qk = 1;  // keys used per sub-record
-    if (kp > 64) qk = (G == 1) ? 4 : (nsub >= kp ? 1 : 2);
+    const int qk = (G == 1) ? 4 : (G == 2 ? 2 : 1);  // keys used per sub-record
     const int nv = qk * nsub;
     if (nv >= kp && !cfg.bad) {
       uint32_t x[4] = {0u, 0u, 0u, 0u};
@@ -1065,17 +1083,11 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
         for (int r = 0; r < 4; r++) x[r] = (r * 64 + lane < nv) ? F.keys[r * 64 + lane] : 0u;
         wave_lds_sync();
       }
-      if (G == 1 && qk == 1) {
-        uint32_t y[1] = {x[0]};
-        wave_sort_desc<1>(y);
-        tau_row = rdl(y[0], kp - 1);
-      } else {
-        wave_sort_desc<4>(x);
-        const int i = kp - 1;
+      wave_sort_desc<4>(x);
+      const int i = kp - 1;
 #pragma unroll
-        for (int r = 0; r < 4; r++)
-          if ((i >> 6) == r) tau_row = rdl(x[r], i & 63);
-      }
+      for (int r = 0; r < 4; r++)
+        if ((i >> 6) == r) tau_row = rdl(x[r], i & 63);
     }
   }
 
@@ -1717,14 +1729,20 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
   }
   __syncthreads();
   uint32_t tk = 0;
-  // Keys this sub-record publishes for the row's survivor bound: the wave max
-  // (K' <= 64), or the chunk's lane maxima of rank wave + 4r (K' > 64).
+  // Keys this sub-record publishes for the row's survivor bound, keys of
+  // distinct elements of the chunk: its group maxima (K' <= 64) or lane
+  // maxima (K' > 64) of rank wave + 4r, so the chunk's four sub-records hold
+  // its top 16.
   uint32_t pub[4] = {fkey(m_w), 0u, 0u, 0u};
   if (!cfg.bad) {
+    bool none = false;  // every element of the chunk is -inf: no entries at all
     if (kp <= 64) {  // the kp-th largest group max: a DPP bitonic sort of the 64
       uint32_t gv[1] = {Lc.groupmax[lane]};
       wave_sort_desc<1, true>(gv);
       tk = rdl(gv[0], kp - 1);
+      none = rdl(gv[0], 0) <= KEY_NEG_INF;
+#pragma unroll
+      for (int r = 0; r < 4; r++) pub[r] = rdl(gv[0], wave + 4 * r);
     }
     if (kp > 64) {
       uint32_t all[4];
@@ -1737,7 +1755,7 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
         if ((i >> 6) == r) tk = rdl(all[r], i & 63);
 #pragma unroll
       for (int r = 0; r < 4; r++) pub[r] = rdl(all[0], wave + 4 * r);
-    } else if (tk <= KEY_NEG_INF) {
+    } else if (tk <= KEY_NEG_INF && !none) {
       uint32_t all[4];
 #pragma unroll
       for (int r = 0; r < 4; r++) all[r] = Lc.lanemax[r * 64 + lane];

@@ -89,3 +89,32 @@ def test_dense_rows_at_k64(ctx, oracle):
     d = run_sample(ctx, x, T, K, P, U, cand_k=128)
     assert (d["status"] == 0).all(), d["status"]
     check_rows(oracle, x, T, K, P, U, d, margins=False, label="dense k64")
+
+
+def test_subnormal_boundary_ties(ctx, oracle):
+    """Rows whose k-th probability is subnormal: neighbouring logits round to
+    the same p, so the candidate set keeps the lowest ids of a p-tie that
+    reaches past the selection.  Heavy-tailed rows (Student-t(3) x 2, as C5),
+    and rows whose tied band sits mostly in one chunk, more than K' deep, so
+    that chunk's entries stop inside the band and its logits are read."""
+    rng = np.random.default_rng(84)
+    rows = 12
+    x = np.empty((rows, V), np.float32)
+    for r in range(8):
+        z = rng.standard_normal(V, dtype=np.float32)
+        chi = sum(rng.standard_normal(V, dtype=np.float32) ** 2 for _ in range(3))
+        x[r] = z / np.sqrt(chi / np.float32(3.0)) * np.float32(2.0)
+    for r in range(8, rows):
+        x[r] = rng.normal(-200.0, 1.0, V).astype(np.float32)
+        x[r, 5 + 1000 * r] = np.float32(0.0)
+        deep = 2 * 16384 + rng.choice(16384, 40, replace=False)      # chunk 2: 40 band values
+        light = 9 * 16384 + rng.choice(16384, 10, replace=False)     # chunk 9: 10 more
+        x[r, deep] = rng.uniform(-100.03, -100.0, 40).astype(np.float32)
+        x[r, light] = rng.uniform(-100.03, -100.0, 10).astype(np.float32)
+    T = np.array([1.0, 0.7, 1.3, 1.0, 1.0, 0.6, 1.0, 1.0, 1.0, 1.0, 1.0, 1.0])
+    K = np.array([20, 20, 50, 100, 5, 20, 63, 2, 20, 21, 10, 50])
+    P = np.array([0.95, 1.0, 0.95, 1.0, 1.0, 0.8, 1.0, 1.0, 1.0, 1.0, 0.999, 1.0])
+    U = _uniforms(rng, rows)
+    d = run_sample(ctx, x, T, K, P, U, cand_k=128)
+    assert (d["status"] == 0).all(), d["status"]
+    check_rows(oracle, x, T, K, P, U, d, margins=False, label="subnormal ties")

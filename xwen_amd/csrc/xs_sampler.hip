@@ -529,9 +529,12 @@ XS_DEV uint64_t pick64(const uint64_t (&x)[R], int i) {
 //       scaled, controlled logit (the softmax partial)
 //   w1  c_s (f32 bits) | c_r (f32 bits) << 32: the partials' offsets
 //   w2  R (f64 bits): sum of e^(v - c_r) over the raw logits (held_row)
-//   w3  wave max (f32 bits) | flags << 32
+//   w3  wave max (f32 bits) | flags << 32 (1 NaN seen, 2 a finite value
+//       seen, 4 entries in descending order)
 //   w4  entry count
 //   w5  bound keys 0 | 1 << 32;  w6  bound keys 2 | 3 << 32
+//   w7  the filter's floor (f32 bits): the entries are every element of the
+//       wave at or above it; +inf when they are not (an overflow)
 //   w8..  entries: pack(key, id) of the wave's candidates
 // A row has n_chunks * NWAVE sub-records, chunk-major, stored transposed:
 // word i of sub-record s sits at i * nsp + s of the row's block (nsp = the
@@ -543,6 +546,7 @@ constexpr int SRECW = SHDR + CAPW;
 constexpr int NHW = 7;              // header words the finalizer reads
 constexpr int EPRE = 16;            // entries per sub-record read with the headers
 constexpr int GMAX = 4;             // sub-record groups of 64 a finalizer handles
+constexpr int KGRP = 32;            // largest K' whose chunk bound comes from group maxima
 constexpr uint32_t KEY_NEG_INF = 0x007FFFFFu;  // fkey(-inf)
 constexpr double LN2D = 0.693147180559945309417;
 
@@ -748,7 +752,6 @@ XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, int nsub, const uin
   const uint32_t hf = live ? (uint32_t)(h[3] >> 32) : 0u;
   const bool nan_seen = __ballot(hf & 1u) != 0;
   const bool finite_seen = __ballot(hf & 2u) != 0;
-  const int maxc = __ballot(cnt > EPRE) ? red_maxi(cnt) : EPRE;
   const float m_s = cfg.scale ? m_v * cfg.inv : m_v;
   double part = 0.0, rpart = 0.0;
   if (live) {
@@ -816,14 +819,18 @@ XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, int nsub, const uin
     }
     M = (int)rdl((uint32_t)incl, 63);
   }
-  // entries past the preloaded ones (a sub-record holding more than EPRE)
+  // entries past the preloaded ones (a sub-record holding more than EPRE); in
+  // a sorted sub-record (flag 4) they end at the first one below the floor
+  const bool srt = (hf & 4u) != 0;
+  int lim = (srt && E[EPRE - 1] < floor_e) ? EPRE : cnt;
 #pragma unroll 1
-  for (int j0 = EPRE; j0 < maxc; j0 += 4) {
+  for (int j0 = EPRE; __ballot(j0 < lim); j0 += 4) {
     uint64_t e[4];
 #pragma unroll
-    for (int u = 0; u < 4; u++) e[u] = (j0 + u < cnt) ? ld_agent(rowrec + (int64_t)(SHDR + j0 + u) * nsp + lane) : 0ull;
+    for (int u = 0; u < 4; u++) e[u] = (j0 + u < lim) ? ld_agent(rowrec + (int64_t)(SHDR + j0 + u) * nsp + lane) : 0ull;
 #pragma unroll
-    for (int u = 0; u < 4; u++) put(e[u], j0 + u < cnt && e[u] >= floor_e);
+    for (int u = 0; u < 4; u++) put(e[u], j0 + u < lim && e[u] >= floor_e);
+    if (srt && j0 + 3 < lim && e[3] < floor_e) lim = j0;
   }
   if (M > SURV) return false;
   F.expt[lane] = et;
@@ -1005,20 +1012,16 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
 
   float mv = -INFINITY;
   uint32_t fw = 0;
-  int maxc = 0;
 #pragma unroll
   for (int g = 0; g < GMAX; g++) {
     if (has(g)) {
-      const uint64_t h3 = hdr(g, 3), h4 = hdr(g, 4);
+      const uint64_t h3 = hdr(g, 3);
       mv = fmaxf(mv, __uint_as_float((uint32_t)h3));
       fw |= (uint32_t)(h3 >> 32);
-      maxc = max(maxc, (int)min((uint32_t)h4, (uint32_t)CAPW));
     }
   }
   const float m_v = wave_maxf(mv);
   const uint32_t fl = wave_or(fw);
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) maxc = max(maxc, xor_lane(maxc, o));
   const float m_s = cfg.scale ? m_v * cfg.inv : m_v;
   double S_d = 0.0, R_d = 0.0;
 #pragma unroll
@@ -1102,14 +1105,17 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
       M += __popcll(b);
     }
   };
-  auto gather_global = [&](int s, int c, int j0, uint64_t fl_e) __attribute__((always_inline)) {
-    // entries j0..c-1 of sub-record s, read from the workspace
-    for (int j = j0; j < maxc; j += 4) {
+  auto gather_global = [&](int s, int c, bool srt, uint64_t fl_e) __attribute__((always_inline)) {
+    // the c entries of sub-record s, read from the workspace; in a sorted
+    // sub-record (flag 4) they end at the first one below the floor
+    int lim = c;
+    for (int j = 0; __ballot(j < lim); j += 4) {
       uint64_t e[4];
 #pragma unroll
-      for (int u = 0; u < 4; u++) e[u] = (j + u < c) ? ld_agent(rr + (int64_t)(SHDR + j + u) * nsp + s) : 0ull;
+      for (int u = 0; u < 4; u++) e[u] = (j + u < lim) ? ld_agent(rr + (int64_t)(SHDR + j + u) * nsp + s) : 0ull;
 #pragma unroll
-      for (int u = 0; u < 4; u++) put(e[u], j + u < c && e[u] >= fl_e);
+      for (int u = 0; u < 4; u++) put(e[u], j + u < lim && e[u] >= fl_e);
+      if (srt && j + 3 < lim && e[3] < fl_e) lim = j;
     }
   };
   auto gather = [&](uint64_t fl_e) __attribute__((always_inline)) {
@@ -1117,7 +1123,10 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
 #pragma unroll
     for (int g = 0; g < GMAX; g++) {
       const int s = g * 64 + lane;
-      if (g < G) gather_global(s, has(g) ? (int)min((uint32_t)hdr(g, 4), (uint32_t)CAPW) : 0, 0, fl_e);
+      if (g < G) {
+        const uint64_t h3 = hdr(g, 3), h4 = hdr(g, 4);
+        gather_global(s, has(g) ? (int)min((uint32_t)h4, (uint32_t)CAPW) : 0, ((h3 >> 32) & 4u) != 0, fl_e);
+      }
     }
   };
   if (!cfg.bad) gather(floor_e);
@@ -1237,10 +1246,137 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
         // exact test, outside it every element provably misses
         const double lo_p = Pk == 0.0f ? 0.0 : 0.5 * ((double)Pk + (double)__uint_as_float(__float_as_uint(Pk) - 1u));
         const double hi_p = 0.5 * ((double)Pk + (double)__uint_as_float(__float_as_uint(Pk) + 1u));
-        const double elo = lo_p * (double)S * (1.0 - 0x1p-10), ehi = hi_p * (double)S * (1.0 + 0x1p-10) + 0x1p-148;
-        const float x_lo = elo > 0x1p-100 ? (float)(log(elo) - 0x1p-8) : -INFINITY;
+        // (e = rn(exp(d)) is within 2^-24 e, or 2^-150 where subnormal, of
+        // exp(d); rn(e / S) == P_k needs lo_p <= e / S <= hi_p, and P_k > 0
+        // needs e > 0, so exp(d) > 2^-150)
+        const double elo = Pk == 0.0f ? 0.0 : fmax(lo_p * (double)S * (1.0 - 0x1p-10) - 0x1p-148, 0x1p-150);
+        const double ehi = hi_p * (double)S * (1.0 + 0x1p-10) + 0x1p-148;
+        const float x_lo = elo > 0.0 ? (float)(log(elo) - 0x1p-8) : -INFINITY;
         const float x_hi = (float)(log(ehi) + 0x1p-8);
         int need = k - g, have = g;
+        auto dv = [&](float x) __attribute__((always_inline)) { return (cfg.scale ? x * cfg.inv : x) - m_s; };
+        if (Pk > 0.0f) {
+          // From the workspace first: a sub-record's entries are all of its
+          // elements at or above its filter floor (header word 7), so all of
+          // its band elements when the floor lies below the band; the other
+          // sub-records' logits are read, in id order, until the ties found
+          // below the next chunk's first id number `need` (not for a
+          // controlled row: only the row scan below rebuilds controlled
+          // values).  The list keeps ~id, so its descending order is id order;
+          // when it fills, only its `need` lowest ids are kept.
+          int nt = 0;
+          auto compact = [&]() __attribute__((always_inline)) {
+            wave_lds_sync();
+            rank_sort_lds(F.list, F.srt, nt);
+#pragma unroll
+            for (int r = 0; r < 2; r++)
+              if (r * 64 + lane < need) F.list[r * 64 + lane] = F.srt[r * 64 + lane];
+            wave_lds_sync();
+            nt = min(nt, need);
+          };
+          auto push = [&](bool hit, uint32_t id) __attribute__((always_inline)) {
+            const uint64_t b = __ballot(hit);
+            if (b) {
+              if (nt + __popcll(b) > SURV) compact();
+              const int pos = nt + lanes_below(b);
+              if (hit) F.list[pos] = (uint64_t)(0xFFFFFFFFu - id);
+              nt += __popcll(b);
+            }
+          };
+          uint64_t inc[GMAX];  // sub-records whose entries may miss band elements
+#pragma unroll
+          for (int g2 = 0; g2 < GMAX; g2++) {
+            inc[g2] = 0ull;
+            if (g2 < G) {
+              const int s = g2 * 64 + lane;
+              const uint64_t h3 = hdr(g2, 3), h4 = hdr(g2, 4), h7 = hdr(g2, 7);
+              const float fx = __uint_as_float((uint32_t)h7);
+              const bool complete = !has(g2) || fx == -__FLT_MAX__ || dv(fx) < x_lo;
+              inc[g2] = __ballot(!complete);
+              const bool srt = ((h3 >> 32) & 4u) != 0;
+              int lim = (complete && has(g2)) ? (int)min((uint32_t)h4, (uint32_t)CAPW) : 0;
+              for (int j = 0; __ballot(j < lim); j += 4) {
+                uint64_t e[4];
+#pragma unroll
+                for (int u = 0; u < 4; u++) e[u] = (j + u < lim) ? ld_agent(rr + (int64_t)(SHDR + j + u) * nsp + s) : 0ull;
+                uint32_t hb = 0;  // bit u: entry j + u ties
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                  const float x = keyf(pk_key(e[u]));
+                  const float d = dv(x);
+                  if (j + u < lim && d >= x_lo && d <= x_hi && exact_p(x, cfg, m_s, S, T) == Pk) hb |= 1u << u;
+                }
+                if (srt && j + 3 < lim && dv(keyf(pk_key(e[3]))) < x_lo) lim = j;  // the rest lie below
+                while (__ballot(hb != 0u)) {
+                  const int u = hb ? (int)__builtin_ctz(hb) : 0;
+                  const uint64_t eu = u == 0 ? e[0] : u == 1 ? e[1] : u == 2 ? e[2] : e[3];
+                  push(hb != 0u, pk_id(eu));
+                  hb &= hb - 1u;
+                }
+              }
+            }
+          }
+          const bool ok = !(ctl_on && ((inc[0] | inc[1] | inc[2] | inc[3]) != 0ull));
+          int cur = -1;  // chunk of the last sub-record read
+          bool enough = !ok;
+#pragma unroll
+          for (int g2 = 0; g2 < GMAX; g2++) {
+            uint64_t m = inc[g2];
+            while (m && !enough) {  // one sub-record's logits: wave w of chunk c, as the chunk pass read them
+              const int s = g2 * 64 + (int)__builtin_ctzll(m);
+              m &= m - 1ull;
+              const int c = s / NWAVE, w = s % NWAVE, s0 = c * SPC;
+              if (c != cur) {  // every tie below chunk c's first id is known: enough of them?
+                cur = c;
+                const uint32_t lim_id = (uint32_t)s0 * SLOT;
+                int below = 0;
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                  if (r * 64 + lane < nt) below += (0xFFFFFFFFu - (uint32_t)F.list[r * 64 + lane]) < lim_id ? 1 : 0;
+                enough = wave_sumi(below) >= need;
+                if (enough) break;
+              }
+#pragma unroll 1
+              for (int j0 = 0; j0 < SPC; j0 += 4) {  // four slots at a time
+                float4 v[4];
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                  const int id0 = (s0 + j0 + j) * SLOT + 4 * (w * 64 + lane);
+                  v[j] = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+                  if (id0 < enc) v[j] = reinterpret_cast<const float4*>(rowp)[id0 >> 2];
+                }
+                uint32_t hb = 0u;  // bit 4j + e: element e of slot j0 + j ties
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                  const int id0 = (s0 + j0 + j) * SLOT + 4 * (w * 64 + lane);
+                  const float xv[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+                  for (int e = 0; e < 4; e++) {
+                    const int id = id0 + e;
+                    bool hit = id < enc;
+                    if (HAS_MASK && hit && !((mrow[id >> 5] >> (id & 31)) & 1u)) hit = false;
+                    const float d = dv(xv[e]);
+                    if (hit && d >= x_lo && d <= x_hi && exact_p(xv[e], cfg, m_s, S, T) == Pk) hb |= 1u << (4 * j + e);
+                  }
+                }
+                while (__ballot(hb != 0u)) {
+                  const int t = hb ? (int)__builtin_ctz(hb) : 0;
+                  push(hb != 0u, (uint32_t)((s0 + j0 + (t >> 2)) * SLOT + 4 * (w * 64 + lane) + (t & 3)));
+                  hb &= hb - 1u;
+                }
+              }
+            }
+          }
+          if (ok && nt >= need) {
+            wave_lds_sync();
+            rank_sort_lds(F.list, F.srt, nt);
+            const uint64_t pkb = (uint64_t)__float_as_uint(Pk + 0.0f) << 32;
+#pragma unroll
+            for (int r = 0; r < 2; r++)
+              if (r * 64 + lane < need) F.psel[have + r * 64 + lane] = pkb | (uint32_t)F.srt[r * 64 + lane];
+            need = 0;  // done: the row scan below does not run
+          }
+        }
         int sc = 0;  // next patch (the list is sorted by id, as the scan runs)
         const uint64_t* pl = HAS_CTL ? a.patch + (int64_t)row * CTL_MAX : nullptr;
         for (int base = 0; base < enc && need > 0; base += 256) {
@@ -1715,11 +1851,13 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
   }
 
   // Candidate bound: the K'-th largest of a set of distinct chunk elements, so
-  // at least K' elements of the chunk lie at or above it.  For K' <= 64 the set
-  // is the 64 maxima of 4-lane groups (each group holds 4 x 64 logits); for
-  // K' > 64, or when fewer than K' groups hold a finite value, it is all 256
-  // lane maxima.  Every wave finds it for itself (no second barrier), by a
-  // bitwise search: the largest key with at least K' members at or above it.
+  // at least K' elements of the chunk lie at or above it.  For K' <= KGRP the
+  // set is the 64 maxima of 4-lane groups (each group holds 4 x 64 logits);
+  // for larger K' it is the 256 lane maxima, whose K'-th passes fewer
+  // elements than the group maxima's would.  Every wave finds it for itself
+  // (no second barrier) with a DPP bitonic sort; when fewer than K' groups
+  // hold a finite value, by a bitwise search over the lane maxima: the
+  // largest key with at least K' of them at or above it.
   const uint32_t km = fkey(mr);
   {
     uint32_t g = max(km, xor_u32(km, 1));
@@ -1730,13 +1868,13 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
   __syncthreads();
   uint32_t tk = 0;
   // Keys this sub-record publishes for the row's survivor bound, keys of
-  // distinct elements of the chunk: its group maxima (K' <= 64) or lane
-  // maxima (K' > 64) of rank wave + 4r, so the chunk's four sub-records hold
-  // its top 16.
+  // distinct elements of the chunk: its group maxima (K' <= KGRP) or lane
+  // maxima (K' > KGRP) of rank wave + 4r, so the chunk's four sub-records
+  // hold its top 16.
   uint32_t pub[4] = {fkey(m_w), 0u, 0u, 0u};
   if (!cfg.bad) {
     bool none = false;  // every element of the chunk is -inf: no entries at all
-    if (kp <= 64) {  // the kp-th largest group max: a DPP bitonic sort of the 64
+    if (kp <= KGRP) {  // the kp-th largest group max: a DPP bitonic sort of the 64
       uint32_t gv[1] = {Lc.groupmax[lane]};
       wave_sort_desc<1, true>(gv);
       tk = rdl(gv[0], kp - 1);
@@ -1744,7 +1882,7 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
 #pragma unroll
       for (int r = 0; r < 4; r++) pub[r] = rdl(gv[0], wave + 4 * r);
     }
-    if (kp > 64) {
+    if (kp > KGRP) {  // the kp-th largest lane max: a sort of the 256
       uint32_t all[4];
 #pragma unroll
       for (int r = 0; r < 4; r++) all[r] = Lc.lanemax[r * 64 + lane];
@@ -1781,8 +1919,8 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
   int cnt = 0;
   bool ovf = false;
   uint64_t* const stg = Tl.stage[wave];
+  const float tf = (tk <= KEY_NEG_INF) ? -__FLT_MAX__ : keyf(tk);  // the filter's floor
   if (!cfg.bad) {
-    const float tf = (tk <= KEY_NEG_INF) ? -__FLT_MAX__ : keyf(tk);
     // every slot's ballot first, so the branches below test values already in
     // scalar registers instead of waiting on each compare
     uint64_t sb[SPC];
@@ -1811,6 +1949,16 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
       ovf = true;
     }
   }
+  // More entries than the finalizer preloads (EPRE), at most 64: stored in
+  // descending order (flag 4), so the finalizer reads past the preloaded ones
+  // only while they reach its bound.
+  if (!ovf && cnt > EPRE && cnt <= 64) {
+    wave_lds_sync();
+    uint64_t v[1] = {lane < cnt ? stg[lane] : 0ull};
+    wave_sort_desc64<1>(v);
+    if (lane < cnt) stg[lane] = v[0];
+    flags |= 4u;
+  }
 
   // Publish the sub-record: header word i and staged entry p go to words i
   // and SHDR + p, one word per lane (an overflow wrote its entries itself).
@@ -1822,6 +1970,7 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
     const uint64_t w4 = (uint64_t)(uint32_t)cnt;
     const uint64_t w5 = ((uint64_t)pub[1] << 32) | pub[0];
     const uint64_t w6 = ((uint64_t)pub[3] << 32) | pub[2];
+    const uint64_t w7 = __float_as_uint(ovf || cfg.bad ? INFINITY : tf);
     const int staged = ovf ? 0 : cnt;
     wave_lds_sync();
     for (int i = lane; i < SHDR + staged; i += 64) {
@@ -1832,8 +1981,9 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
       v = i == 4 ? w4 : v;
       v = i == 5 ? w5 : v;
       v = i == 6 ? w6 : v;
+      v = i == 7 ? w7 : v;
       if (i >= SHDR) v = stg[i - SHDR];
-      if (i != SHDR - 1) st_agent(sub + (uint32_t)i * (uint32_t)nsp, v);
+      st_agent(sub + (uint32_t)i * (uint32_t)nsp, v);
     }
   }
 

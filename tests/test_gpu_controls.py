@@ -177,3 +177,57 @@ def test_verify_with_per_position_controls(ctx):
     for s in range(3):
         assert list(com[s]) == list(drafts[s]) + [123]
     assert list(com[3][:2]) == list(drafts[3][:2]) and com[3][2] != drafts[3][2]
+
+
+@pytest.mark.parametrize("greedy", [False, True])
+def test_controls_on_flat_rows(ctx, oracle, greedy):
+    """Rows of one repeated value, so more than 256 of a wave's elements tie at
+    the chunk bound and the chunk pass re-scans the wave exactly; the re-scan
+    must see the banned, biased and pulled values, not the raw ones."""
+    from xwen_amd import sampler as xsm
+    S = xsm.SampleControl
+    n = 8
+    x = np.zeros((n, V), np.float32)
+    x[2] = np.float32(1.0)
+    x[3, : V // 2] = np.float32(2.0)
+    x[5] = np.float32(-3.5)
+    ctls = [
+        S(banned=list(range(10))),                          # the lowest ids banned
+        S(bias=[(50, -1.0), (7000, 0.5), (7001, 0.5)]),     # two raised ids tie on top
+        S(bias=[(5, -2.0), (6, -2.0)], pull=(6, 0.5)),      # a pull half way back up
+        S(banned=list(range(0, 200, 2))),                   # every other id of the plateau's start
+        S(banned=list(range(2000))),                        # 2,000 bans: all of chunk 0's first slots
+        S(banned=[1, 3], bias=[(0, -0.25)]),
+        S(banned=list(range(1024, 1100))),                  # a block of bans in slot 1
+        None,
+    ]
+    T = 0.0 if greedy else np.array([1.0, 0.7, 1.0, 1.3, 1.0, 0.8, 1.0, 1.0])
+    K = np.array([20, 20, 50, 20, 1 if greedy else 64, 20, 30, 20])
+    P = np.array([1.0, 0.9, 0.95, 1.0, 1.0, 0.5, 1.0, 0.9])
+    rng = np.random.default_rng(41 + greedy)
+    U = rng.integers(0, 1 << 23, n).astype(np.float32) * np.float32(2.0 ** -23)
+    d = run_sample(ctx, x, T, K, P, U, ctls=ctls, cand_k=64)
+    assert (d["status"] == 0).all(), d["status"]
+    check_rows(oracle, x, T, K, P, U, d, ctls=ctls, margins=False, label=f"flat controls greedy={greedy}")
+    for r, c in enumerate(ctls):
+        if c is not None and c.banned:
+            assert d["token"][r] not in set(c.banned)
+
+
+def test_controls_on_flat_rows_with_an_allow_mask(ctx, oracle):
+    from xwen_amd import sampler as xsm
+    S = xsm.SampleControl
+    n = 4
+    x = np.zeros((n, V), np.float32)
+    allow = np.zeros((n, V), bool)
+    allow[0, 5:] = True
+    allow[1, ::3] = True
+    allow[2, 100:5000] = True
+    allow[3, :] = True
+    mask = workloads.pack_mask(allow)
+    ctls = [S(banned=[5, 6, 7]), S(bias=[(3, -1.0), (9, 0.25)]), S(banned=list(range(100, 140))), S(pull=(77, 1.0))]
+    T, K, P = np.array([1.0, 0.0, 1.0, 0.7]), np.array([20, 20, 40, 20]), np.array([1.0, 1.0, 0.9, 0.95])
+    U = np.array([0.1, 0.0, 0.6, 0.9], np.float32)
+    d = run_sample(ctx, x, T, K, P, U, mask=mask, ctls=ctls, cand_k=64)
+    assert (d["status"] == 0).all(), d["status"]
+    check_rows(oracle, x, T, K, P, U, d, mask=mask, ctls=ctls, margins=False, label="flat controls + mask")

@@ -608,31 +608,88 @@ XS_DEV float q4(const v4f& q, int e) { return e == 0 ? q.x : e == 1 ? q.y : e ==
 // elements: every key above a threshold key, then the lowest ids equal to it.
 // The threshold is the bound when fewer than K' keys lie strictly above it,
 // else the wave's K'-th largest key (bisection).  Elements that are -inf or
-// NaN never become candidates.  Re-reads the wave's elements from memory, so
-// the streaming path keeps no registers for it.  Returns the count.
-template <bool HAS_MASK>
-XS_DEV int wave_overflow(const float* rowp, const uint32_t* mrow, int s0, int ns,
-                                          int enc, uint64_t* sub, int nsp, int kp, uint32_t tk) {
+// NaN never become candidates.  Re-reads the wave's elements from memory (the
+// streaming pass's registers are free by then) and masks and controls them as
+// that pass did, so a controlled row's bans and biases count here as they do
+// in the filter.  Returns the count.
+// The chunk's sparse controls as the streaming pass applies them.
+struct ChunkCtl {
+  const uint64_t* pl;  // the row's patch list, (id << 32) | final value bits, by id
+  int p0, p1;          // this chunk's patches
+  int pull, force;     // ids, or -1
+  float pull_val, force_val;
+};
+
+template <bool HAS_MASK, bool HAS_CTL>
+XS_DEV int wave_overflow(const float* rowp, const uint32_t* mrow, int s0, int ns, int enc,
+                         uint64_t* sub, int nsp, int kp, uint32_t tk, const ChunkCtl& cc) {
+  constexpr int H = SPC / 2;  // slots per round of loads
   const int tid = threadIdx.x;
-  // element e of this lane's float4 in slot j, controlled; -inf when absent
-  auto elem = [&](int j, int e) __attribute__((always_inline)) -> float {
-    const int id = (s0 + j) * SLOT + 4 * tid + e;
-    if (j >= ns || id >= enc) return -INFINITY;
-    float x = rowp[id];
-    if (HAS_MASK && !((mrow[id >> 5] >> (id & 31)) & 1u)) x = -INFINITY;
-    return x;
+  // Slots h*H .. h*H+H-1 of the wave's elements as the streaming pass saw
+  // them (masked, controlled, -inf where absent), re-read with one round of
+  // loads; pc is the patch cursor, consumed in slot order.
+  auto load = [&](int h, v4f (&xv)[H], int& pc) __attribute__((always_inline)) {
+    uint32_t mw[H];
+#pragma unroll
+    for (int u = 0; u < H; u++) {
+      const int j = h * H + u;
+      const int id0 = (s0 + j) * SLOT + 4 * tid;
+      const bool in = j < ns && id0 < enc;
+      xv[u] = v4f{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+      if (in) xv[u] = *reinterpret_cast<const v4f*>(rowp + id0);
+      mw[u] = (HAS_MASK && in) ? mrow[id0 >> 5] >> (id0 & 31) : 0xFu;
+    }
+#pragma unroll
+    for (int u = 0; u < H; u++) {
+      const int j = h * H + u;
+      const int id0 = (s0 + j) * SLOT + 4 * tid;
+      float x[4] = {xv[u].x, xv[u].y, xv[u].z, xv[u].w};
+#pragma unroll
+      for (int e = 0; e < 4; e++)
+        if (j >= ns || id0 + e >= enc || (HAS_MASK && !((mw[u] >> e) & 1u))) x[e] = -INFINITY;
+      if (HAS_CTL && j < ns) {
+        const int sb = (s0 + j) * SLOT;
+        if (cc.force >= 0) {
+#pragma unroll
+          for (int e = 0; e < 4; e++) x[e] = (id0 + e == cc.force) ? cc.force_val : -INFINITY;
+        } else {
+          while (pc < cc.p1) {
+            const uint64_t pe = cc.pl[pc];
+            const int off = (int)(uint32_t)(pe >> 32) - sb;
+            if (off >= SLOT) break;
+            if ((off >> 2) == tid) {
+              const float pv = __uint_as_float((uint32_t)pe);
+#pragma unroll
+              for (int e = 0; e < 4; e++) x[e] = ((off & 3) == e) ? pv : x[e];
+            }
+            pc++;
+          }
+          const int pt = cc.pull - sb;
+          if (pt >= 0 && pt < SLOT && (pt >> 2) == tid) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) x[e] = ((pt & 3) == e) ? cc.pull_val : x[e];
+          }
+        }
+      }
+      xv[u] = v4f{x[0], x[1], x[2], x[3]};
+    }
   };
   auto valid = [](float x) __attribute__((always_inline)) { return x == x && x > -INFINITY; };
   auto count = [&](uint32_t key, bool strict) __attribute__((always_inline)) -> int {
-    int c = 0;
+    int c = 0, pc = cc.p0;
 #pragma unroll 1
-    for (int j = 0; j < SPC; j++)
-#pragma unroll 1
-      for (int e = 0; e < 4; e++) {
-        const float x = elem(j, e);
-        const uint32_t k = fkey(x);
-        c += (valid(x) && (strict ? k > key : k >= key)) ? 1 : 0;
-      }
+    for (int h = 0; h < 2; h++) {
+      v4f xv[H];
+      load(h, xv, pc);
+#pragma unroll
+      for (int u = 0; u < H; u++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const float x = q4(xv[u], e);
+          const uint32_t k = fkey(x);
+          c += (valid(x) && (strict ? k > key : k >= key)) ? 1 : 0;
+        }
+    }
     return wave_sumi(c);
   };
   uint32_t eq = max(tk, fkey(-__FLT_MAX__));
@@ -645,42 +702,64 @@ XS_DEV int wave_overflow(const float* rowp, const uint32_t* mrow, int s0, int ns
     }
     eq = ans;
   }
+  // everything above eq, in slot order
   int n = 0;
+  {
+    int pc = cc.p0;
 #pragma unroll 1
-  for (int j = 0; j < SPC; j++)
-#pragma unroll 1
-    for (int e = 0; e < 4; e++) {
-      const float x = elem(j, e);
-      const bool hit = valid(x) && fkey(x) > eq;
-      const uint64_t b = __ballot(hit);
-      const int pos = n + lanes_below(b);
-      if (hit && pos < CAPW) st_agent(&sub[(int64_t)(SHDR + pos) * nsp], pack(fkey(x), (uint32_t)((s0 + j) * SLOT + 4 * tid + e)));
-      n += __popcll(b);
+    for (int h = 0; h < 2; h++) {
+      v4f xv[H];
+      load(h, xv, pc);
+#pragma unroll
+      for (int u = 0; u < H; u++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const float x = q4(xv[u], e);
+          const bool hit = valid(x) && fkey(x) > eq;
+          const uint64_t b = __ballot(hit);
+          if (b) {
+            const int pos = n + lanes_below(b);
+            if (hit && pos < CAPW) st_agent(&sub[(int64_t)(SHDR + pos) * nsp], pack(fkey(x), (uint32_t)((s0 + h * H + u) * SLOT + 4 * tid + e)));
+            n += __popcll(b);
+          }
+        }
     }
+  }
   n = min(n, CAPW);
   // ties at eq, lowest ids first: slot j covers ids (s0 + j) * SLOT in lane order
   int need = kp - n;
+  {
+    int pc = cc.p0;
 #pragma unroll 1
-  for (int j = 0; j < SPC && need > 0; j++) {
-    bool t[4];
-    int c = 0;
+    for (int h = 0; h < 2 && need > 0; h++) {
+      v4f xv[H];
+      load(h, xv, pc);
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
-      const float x = elem(j, e);
-      t[e] = valid(x) && fkey(x) == eq;
-      c += t[e] ? 1 : 0;
-    }
-    const int incl = wave_incl_scan(c);
-    int pos = incl - c;
+      for (int u = 0; u < H; u++) {
+        if (need > 0) {
+          bool t[4];
+          int c = 0;
 #pragma unroll
-    for (int e = 0; e < 4; e++)
-      if (t[e]) {
-        if (pos < need && n + pos < CAPW) st_agent(&sub[(int64_t)(SHDR + n + pos) * nsp], pack(eq, (uint32_t)((s0 + j) * SLOT + 4 * tid + e)));
-        pos++;
+          for (int e = 0; e < 4; e++) {
+            const float x = q4(xv[u], e);
+            t[e] = valid(x) && fkey(x) == eq;
+            c += t[e] ? 1 : 0;
+          }
+          const int incl = wave_incl_scan(c);
+          int pos = incl - c;
+#pragma unroll
+          for (int e = 0; e < 4; e++)
+            if (t[e]) {
+              if (pos < need && n + pos < CAPW)
+                st_agent(&sub[(int64_t)(SHDR + n + pos) * nsp], pack(eq, (uint32_t)((s0 + h * H + u) * SLOT + 4 * tid + e)));
+              pos++;
+            }
+          const int tot = (int)rdl((uint32_t)incl, 63);
+          n += min(tot, need);
+          need -= tot;
+        }
       }
-    const int tot = (int)rdl((uint32_t)incl, 63);
-    n += min(tot, need);
-    need -= tot;
+    }
   }
   return min(n, CAPW);
 }
@@ -1696,6 +1775,7 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
     ctl_force = cr.force_id;
     ctl_fval = cr.force_val;
   }
+  const int pc0 = pc;  // the chunk's first patch
 
   // Online reduction, one float4 at a time, branch-free.  The softmax partial
   // is summed in the reference's scaled domain, s = v * inv rounded to f32 as
@@ -1945,7 +2025,8 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
       }
     }
     if (cnt > CAPW) {  // the exact re-scan writes its entries straight to the sub-record
-      cnt = wave_overflow<HAS_MASK>(rowp, mrow, s0, ns, enc, sub, nsp, kp, tk);
+      const ChunkCtl cc{pl, pc0, phi, ctl_pull, ctl_force, ctl_pval, ctl_fval};
+      cnt = wave_overflow<HAS_MASK, HAS_CTL>(rowp, mrow, s0, ns, enc, sub, nsp, kp, tk, cc);
       ovf = true;
     }
   }

@@ -967,7 +967,7 @@ XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, int nsub, const uin
         slow = other || pbelow == Pk;
       }
       if (slow && Pk == 0.0f && !want_cands) slow = false;
-      if (slow) return false;  // ties at P_k: the general path scans the row
+      if (slow) return false;  // ties at P_k: the general path resolves them
     }
 
     // The draw (truncate_top_p, then WeightedIndex), serial f32: lane i
@@ -1066,10 +1066,10 @@ XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, int nsub, const uin
 
 // ---------------------------------------------------------------------------
 // Row finalize, general case (the rows fin_fast leaves): any number of
-// sub-records up to GMAX * 64, K' up to KSEL, survivors past 64, entries past
-// EPRE, and the id-ordered scan for probability ties at the top-k boundary.
-// Lane l handles sub-records l + 64g.  Out of line: it is rare, and inlined
-// it would cost the streaming path registers.
+// sub-records up to GMAX * 64, K' up to KSEL, survivors past SURV, sparse
+// controls, and probability ties at the top-k boundary.  Lane l handles
+// sub-records l + 64g.  Headers and entries are read from the workspace
+// where they are used, so the common path keeps its register budget.
 template <bool HAS_MASK, bool WANT_LSE, bool HAS_CTL>
 XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* rowrec,
                         int nsp, int nsub, const float* rowp, const uint32_t* mrow, const CtlRow& cr,
@@ -1315,7 +1315,7 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
       if (slow && Pk == 0.0f && !want_cands) slow = false;
       if (slow) {
         // the candidates are every selected entry with p > P_k, then the lowest
-        // ids of the whole row with p == P_k, found by an id-ordered scan
+        // ids of the whole row with p == P_k
         F.psel[lane] = pk[0];
         F.psel[64 + lane] = pk[1];
         int g = 0;

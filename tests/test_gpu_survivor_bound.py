@@ -118,3 +118,31 @@ def test_subnormal_boundary_ties(ctx, oracle):
     d = run_sample(ctx, x, T, K, P, U, cand_k=128)
     assert (d["status"] == 0).all(), d["status"]
     check_rows(oracle, x, T, K, P, U, d, margins=False, label="subnormal ties")
+
+
+def test_draws_inside_runs_of_equal_probability(ctx, oracle):
+    """K' > 64 (the general finalizer) on rows whose top 140 logits are
+    consecutive floats below 0.25 on scattered ids: neighbouring logits round
+    to the same p, so the (p desc, id asc) order differs from the logit order
+    inside runs that carry real weight.  With no candidate list requested the
+    finalizer leaves that order to the draw; with one it sorts.  Many
+    uniforms per row land draws inside the runs; tokens against the oracle."""
+    rng = np.random.default_rng(85)
+    base = rng.normal(-20.0, 1.0, V).astype(np.float32)
+    vals = [np.float32(0.25)]
+    for _ in range(139):
+        vals.append(np.nextafter(vals[-1], np.float32(-1.0)))
+    ids = rng.choice(V, 140, replace=False)
+    row = base.copy()
+    row[ids] = np.array(vals, np.float32)
+    rows = 32
+    x = np.repeat(row[None, :], rows, axis=0)
+    T = np.where(np.arange(rows) % 4 == 3, 0.9, 1.0)
+    K = np.where(np.arange(rows) % 2 == 0, 100, 127)
+    P = np.where(np.arange(rows) % 3 == 0, 0.9, 1.0)
+    U = ((np.arange(rows) + 0.5) / rows).astype(np.float32)
+    U = (np.floor(U * (1 << 23)) * 2.0 ** -23).astype(np.float32)
+    for cand_k in (0, 128):
+        d = run_sample(ctx, x, T, K, P, U, cand_k=cand_k)
+        assert (d["status"] == 0).all(), d["status"]
+        check_rows(oracle, x, T, K, P, U, d, margins=False, label=f"equal-p runs cand_k={cand_k}")

@@ -1068,12 +1068,12 @@ XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, int nsub, const uin
 // Row finalize, general case (the rows fin_fast leaves): any number of
 // sub-records up to GMAX * 64, K' up to KSEL, survivors past SURV, sparse
 // controls, and probability ties at the top-k boundary.  Lane l handles
-// sub-records l + 64g.  Headers and entries are read from the workspace
-// where they are used, so the common path keeps its register budget.
+// sub-records l + 64g; group 0's header words and first EPRE entries are the
+// ones finalize_row preloaded, the rest are read where they are used.
 template <bool HAS_MASK, bool WANT_LSE, bool HAS_CTL>
 XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* rowrec,
                         int nsp, int nsub, const float* rowp, const uint32_t* mrow, const CtlRow& cr,
-                        FinLds& F) {
+                        const uint64_t (&h)[NHW], const uint64_t (&E)[EPRE], FinLds& F) {
   const int lane = lane_id();
   const int kp = cfg.kp, enc = (int)a.enc;
   const bool stoch = !cfg.greedy && !cfg.bad;
@@ -1081,11 +1081,14 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
   const int G = (nsub + 63) >> 6;
   const float u_row = a.greedy_all ? 0.0f : a.uniforms[row];  // prefetched for the draw
   const double et = (&kExpT[0][0])[lane];  // the exp table, staged into LDS below
-  // Headers and entries are read from the workspace where they are used
-  // (this path is rare; holding them in registers would cost the kernel's
-  // common path its register budget).
   auto has = [&](int g) __attribute__((always_inline)) { return g < G && g * 64 + lane < nsub; };
   auto hdr = [&](int g, int i) __attribute__((always_inline)) -> uint64_t {
+    if (g == 0 && i < NHW) {  // sub-records 0..63: the words finalize_row preloaded
+      uint64_t v = h[0];
+#pragma unroll
+      for (int t = 1; t < NHW; t++) v = i == t ? h[t] : v;
+      return has(0) ? v : 0ull;
+    }
     return has(g) ? ld_agent(&rr[i * nsp + g * 64 + lane]) : 0ull;
   };
 
@@ -1184,11 +1187,18 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
       M += __popcll(b);
     }
   };
-  auto gather_global = [&](int s, int c, bool srt, uint64_t fl_e) __attribute__((always_inline)) {
-    // the c entries of sub-record s, read from the workspace; in a sorted
-    // sub-record (flag 4) they end at the first one below the floor
-    int lim = c;
-    for (int j = 0; __ballot(j < lim); j += 4) {
+  auto gather_global = [&](int g, int s, int c, bool srt, uint64_t fl_e) __attribute__((always_inline)) {
+    // the c entries of sub-record s (the first EPRE of group 0 preloaded, the
+    // rest read from the workspace); in a sorted sub-record (flag 4) they end
+    // at the first one below the floor
+    int lim = c, j = 0;
+    if (g == 0) {
+#pragma unroll
+      for (int u = 0; u < EPRE; u++) put(E[u], u < lim && E[u] >= fl_e);
+      if (srt && EPRE - 1 < lim && E[EPRE - 1] < fl_e) lim = EPRE;
+      j = EPRE;
+    }
+    for (; __ballot(j < lim); j += 4) {
       uint64_t e[4];
 #pragma unroll
       for (int u = 0; u < 4; u++) e[u] = (j + u < lim) ? ld_agent(rr + (int64_t)(SHDR + j + u) * nsp + s) : 0ull;
@@ -1204,7 +1214,7 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
       const int s = g * 64 + lane;
       if (g < G) {
         const uint64_t h3 = hdr(g, 3), h4 = hdr(g, 4);
-        gather_global(s, has(g) ? (int)min((uint32_t)h4, (uint32_t)CAPW) : 0, ((h3 >> 32) & 4u) != 0, fl_e);
+        gather_global(g, s, has(g) ? (int)min((uint32_t)h4, (uint32_t)CAPW) : 0, ((h3 >> 32) & 4u) != 0, fl_e);
       }
     }
   };
@@ -1249,6 +1259,7 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
   // same pass, by the lane just past the selection
   const float vL = nsel > 0 ? keyf(pk_key(F.srt[nsel - 1])) : -INFINITY;
   float pbelow = 0.0f;
+  bool lazy_order = false;  // the (p desc, id asc) repair left to the draw
   if (stoch && st == XS_ROW_OK) {
     const bool need_below = !cfg.full && vL != -INFINITY;
 #pragma unroll
@@ -1284,7 +1295,12 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
     const uint64_t first1 = shfl64(pk[1], 0);
     if (lane + 1 < nsel && pk[0] < (lane < 63 ? n0 : first1)) bad = true;
     if (64 + lane + 1 < nsel && pk[1] < n1) bad = true;
-    if (__ballot(bad)) {
+    // Without a candidate list only the drawn entry's id needs the repaired
+    // order: permuting a run of equal p leaves the weight sequence, and so
+    // top-p and the draw's index, unchanged.  The draw then picks the id at
+    // its index within the run (run_pick below) instead of sorting here.
+    lazy_order = __ballot(bad) != 0 && !want_cands;
+    if (__ballot(bad) && !lazy_order) {
       F.psel[lane] = pk[0];
       F.psel[64 + lane] = pk[1];
       wave_lds_sync();
@@ -1607,6 +1623,28 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
           const int idx = (int)__popcll(__ballot(lane < k - 1 && cum0 <= x_draw)) +
                           (int)__popcll(__ballot(64 + lane < k - 1 && cum1 <= x_draw));
           tok = (int)pk_id(pick64(pk, idx));
+          if (lazy_order) {
+            // entries < k with the drawn entry's p: a contiguous run [lo, hi);
+            // the id at position idx of its (id asc) order is the (idx - lo)-th
+            // smallest id of the run, found by bisection over id bits
+            const uint32_t pi = (uint32_t)(pick64(pk, idx) >> 32);
+            const uint32_t ph0 = (uint32_t)(pk[0] >> 32), ph1 = (uint32_t)(pk[1] >> 32);
+            const bool in0 = lane < k, in1 = 64 + lane < k;
+            const int lo = (int)__popcll(__ballot(in0 && ph0 > pi)) + (int)__popcll(__ballot(in1 && ph1 > pi));
+            const int hi = (int)__popcll(__ballot(in0 && ph0 >= pi)) + (int)__popcll(__ballot(in1 && ph1 >= pi));
+            if (hi - lo > 1) {
+              const bool r0 = in0 && ph0 == pi, r1 = in1 && ph1 == pi;
+              const uint32_t i0 = pk_id(pk[0]), i1 = pk_id(pk[1]);
+              const int t = idx - lo;
+              uint32_t y = 0;  // the largest y with at most t run ids below it
+              for (int bit = 30; bit >= 0; bit--) {
+                const uint32_t c = y | (1u << bit);
+                const int n = (int)__popcll(__ballot(r0 && i0 < c)) + (int)__popcll(__ballot(r1 && i1 < c));
+                if (n <= t) y = c;
+              }
+              tok = (int)y;
+            }
+          }
         }
       }
     }
@@ -1678,7 +1716,7 @@ XS_DEV void finalize_row(const Args& a, const Cfg& cfg, int row, const uint64_t*
   if (HAS_CTL) cr = a.ctl_row[row];
   const bool done = !(HAS_CTL && cr.active) && nsub <= 64 && cfg.kp <= 64 && !cfg.bad &&
                     fin_fast<HAS_MASK, WANT_LSE>(a, cfg, row, nsub, h, E, rowrec, nsp, F);
-  if (!done) fin_general<HAS_MASK, WANT_LSE, HAS_CTL>(a, cfg, row, rowrec, nsp, nsub, rowp, mrow, cr, F);
+  if (!done) fin_general<HAS_MASK, WANT_LSE, HAS_CTL>(a, cfg, row, rowrec, nsp, nsub, rowp, mrow, cr, h, E, F);
 
   if (a.span > 0) {
     drain();  // this row's token and status are acknowledged

@@ -1241,12 +1241,25 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
   F.expt[lane] = et;
   wave_lds_sync();
 
-  // Sort the survivors (logit desc, id asc); the first K' are the selection.
-  rank_sort_lds(F.list, F.srt, min(M, SURV));
+  // Sort the survivors (logit desc, id asc); the first K' are the selection:
+  // up to 128 by a bitonic sort in registers, more by rank in LDS.
   const int nsel = min(M, kp);  // == kp unless the row holds fewer finite values
   uint64_t sel[2];
+  uint64_t last_sel;  // the K'-th survivor
+  if (M <= 128) {
+    uint64_t x[2];
 #pragma unroll
-  for (int r = 0; r < 2; r++) sel[r] = (r * 64 + lane < nsel) ? F.srt[r * 64 + lane] : 0ull;
+    for (int r = 0; r < 2; r++) x[r] = (r * 64 + lane < M) ? F.list[r * 64 + lane] : 0ull;  // entries are > 0
+    wave_sort_desc64<2>(x);
+#pragma unroll
+    for (int r = 0; r < 2; r++) sel[r] = (r * 64 + lane < nsel) ? x[r] : 0ull;
+    last_sel = nsel > 0 ? pick64(x, nsel - 1) : 0ull;
+  } else {
+    rank_sort_lds(F.list, F.srt, min(M, SURV));
+#pragma unroll
+    for (int r = 0; r < 2; r++) sel[r] = (r * 64 + lane < nsel) ? F.srt[r * 64 + lane] : 0ull;
+    last_sel = nsel > 0 ? F.srt[nsel - 1] : 0ull;
+  }
 
   // Probabilities of the selection and the (p desc, id asc) order; p is
   // non-increasing along the logit order, so only runs of equal p move.
@@ -1257,7 +1270,7 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
   const double* T = F.expt;
   // the value the boundary proof needs, p(next_below(vL)), is computed in the
   // same pass, by the lane just past the selection
-  const float vL = nsel > 0 ? keyf(pk_key(F.srt[nsel - 1])) : -INFINITY;
+  const float vL = nsel > 0 ? keyf(pk_key(last_sel)) : -INFINITY;
   float pbelow = 0.0f;
   bool lazy_order = false;  // the (p desc, id asc) repair left to the draw
   if (stoch && st == XS_ROW_OK) {

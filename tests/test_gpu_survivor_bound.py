@@ -146,3 +146,34 @@ def test_draws_inside_runs_of_equal_probability(ctx, oracle):
         d = run_sample(ctx, x, T, K, P, U, cand_k=cand_k)
         assert (d["status"] == 0).all(), d["status"]
         check_rows(oracle, x, T, K, P, U, d, margins=False, label=f"equal-p runs cand_k={cand_k}")
+
+
+@pytest.mark.parametrize("background", ["flat", "normal"])
+def test_thousands_of_subnormal_ties(ctx, oracle, background):
+    """One dominant logit and thousands of logits whose p rounds to the
+    smallest subnormal, packed into two chunks (their filter floors lie inside
+    the tied band, so both chunks' logits are read): the tie list fills and
+    keeps its lowest ids, and the read stops once the ties below the next
+    chunk's first id are enough.  On a flat background every wave overflows
+    (its entries are then incomplete, so every chunk's logits are read); on a
+    normal one the other chunks' entries are complete."""
+    rng = np.random.default_rng(86)
+    rows = 4
+    if background == "flat":
+        x = np.full((rows, V), np.float32(-200.0))
+    else:
+        x = rng.normal(-200.0, 1.0, (rows, V)).astype(np.float32)
+    for r in range(rows):
+        x[r, 5 + r] = np.float32(0.0)
+        c1 = 16384 + rng.choice(16384, 500, replace=False)
+        c3 = 3 * 16384 + rng.choice(16384, 3000, replace=False)
+        x[r, c1] = rng.uniform(-103.7, -103.3, 500).astype(np.float32)
+        x[r, c3] = rng.uniform(-103.7, -103.3, 3000).astype(np.float32)
+    T = np.ones(rows)
+    K = np.array([127, 100, 64, 127])
+    P = np.ones(rows)
+    U = np.array([0.0, 0.5, 0.999, 0.25], np.float32)
+    for cand_k in (128, 0):
+        d = run_sample(ctx, x, T, K, P, U, cand_k=cand_k)
+        assert (d["status"] == 0).all(), d["status"]
+        check_rows(oracle, x, T, K, P, U, d, margins=False, label=f"subnormal ties {background} cand_k={cand_k}")

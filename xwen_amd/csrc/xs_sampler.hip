@@ -1437,6 +1437,7 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
               if (c != cur) {  // every tie below chunk c's first id is known: enough of them?
                 cur = c;
                 const uint32_t lim_id = (uint32_t)s0 * SLOT;
+                wave_lds_sync();
                 int below = 0;
 #pragma unroll
                 for (int r = 0; r < 4; r++)

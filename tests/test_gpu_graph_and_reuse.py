@@ -95,3 +95,81 @@ def test_graph_replays_match_the_eager_call():
         other = _call(ctx, x, 1.0, 20, 0.95, 0.5)
         assert (other["status"] == 0).all()
     ctx.close()
+
+
+def test_verify_graph_replays_match_the_eager_call():
+    """xs_verify captured and replayed: the row and sequence tickets are reset
+    inside the launch, so every replay walks the drafts as the eager call."""
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from xwen_amd import sampler as xsm
+    wl = workloads.c4_verify(seqs=4)
+    rows = wl.seqs * wl.span
+    ctx = xsm.Context(max_rows=64, vocab=V)
+    lg = torch.as_tensor(wl.logits).cuda()
+    p = xsm.params_tensor(wl.temperature, wl.top_k, wl.top_p, rows, "cuda")
+    u = torch.as_tensor(wl.u).cuda()
+    dr = torch.as_tensor(wl.drafts).cuda()
+    ctx.bind_current_stream()
+    out = xsm.verify_batch(ctx, lg, wl.seqs, wl.span, p, u, dr, eog=[248046])
+    torch.cuda.synchronize()
+    want = {k: v.cpu().numpy().copy() for k, v in vars(out).items()}
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        ctx.bind_current_stream()
+        with torch.cuda.graph(g, stream=side):
+            ctx.bind_current_stream()
+            xsm.verify_batch(ctx, lg, wl.seqs, wl.span, p, u, dr, eog=[248046], out=out)
+    ctx.bind_current_stream()
+    torch.cuda.synchronize()
+    for rep in range(4):
+        out.accepted.fill_(-5)
+        out.committed.fill_(-5)
+        out.row_token.fill_(-5)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for k, v in vars(out).items():
+            assert (v.cpu().numpy() == want[k]).all(), (rep, k)
+        # an eager sample call of another shape on the same context in between
+        x = np.random.default_rng(rep).normal(0, 2, (3, 70_000)).astype(np.float32)
+        assert (_call(ctx, x, 1.0, 20, 0.9, 0.5)["status"] == 0).all()
+    ctx.close()
+
+
+def test_two_contexts_on_two_streams_run_concurrently():
+    """Each context owns its workspace and tickets: launches on two streams at
+    once give the same results as one after the other."""
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from xwen_amd import sampler as xsm
+    wa, wb = workloads.c2_batch(rows=64), workloads.c5_heterogeneous(rows=64)
+    ca, cb = xsm.Context(max_rows=64, vocab=V), xsm.Context(max_rows=64, vocab=V)
+    sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+
+    def launch(ctx, wl, stream):
+        with torch.cuda.stream(stream):
+            ctx.bind_current_stream()
+            lg = torch.as_tensor(wl.logits).cuda()
+            p = xsm.params_tensor(wl.temperature, wl.top_k, wl.top_p, 64, "cuda")
+            u = torch.as_tensor(wl.u).cuda()
+            outs = [xsm.sample_batch(ctx, lg, p, u, cand_k=32, stats=True) for _ in range(6)]
+        return outs, (lg, p, u)
+
+    seq_a, _ka = launch(ca, wa, sa)
+    torch.cuda.synchronize()
+    seq_b, _kb = launch(cb, wb, sb)
+    torch.cuda.synchronize()
+    con_a, _kc = launch(ca, wa, sa)
+    con_b, _kd = launch(cb, wb, sb)
+    torch.cuda.synchronize()
+    for seq, con in ((seq_a, con_a), (seq_b, con_b)):
+        ref = seq[0]
+        for o in seq + con:
+            assert (o.token.cpu() == ref.token.cpu()).all()
+            assert (o.cand_id.cpu() == ref.cand_id.cpu()).all()
+            assert (o.soft_sum.cpu().view(torch.int32) == ref.soft_sum.cpu().view(torch.int32)).all()
+    ca.close()
+    cb.close()

@@ -891,9 +891,11 @@ XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, int nsub, const uin
     }
     const int incl = wave_incl_scan(c);
     int pos = incl - c;
+    uint64_t* const spare = &F.srt[lane];  // non-survivors write here: no exec-mask branches
 #pragma unroll
     for (int j = 0; j < EPRE; j++) {
-      if (ok[j] && pos < SURV) F.list[pos] = E[j];
+      uint64_t* const dst = (ok[j] && pos < SURV) ? &F.list[pos] : spare;
+      *dst = E[j];
       pos += ok[j] ? 1 : 0;
     }
     M = (int)rdl((uint32_t)incl, 63);

@@ -18,8 +18,9 @@ Prints one JSON line (rank 0, N = 1):
 
 `--workload c3|c4|c5` times the other measured configurations the same way
 (masked rows, a speculative verify block through xs_verify, a heterogeneous
-256-row batch with held_row statistics); their lines carry no cpu_baseline and
-no traffic figure.  The default (c2) is the headline line.
+256-row batch with held_row statistics); their lines carry no traffic figure.
+The default (c2) is the headline line.  `--cpu-threads N` runs the CPU
+baseline N rows at a time (its `cores`).
 """
 from __future__ import annotations
 
@@ -42,20 +43,40 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def cpu_baseline(wl, seconds: float) -> dict:
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown CPU"
+
+
+def cpu_baseline(name: str, wl, seconds: float, threads: int) -> dict:
     """Time the oracle (libm expf, serial f32 sums: the reference's control-path
-    arithmetic) on the workload's rows, one thread, for about `seconds`."""
+    arithmetic) on the workload's rows for about `seconds`, `threads` rows at a
+    time: the mask for c3, the accept_drafts walks for c4, held_row for c5."""
     import numpy as np
 
     from oracle import oracle as o
     o.build()
     o.set_exp_mode(1)
-    rows = wl.logits.shape[0]
+    rows, V = wl.logits.shape
+    mask = wl.mask if name == "c3" else None
     done, reps = 0, 0
     t0 = time.perf_counter()
     while True:
-        o.sample_rows(wl.logits, wl.logits.shape[1], wl.temperature, wl.top_k, wl.top_p, wl.u,
-                      sum_mode=o.SUM_SEQ_F32, nthreads=1)
+        d = o.sample_rows(wl.logits, V, wl.temperature, wl.top_k, wl.top_p, wl.u, mask=mask,
+                          sum_mode=o.SUM_SEQ_F32, nthreads=threads)
+        if name == "c4":
+            tok = d["token"]
+            for q in range(wl.seqs):
+                t = tok[q * wl.span:(q + 1) * wl.span]
+                o.accept_drafts(list(wl.drafts[q]), 1 << 62, list(t), [False] * wl.span)
+        if name == "c5":
+            for r in range(rows):
+                o.held_row(wl.logits[r], V)
         done += rows
         reps += 1
         if time.perf_counter() - t0 >= seconds:
@@ -63,9 +84,12 @@ def cpu_baseline(wl, seconds: float) -> dict:
     dt = time.perf_counter() - t0
     o.set_exp_mode(0)
     del np
-    return {"value": round(done / dt, 2), "unit": "rows/s", "cores": 1, "kind": "port",
-            "sample": f"{reps} passes over the {rows} batch rows (V=248,320), 1 thread, "
-                      f"oracle control path with libm expf, {dt:.1f} s"}
+    extra = {"c3": " + allow-masks", "c4": " + the accept_drafts walks",
+             "c5": " + held_row (serial)"}.get(name, "")
+    return {"value": round(done / dt, 2), "unit": "rows/s", "cores": threads, "kind": "port",
+            "sample": f"{reps} passes over the {rows} rows of {name.upper()} (V=248,320){extra}, "
+                      f"{threads} thread{'s' if threads > 1 else ''} of {os.cpu_count()} "
+                      f"({cpu_model()}), oracle control path with libm expf, {dt:.1f} s"}
 
 
 def measured_traffic() -> int | None:
@@ -199,6 +223,8 @@ def main() -> int:
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of a hipGraph")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-threads", type=int, default=1,
+                    help="rows the CPU baseline samples at once (one per thread)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES")
     ap.add_argument("--workload", choices=["c2", "c3", "c4", "c5"], default="c2",
                     help="c2 (default) is the headline configuration")
@@ -317,9 +343,9 @@ def main() -> int:
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic() if headline else None},
     }
-    if not args.no_cpu_baseline and headline:
-        log(f"CPU baseline (~{args.cpu_seconds:.0f} s)")
-        result["cpu_baseline"] = cpu_baseline(wl, args.cpu_seconds)
+    if not args.no_cpu_baseline:
+        log(f"CPU baseline (~{args.cpu_seconds:.0f} s, {args.cpu_threads} thread(s))")
+        result["cpu_baseline"] = cpu_baseline(args.workload, wl, args.cpu_seconds, args.cpu_threads)
     else:
         result["cpu_baseline"] = None
     del S

@@ -125,8 +125,11 @@ def setup(name, nbuf, dev, torch, workloads, xsm, _lib, lib) -> dict:
     import numpy as np
 
     log(f"generating the {name} workload")
-    wl = {"c2": workloads.c2_batch, "c3": workloads.c3_masked, "c4": workloads.c4_verify,
+    wl = {"c1": workloads.c1_single, "c1g": lambda: workloads.c1_single(greedy=True),
+          "c2": workloads.c2_batch, "c3": workloads.c3_masked, "c4": workloads.c4_verify,
           "c5": workloads.c5_heterogeneous}[name]()
+    if name in ("c1", "c1g"):  # one 1 MB row: rotate enough copies to leave the Infinity Cache
+        nbuf = max(nbuf, 300)
     rows, V = wl.logits.shape
     ctx = xsm.Context(max_rows=rows, vocab=V)
     base = torch.as_tensor(wl.logits).to(dev)
@@ -194,7 +197,7 @@ def setup(name, nbuf, dev, torch, workloads, xsm, _lib, lib) -> dict:
 
     status_of = (lambda o: o.row_status) if name == "c4" else (lambda o: o.status)
     S = dict(wl=wl, rows=rows, ctx=ctx, step=step, outs=outs, alg_bytes=rows * row_bytes,
-             token_of=token_of, status_of=status_of, bufs=bufs, keep=(params, u, argv))
+             token_of=token_of, status_of=status_of, bufs=bufs, keep=(params, u, argv), nbuf=nbuf)
     if name == "c4":
         S["keep"] += (drafts,)
     elif name == "c3":
@@ -203,6 +206,10 @@ def setup(name, nbuf, dev, torch, workloads, xsm, _lib, lib) -> dict:
 
 
 WORKLOAD_TEXT = {
+    "c1": "C1 single-row decode: 1 row x V=248,320 fp32, T 1.0 / top_k 20 / top_p 0.95 "
+          "(latency per row; 300 rotating copies)",
+    "c1g": "C1 single-row greedy decode: 1 row x V=248,320 fp32, T 0 (latency per row; "
+           "300 rotating copies)",
     "c2": "C2 batched sampling: 64 rows x V=248,320 fp32, T 0.7 / top_k 20 / top_p 0.80, "
           "one uniform per row",
     "c3": "C3 grammar-constrained sampling: 32 rows x V=248,320 fp32 + packed u32 allow-masks "
@@ -226,8 +233,8 @@ def main() -> int:
     ap.add_argument("--cpu-threads", type=int, default=1,
                     help="rows the CPU baseline samples at once (one per thread)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES")
-    ap.add_argument("--workload", choices=["c2", "c3", "c4", "c5"], default="c2",
-                    help="c2 (default) is the headline configuration")
+    ap.add_argument("--workload", choices=["c1", "c1g", "c2", "c3", "c4", "c5"], default="c2",
+                    help="c2 (default) is the headline configuration; c1/c1g one row (latency)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path "
@@ -264,7 +271,8 @@ def main() -> int:
 
     use_graph = not args.no_graph
     graph = None
-    per_graph = args.nbuf * 20
+    nbuf = S["nbuf"]
+    per_graph = nbuf * 20 if nbuf <= 10 else nbuf  # every graph replay cycles all copies
     if use_graph:
         try:
             g = torch.cuda.CUDAGraph()
@@ -322,7 +330,7 @@ def main() -> int:
     if headline:
         config.update({"temperature": 0.7, "top_k": 20, "top_p": 0.8})
     config.update({"launch": "hipGraph" if graph is not None else "eager",
-                   "rotating_buffers": args.nbuf, "buffer_bytes_total": args.nbuf * alg_bytes})
+                   "rotating_buffers": nbuf, "buffer_bytes_total": nbuf * alg_bytes})
     result = {
         "metric": ("sampled rows/sec at V=248,320 batch 64 (1 GPU); achieved HBM GB/s vs peak"
                    if headline else f"sampled rows/sec at V=248,320, {args.workload.upper()} (1 GPU)"),

@@ -12,16 +12,22 @@
 //                candidate list that provably holds every element of the row's
 //                K' best (logit desc, id asc) that lies in the chunk.  The
 //                candidate bound is the K'-th largest maximum of the chunk's 64
-//                four-lane groups (distinct elements, so at least K' elements
-//                of the chunk lie at or above it).
+//                four-lane groups, or of its 256 lanes for K' > 32 (distinct
+//                elements, so at least K' elements of the chunk lie at or
+//                above it); the sub-record also keeps the chunk's top 16 of
+//                those maxima, for the row's survivor bound, and the filter's
+//                floor.
 //   finalize     the last workgroup of a row (atomic arrival ticket) merges the
-//                sub-records, recomputes the exact f32
+//                sub-records: it keeps the entries at or above the K'-th
+//                largest published maximum, recomputes the exact f32
 //                probability of the K' = top_k + 1 survivors with a correctly
 //                rounded exp, orders them by (p desc, id asc) -- the
 //                reference's top_k_desc order -- proves the k-th boundary is
-//                not a probability tie reaching past the survivors (or scans
-//                the row for the lowest tied ids when it is), then runs the
-//                reference's serial f32 top-p cut and WeightedIndex draw.
+//                not a probability tie reaching past the survivors (or finds
+//                the lowest tied ids of the row when it is: from the entries
+//                wherever a filter floor lies below the tied band, else from
+//                the logits), then runs the reference's serial f32 top-p cut
+//                and WeightedIndex draw.
 //   verify       for a speculative block, the last row finalizer of a
 //                sequence runs accept_drafts over the sequence's rows.
 //   controls     a call with sparse controls first runs control_kernel (one

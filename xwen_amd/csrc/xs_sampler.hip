@@ -2076,9 +2076,8 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
         for (int e = 0; e < 4; e++) {
           if (eb[e]) {
             const float x = q4(q[j], e);
-            const bool hit = (eb[e] >> lane) & 1ull;
             const uint32_t pos = (uint32_t)cnt + (uint32_t)lanes_below(eb[e]);
-            if (hit && pos < (uint32_t)CAPW) stg[pos] = pack(fkey(x), (uint32_t)(base_id + j * SLOT + e));
+            if (x >= tf && pos < (uint32_t)CAPW) stg[pos] = pack(fkey(x), (uint32_t)(base_id + j * SLOT + e));
             cnt += __popcll(eb[e]);
           }
         }

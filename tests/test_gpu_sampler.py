@@ -1,8 +1,7 @@
 """Parity of the HIP sampler (through the C ABI) with the CPU oracle.
 
-The bar: greedy argmax, the top-k candidate set and the
-chosen ids bit-exact with ties to the lower id; probabilities and log-probs
-within 1e-5 relative.
+The bar: greedy argmax, the top-k candidate set and the chosen ids bit-exact
+with ties to the lower id; probabilities and log-probs within 1e-5 relative.
 
 How each row is checked:
   * greedy rows: token and status equal the oracle's argmax (sampler.rs:268-286).

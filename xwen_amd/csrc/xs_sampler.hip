@@ -1579,19 +1579,27 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
       if (lane >= k) w[0] = 0.0f;
       if (64 + lane >= k) w[1] = 0.0f;
       // prefix[r] = init + w_0 + ... + w_(r*64+lane), left to right in f32
-      auto prefix = [&](float init, float (&pre)[2]) __attribute__((always_inline)) {
+      // A chain given a finite `stop` ends after the batch of 8 in which some
+      // prefix reaches it: the top-p cut uses the prefixes only up to the
+      // first that reaches top_p, and the draw only the total there.
+      auto prefix = [&](float init, float (&pre)[2], float stop) __attribute__((always_inline)) {
         float acc = init;
         const int k0 = min(k, 64);
+        bool cut = false;
         for (int b0 = 0; b0 < k0; b0 += 8) {
           float qv[8];
 #pragma unroll
           for (int u = 0; u < 8; u++) qv[u] = rdlf(w[0], (b0 + u) & 63);
 #pragma unroll
           for (int u = 0; u < 8; u++) acc = acc + ((lane >= b0 + u) ? qv[u] : 0.0f);
+          if (__ballot(lane < b0 + 8 && lane < k && acc >= stop)) {
+            cut = true;
+            break;
+          }
         }
         pre[0] = acc;
         pre[1] = acc;
-        if (k > 64) {
+        if (k > 64 && !cut) {
           float acc1 = rdlf(acc, 63);
           for (int b0 = 0; b0 < k - 64; b0 += 8) {
             float qv[8];
@@ -1609,7 +1617,7 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
       bool zero = false;
       if (!(cfg.top_p >= 1.0f)) {
         float pre[2];
-        prefix(-0.0f, pre);  // the serial sum folds from -0.0 as Rust's f32 Sum does
+        prefix(-0.0f, pre, INFINITY);  // the serial sum folds from -0.0 as Rust's f32 Sum does
         const float sum = at(pre, k - 1);
         if (!(sum > 0.0f)) {
           zero = true;  // all weights zero: truncate_top_p returns them unchanged
@@ -1622,7 +1630,7 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
         st = XS_ROW_ZERO_WEIGHT;
       } else {
         float c[2];
-        prefix(0.0f, c);
+        prefix(0.0f, c, cfg.top_p >= 1.0f ? INFINITY : cfg.top_p);
         int keep = k;
         if (!(cfg.top_p >= 1.0f)) {
           const uint64_t b0m = __ballot(lane < k && c[0] >= cfg.top_p);

@@ -450,6 +450,22 @@ XS_DEV void rank_sort_lds(const uint64_t* src, uint64_t* dst, int n) {
 }
 
 XS_DEV uint32_t rdl(uint32_t x, int i) { return (uint32_t)__builtin_amdgcn_readlane((int)x, i); }
+// The k-th largest of 64*R u32 keys held R per lane, by a bitwise search:
+// the largest value with at least k keys at or above it (ballot counts; no
+// sort).  k >= 1.
+template <int R>
+XS_DEV uint32_t kth_largest(const uint32_t (&x)[R], int k) {
+  uint32_t t = 0;
+#pragma unroll 1
+  for (int bit = 31; bit >= 0; bit--) {
+    const uint32_t c = t | (1u << bit);
+    int n = 0;
+#pragma unroll
+    for (int r = 0; r < R; r++) n += (int)__popcll(__ballot(x[r] >= c));
+    if (n >= k) t = c;
+  }
+  return t;
+}
 XS_DEV float rdlf(float x, int i) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), i)); }
 XS_DEV uint64_t rdl64(uint64_t x, int i) {
   return ((uint64_t)rdl((uint32_t)(x >> 32), i) << 32) | rdl((uint32_t)x, i);
@@ -865,13 +881,9 @@ XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, int nsub, const uin
     wave_sort_desc<1>(x);
     tau = rdl(x[0], kp - 1);
   } else if (4 * nsub >= kp) {
-    uint32_t x[4] = {live ? (uint32_t)h[5] : 0u, live ? (uint32_t)(h[5] >> 32) : 0u,
-                     live ? (uint32_t)h[6] : 0u, live ? (uint32_t)(h[6] >> 32) : 0u};
-    wave_sort_desc<4>(x);
-    const int i = kp - 1;
-#pragma unroll
-    for (int r = 0; r < 4; r++)
-      if ((i >> 6) == r) tau = rdl(x[r], i & 63);
+    const uint32_t x[4] = {live ? (uint32_t)h[5] : 0u, live ? (uint32_t)(h[5] >> 32) : 0u,
+                           live ? (uint32_t)h[6] : 0u, live ? (uint32_t)(h[6] >> 32) : 0u};
+    tau = kth_largest<4>(x, kp);
   }
   // Gather the survivors into LDS, then order them by rank: a survivor's
   // position is the number of survivors above it ((key, ~id) are distinct).
@@ -1176,11 +1188,7 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
         for (int r = 0; r < 4; r++) x[r] = (r * 64 + lane < nv) ? F.keys[r * 64 + lane] : 0u;
         wave_lds_sync();
       }
-      wave_sort_desc<4>(x);
-      const int i = kp - 1;
-#pragma unroll
-      for (int r = 0; r < 4; r++)
-        if ((i >> 6) == r) tau_row = rdl(x[r], i & 63);
+      tau_row = kth_largest<4>(x, kp);
     }
   }
 

@@ -161,6 +161,9 @@ def setup(name, nbuf, dev, torch, workloads, xsm, _lib, lib) -> dict:
         outs = [xsm.Draws(token=torch.empty(rows, **i32), status=torch.empty(rows, **i32))
                 for _ in range(nbuf)]
         extra = {}
+        # a heterogeneous batch starts its costliest rows first (xs_sample's
+        # row_order hint); the others run in their natural order
+        order = xsm.cost_order(wl.temperature, wl.top_k) if name == "c5" else None
         if name == "c3":
             extra["mask"] = torch.as_tensor(wl.mask.view(np.int32)).to(dev)
             row_bytes += 4 * wl.mask.shape[1]
@@ -184,6 +187,8 @@ def setup(name, nbuf, dev, torch, workloads, xsm, _lib, lib) -> dict:
                 a.row_max, a.row_lse = outs[i].row_max.data_ptr(), outs[i].row_lse.data_ptr()
                 a.n_top, a.top_ld = wl.n_top, wl.n_top
                 a.top_id, a.top_logprob = outs[i].top_id.data_ptr(), outs[i].top_logprob.data_ptr()
+            if order is not None:
+                a.row_order = order.ctypes.data
             argv.append(a)
         call = lib.xs_sample
         token_of = lambda o: o.token
@@ -202,6 +207,8 @@ def setup(name, nbuf, dev, torch, workloads, xsm, _lib, lib) -> dict:
         S["keep"] += (drafts,)
     elif name == "c3":
         S["keep"] += (extra["mask"],)
+    elif name == "c5":
+        S["keep"] += (order,)  # the launches read it on the host at each call
     return S
 
 
@@ -217,7 +224,7 @@ WORKLOAD_TEXT = {
     "c4": "C4 speculative verify: 16 sequences x 16 positions x V=248,320 fp32, 15 drafts each, "
           "top_k 20 / top_p 0.95 / T 1.0, accept_drafts on the device",
     "c5": "C5 heterogeneous batch: 256 rows x V=248,320 fp32 Student-t(3)x2, per-row T/k/p, "
-          "held_row max / logsumexp / top-20 log-probs",
+          "held_row max / logsumexp / top-20 log-probs; rows started costliest first (row_order)",
 }
 
 

@@ -163,7 +163,17 @@ typedef struct {
   const xs_row_control* controls; /* [rows] */
   const uint32_t* ctl_ids;        /* banned and bias ids of every row */
   const float* ctl_delta;         /* bias deltas, indexed as ctl_ids */
+  /* Scheduling hint, a HOST pointer (the one host pointer here), or NULL: a
+   * permutation of 0..rows-1 giving the order in which rows are started.
+   * Listing the rows with the costliest finalization first (top_k above 63,
+   * held_row statistics, sparse controls) lets their long finalizers overlap
+   * the other rows' streaming instead of ending the launch.  Outputs are the
+   * same in any order.  rows <= XS_ORDER_MAX; not a permutation is
+   * XS_ERR_ARG.  No counterpart in the reference, which samples one row at a
+   * time. */
+  const int32_t* row_order;
 } xs_sample_args;
+#define XS_ORDER_MAX 1024
 
 int xs_sample(xs_context* ctx, const xs_sample_args* args);
 

@@ -1,0 +1,81 @@
+"""xs_sample's row_order scheduling hint: any permutation gives the same
+outputs as the natural order, row for row; a non-permutation is an argument
+error."""
+import numpy as np
+import pytest
+
+from tests import workloads
+from xwen_amd import sampler as xsm
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+V = workloads.V
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    c = xsm.Context(max_rows=64, vocab=V)
+    c.bind_current_stream()
+    yield c
+    c.close()
+
+
+def _outputs(ctx, wl, order, **kw):
+    rows = wl.logits.shape[0]
+    lg = torch.as_tensor(wl.logits).cuda()
+    p = xsm.params_tensor(wl.temperature, wl.top_k, wl.top_p, rows, "cuda")
+    u = torch.as_tensor(wl.u).cuda()
+    out = xsm.sample_batch(ctx, lg, p, u, order=order, **kw)
+    torch.cuda.synchronize()
+    return {k: v.cpu().numpy() for k, v in vars(out).items() if v is not None}
+
+
+def test_any_order_gives_the_same_draws(ctx):
+    wl = workloads.c5_heterogeneous(rows=64)
+    base = _outputs(ctx, wl, None, cand_k=100, n_top=20)
+    rng = np.random.default_rng(91)
+    orders = [xsm.cost_order(wl.temperature, wl.top_k), rng.permutation(64), np.arange(64)[::-1]]
+    for order in orders:
+        got = _outputs(ctx, wl, order, cand_k=100, n_top=20)
+        for k, v in base.items():
+            assert (got[k].view(np.uint8) == v.view(np.uint8)).all(), k
+    assert (base["status"] == 0).all()
+
+
+def test_order_with_masks_and_controls(ctx):
+    wl = workloads.c3_masked()
+    rows = wl.logits.shape[0]
+    mask = torch.as_tensor(wl.mask.view(np.int32)).cuda()
+    S = xsm.SampleControl
+    ctls = [S(banned=[int(np.argmax(wl.logits[r]))]) if r % 3 == 1 else None for r in range(rows)]
+    controls = xsm.controls_tensor(ctls, "cuda")
+    base = _outputs(ctx, wl, None, cand_k=20, allowed=mask, controls=controls)
+    order = xsm.cost_order(wl.temperature, wl.top_k, controlled=[c is not None for c in ctls])
+    got = _outputs(ctx, wl, order, cand_k=20, allowed=mask, controls=controls)
+    for k, v in base.items():
+        assert (got[k].view(np.uint8) == v.view(np.uint8)).all(), k
+
+
+def test_bad_orders_are_argument_errors(ctx):
+    from xwen_amd import _lib
+    wl = workloads.c2_batch(rows=8)
+    lg = torch.as_tensor(wl.logits).cuda()
+    p = xsm.params_tensor(wl.temperature, wl.top_k, wl.top_p, 8, "cuda")
+    u = torch.as_tensor(wl.u).cuda()
+    for order in ([0, 1, 2, 3, 4, 5, 6, 6], [0, 1, 2, 3, 4, 5, 6, 8], [-1, 1, 2, 3, 4, 5, 6, 7]):
+        with pytest.raises(_lib.XsError):
+            xsm.sample_batch(ctx, lg, p, u, order=order)
+    # more rows than an order may list
+    n = _lib.ORDER_MAX + 1
+    big = xsm.Context(max_rows=n, vocab=1024)
+    big.bind_current_stream()
+    x = torch.zeros((n, 1024), dtype=torch.float32, device="cuda")
+    pb = xsm.params_tensor(1.0, 20, 0.9, n, "cuda")
+    ub = torch.zeros(n, dtype=torch.float32, device="cuda")
+    with pytest.raises(_lib.XsError):
+        xsm.sample_batch(big, x, pb, ub, order=np.arange(n))
+    torch.cuda.synchronize()
+    big.close()

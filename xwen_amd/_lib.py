@@ -20,6 +20,7 @@ ROW_OK, ROW_NAN, ROW_NO_FINITE, ROW_MASK_SHORT, ROW_FORCE_OOR, ROW_ZERO_WEIGHT, 
 K_MAX = 127
 TOP_MAX = 128
 CTL_MAX = 2048
+ORDER_MAX = 1024
 
 _vp = C.c_void_p
 _i64 = C.c_int64
@@ -50,6 +51,7 @@ class SampleArgs(C.Structure):
         ("row_max", _vp), ("row_lse", _vp), ("n_top", _i32), ("top_id", _vp),
         ("top_logprob", _vp), ("top_ld", _i64),
         ("controls", _vp), ("ctl_ids", _vp), ("ctl_delta", _vp),
+        ("row_order", _vp),  # host array [rows] (int32), or NULL
     ]
 
 

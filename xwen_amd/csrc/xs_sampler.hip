@@ -391,6 +391,9 @@ struct Args {
   int32_t* seq_ticket;  // [seqs * TSTRIDE] rows of the sequence that are finalized (0 between calls)
   int32_t n_chunks, nslots;
   uint64_t* rec;     // [rows, SRECW, nsp]: word i of sub-record s of a row at i * nsp + s
+  // the row the r-th group of n_chunks workgroups takes (has_order), else r
+  int32_t has_order;
+  uint16_t order[XS_ORDER_MAX];
 };
 
 
@@ -1808,8 +1811,9 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
   __shared__ TailLds Tl;
   const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
   const int nc = a.n_chunks;
-  const int row = blockIdx.x / nc;
-  const int chunk = blockIdx.x - row * nc;
+  const int rb = blockIdx.x / nc;
+  const int chunk = blockIdx.x - rb * nc;
+  const int row = a.has_order ? (int)a.order[rb] : rb;
   const int enc = (int)a.enc;
 
   // ---------------- chunk pass ----------------
@@ -2497,6 +2501,15 @@ int xs_sample(xs_context* ctx, const xs_sample_args* in) {
   if ((in->top_id || in->top_logprob) && in->top_ld < in->n_top) return XS_ERR_ARG;
   const bool lse = in->row_max || in->row_lse || in->top_id || in->top_logprob;
   if (lse && (in->allowed || in->controls)) return XS_ERR_ARG;
+  if (in->row_order) {  // a permutation of 0..rows-1
+    if (in->rows > XS_ORDER_MAX) return XS_ERR_ARG;
+    std::vector<uint8_t> seen((size_t)in->rows, 0);
+    for (int64_t i = 0; i < in->rows; i++) {
+      const int32_t r = in->row_order[i];
+      if (r < 0 || r >= in->rows || seen[(size_t)r]) return XS_ERR_ARG;
+      seen[(size_t)r] = 1;
+    }
+  }
   if (hipSetDevice(ctx->device) != hipSuccess) return XS_ERR_HIP;
   int32_t data_err = XS_ROW_OK;
   if (in->width < in->enc) data_err = XS_ROW_NARROW;
@@ -2538,6 +2551,10 @@ int xs_sample(xs_context* ctx, const xs_sample_args* in) {
   a.n_chunks = chunks_for(in->enc);
   a.nslots = (int32_t)slots_for(in->enc);
   a.rec = ctx->rec;
+  if (in->row_order) {
+    a.has_order = 1;
+    for (int64_t i = 0; i < in->rows; i++) a.order[i] = (uint16_t)in->row_order[i];
+  }
   return launch(ctx, a, in->rows, 1, in->allowed != nullptr, lse);
 }
 

@@ -214,9 +214,11 @@ class Draws:
 def sample_batch(ctx: Context, logits, params, uniforms, *, enc: int | None = None,
                  width: int | None = None, allowed=None, allowed_words: int | None = None,
                  cand_k: int = 0, stats: bool = False, n_top: int = 0, out: Draws | None = None,
-                 controls: Controls | None = None, check: bool = True) -> Draws:
+                 controls: Controls | None = None, order=None, check: bool = True) -> Draws:
     """One xs_sample call.  logits: float32 [rows, ld] CUDA tensor (ld % 4 == 0);
-    params: the uint8 tensor from params_tensor; uniforms: float32 [rows]."""
+    params: the uint8 tensor from params_tensor; uniforms: float32 [rows];
+    order: an optional host permutation of the rows (see cost_order), the
+    order in which the launch starts them."""
     torch = _torch()
     rows, ld = logits.shape
     dev = logits.device
@@ -267,10 +269,32 @@ def sample_batch(ctx: Context, logits, params, uniforms, *, enc: int | None = No
         a.controls = controls.rows.data_ptr()
         a.ctl_ids = controls.ids.data_ptr()
         a.ctl_delta = controls.delta.data_ptr()
+    keep = None
+    if order is not None:
+        keep = np.ascontiguousarray(np.asarray(order, np.int32))  # alive through the call
+        a.row_order = keep.ctypes.data
     rc = ctx.lib.xs_sample(ctx.h, C.byref(a))
+    del keep
     if check:
         _lib.check(rc, "xs_sample")
     return out
+
+
+def cost_order(temperature, top_k, *, controlled=None) -> np.ndarray:
+    """A row order for sample_batch that starts the rows with the costliest
+    finalization first: stochastic rows by top_k, largest first (above 63 the
+    general finalizer runs), then greedy rows; rows with sparse controls
+    (`controlled`, a bool per row) before all others.  Stable, so equal rows
+    keep their order."""
+    t = np.asarray(temperature, np.float64)
+    k = np.asarray(top_k, np.int64)
+    rows = max(t.size, k.size)
+    t = np.broadcast_to(t, (rows,))
+    k = np.broadcast_to(k, (rows,))
+    cost = np.where((t <= 0.0) | (k <= 1), 0, np.minimum(k, 1 << 20)).astype(np.int64)
+    if controlled is not None:
+        cost = cost + np.where(np.broadcast_to(np.asarray(controlled, bool), (rows,)), 1 << 21, 0)
+    return np.argsort(-cost, kind="stable").astype(np.int32)
 
 
 @dataclass

@@ -391,10 +391,13 @@ struct Args {
   int32_t* seq_ticket;  // [seqs * TSTRIDE] rows of the sequence that are finalized (0 between calls)
   int32_t n_chunks, nslots;
   uint64_t* rec;     // [rows, SRECW, nsp]: word i of sub-record s of a row at i * nsp + s
-  // the row the r-th group of n_chunks workgroups takes (has_order), else r
-  int32_t has_order;
-  uint16_t order[XS_ORDER_MAX];
 };
+
+// The row the r-th group of n_chunks workgroups takes, for launches given a
+// row order; other launches pass the empty struct, so their kernel arguments
+// stay small (a 2 KiB table in every launch's arguments cost 0.2-0.5 us).
+template <bool ORD> struct RowOrder { uint16_t v[XS_ORDER_MAX]; };
+template <> struct RowOrder<false> {};
 
 
 
@@ -1805,15 +1808,16 @@ XS_DEV void finalize_row(const Args& a, const Cfg& cfg, int row, const uint64_t*
 // the chunk and publishes it as one sub-record; the row's last workgroup to
 // arrive (an atomic ticket per row) finalizes the row with its first wave.
 
-template <bool HAS_MASK, bool WANT_LSE, bool HAS_CTL>
-__global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) void sample_kernel(Args a) {
+template <bool HAS_MASK, bool WANT_LSE, bool HAS_CTL, bool ORD>
+__global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) void sample_kernel(Args a, RowOrder<ORD> ro) {
   __shared__ ChunkLds Lc;
   __shared__ TailLds Tl;
   const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
   const int nc = a.n_chunks;
   const int rb = blockIdx.x / nc;
   const int chunk = blockIdx.x - rb * nc;
-  const int row = a.has_order ? (int)a.order[rb] : rb;
+  int row = rb;
+  if constexpr (ORD) row = ro.v[rb];
   const int enc = (int)a.enc;
 
   // ---------------- chunk pass ----------------
@@ -1858,14 +1862,19 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
   const int pc0 = pc;  // the chunk's first patch
 
   // Online reduction, one float4 at a time, branch-free.  The softmax partial
-  // is summed in the reference's scaled domain, s = v * inv rounded to f32 as
-  // softmax_in_place does, as sum exp2(s*log2e - cL) with a per-lane offset
-  // cL = rn(c*log2e), c the lane's first scaled float4 max (0 if that is
-  // -inf); the constant error of cL is taken out exactly (an fma) when the
-  // lanes are combined.  A lane whose later values could overflow a term
-  // (more than 60 above c) is summed again after the loop against its max.
-  // A NaN, or a +inf value (inf - inf at the recount), makes the sum NaN: the
-  // stochastic NaN test.  The four terms of a float4 are added pairwise.
+  // is sum exp2(v*invL - cL), invL = rn(inv*log2e), one fma per term, with a
+  // per-lane offset cL = rn(g*invL), g the lane's first float4 max (cL = 0
+  // when g*inv is not finite).  Against the reference's terms e^(s - c),
+  // s = rn(v*inv) as softmax_in_place scales, a term's exponent differs by
+  // the rounding of s (at most an ulp of s, about 1e-6 relative at |s| < 32),
+  // well inside the 1e-5 relative bar on probabilities; the selection's
+  // probabilities are computed later from the exact s.  The lanes are
+  // combined at the wave max m with the factor 2^(cL - m*invL), the product
+  // split exactly (an fma), so the wave's largest term is exactly 1.  A lane
+  // whose later values could overflow a term (more than 60 above its first
+  // max) is summed again after the loop against its max.  A NaN, or a +inf
+  // value (inf - inf at the recount), makes the sum NaN: the stochastic NaN
+  // test.  The four terms of a float4 are added pairwise.
   //
   // The held_row partial (raw logits, f64 like the reference's denominator)
   // keeps its per-lane offset at the lane's running max instead, so the
@@ -1873,6 +1882,7 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
   // accumulate in f64 without being absorbed: ln of a near-1 sum stays
   // accurate to ~1e-15.
   const float inv = cfg.inv;
+  const float invL = cfg.scale ? inv * LOG2E : LOG2E;
   float mr = -INFINITY;
   float gm[SPC];
   float sum = 0.0f, cL = 0.0f, c_s = 0.0f;
@@ -1925,17 +1935,13 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
     if (stoch) {
       if (j == 0) {
         const float c = cfg.scale ? gm[0] * inv : gm[0];
-        c_s = (c > -INFINITY && c < INFINITY) ? c : 0.0f;
-        cL = c_s * LOG2E;
+        const bool fin = c > -INFINITY && c < INFINITY;
+        c_s = fin ? c : 0.0f;
+        cL = fin ? gm[0] * invL : 0.0f;
       }
       float t[4];
-      if (cfg.scale) {
 #pragma unroll
-        for (int e = 0; e < 4; e++) t[e] = xexp2(__builtin_fmaf(x[e] * inv, LOG2E, -cL));
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; e++) t[e] = xexp2(__builtin_fmaf(x[e], LOG2E, -cL));
-      }
+      for (int e = 0; e < 4; e++) t[e] = xexp2(__builtin_fmaf(x[e], invL, -cL));
       sum += (t[0] + t[1]) + (t[2] + t[3]);
     } else {
 #pragma unroll
@@ -1960,8 +1966,7 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
     const float ms = cfg.scale ? mr * inv : mr;
     const bool redo = ms > c_s + 60.0f;
     if (__ballot(redo)) {
-      const float cn = redo ? ms : c_s;
-      const float cLn = cn * LOG2E;
+      const float cLn = redo ? mr * invL : cL;
       float s2 = 0.0f;
 #pragma unroll
       for (int j = 0; j < SPC; j++) {
@@ -1969,20 +1974,21 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
 #pragma unroll
         for (int e = 0; e < 4; e++) {
           const float xv = q4(q[j], e);
-          t[e] = xexp2(__builtin_fmaf(cfg.scale ? xv * inv : xv, LOG2E, -cLn));
+          t[e] = xexp2(__builtin_fmaf(xv, invL, -cLn));
         }
         s2 += (t[0] + t[1]) + (t[2] + t[3]);
       }
       if (redo) {
         sum = s2;
-        c_s = cn;
         cL = cLn;
       }
     }
-    // lanes to the wave's scaled max: factor e^(c_s - m_s) * 2^-(c_s*log2e - cL)
+    // lanes to the wave max: factor 2^(cL - m_w*invL), the product split into
+    // hi + lo exactly; the published offset is the scaled max c_w
     c_w = cfg.scale ? m_w * inv : m_w;
-    const float err = __builtin_fmaf(c_s, LOG2E, -cL);
-    const float d = __builtin_fmaf(c_s - c_w, LOG2E, -err);
+    const float hi = m_w * invL;
+    const float lo = __builtin_fmaf(m_w, invL, -hi);
+    const float d = (cL - hi) - lo;
     const double part = (sum != 0.0f) ? (double)sum * (double)xexp2(d) : (double)sum;
     P = red_sumd(part);
     if (P != P) flags |= 1u;
@@ -2402,12 +2408,22 @@ int check_common(xs_context* ctx, const Call& c) {
 // rows itself); a call with sparse controls runs control_kernel (one
 // workgroup per row) first.
 template <bool M, bool S, bool C>
-void launch2(xs_context* ctx, xs::Args& a, int64_t rows, dim3 g1) {
+void launch2(xs_context* ctx, xs::Args& a, int64_t rows, dim3 g1, const int32_t* order) {
   if (C) hipLaunchKernelGGL((xs::control_kernel<M>), dim3((unsigned)rows), dim3(xs::BLOCK), 0, ctx->stream, a);
-  hipLaunchKernelGGL((xs::sample_kernel<M, S, C>), g1, dim3(xs::BLOCK), 0, ctx->stream, a);
+  if (order) {
+    xs::RowOrder<true> ro;
+    for (int64_t i = 0; i < rows; i++) ro.v[i] = (uint16_t)order[i];
+    hipLaunchKernelGGL((xs::sample_kernel<M, S, C, true>), g1, dim3(xs::BLOCK), 0, ctx->stream, a, ro);
+  } else {
+    hipLaunchKernelGGL((xs::sample_kernel<M, S, C, false>), g1, dim3(xs::BLOCK), 0, ctx->stream, a,
+                       xs::RowOrder<false>{});
+  }
 }
 
-int launch(xs_context* ctx, xs::Args& a, int64_t rows, int span, bool mask, bool lse) {
+// order: null, or a host permutation of the rows (checked by the caller,
+// rows <= XS_ORDER_MAX)
+int launch(xs_context* ctx, xs::Args& a, int64_t rows, int span, bool mask, bool lse,
+           const int32_t* order = nullptr) {
   const bool ctl = a.controls != nullptr;
   const int64_t grid = rows * (int64_t)a.n_chunks;
   if (grid == 0) return XS_OK;
@@ -2419,11 +2435,11 @@ int launch(xs_context* ctx, xs::Args& a, int64_t rows, int span, bool mask, bool
   a.row_ticket = ctx->row_ticket;
   a.seq_ticket = ctx->seq_ticket;
   const dim3 g1((unsigned)grid);
-  if (ctl && mask) launch2<true, false, true>(ctx, a, rows, g1);
-  else if (ctl) launch2<false, false, true>(ctx, a, rows, g1);
-  else if (mask) launch2<true, false, false>(ctx, a, rows, g1);
-  else if (lse) launch2<false, true, false>(ctx, a, rows, g1);
-  else launch2<false, false, false>(ctx, a, rows, g1);
+  if (ctl && mask) launch2<true, false, true>(ctx, a, rows, g1, order);
+  else if (ctl) launch2<false, false, true>(ctx, a, rows, g1, order);
+  else if (mask) launch2<true, false, false>(ctx, a, rows, g1, order);
+  else if (lse) launch2<false, true, false>(ctx, a, rows, g1, order);
+  else launch2<false, false, false>(ctx, a, rows, g1, order);
   return hipGetLastError() == hipSuccess ? XS_OK : XS_ERR_HIP;
 }
 
@@ -2551,11 +2567,7 @@ int xs_sample(xs_context* ctx, const xs_sample_args* in) {
   a.n_chunks = chunks_for(in->enc);
   a.nslots = (int32_t)slots_for(in->enc);
   a.rec = ctx->rec;
-  if (in->row_order) {
-    a.has_order = 1;
-    for (int64_t i = 0; i < in->rows; i++) a.order[i] = (uint16_t)in->row_order[i];
-  }
-  return launch(ctx, a, in->rows, 1, in->allowed != nullptr, lse);
+  return launch(ctx, a, in->rows, 1, in->allowed != nullptr, lse, in->row_order);
 }
 
 int xs_verify(xs_context* ctx, const xs_verify_args* in) {

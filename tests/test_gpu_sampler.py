@@ -351,6 +351,28 @@ def test_infinities(ctx, oracle):
     assert d["status"][0] == 2
 
 
+def test_tall_peaks_and_extreme_temperatures(ctx, oracle):
+    """Rows shaped like a language model's logits: a few tokens 15-55 above a
+    N(0, 3^2) bulk, at T from 1.0 down to 0.05.  The lanes holding the peaks
+    start their softmax offsets far below them, where an f32 exponent of 60
+    to 90 loses 3e-6 to rounding; the recount and the lane factor must still
+    keep the denominator within DENOM_RTOL.  Also 1/T overflowing f32
+    (T = 1e-45: every s is +-inf) and T = 1e6 (every s near 0)."""
+    rng = np.random.default_rng(4242)
+    rows, v = 16, 65536
+    x = (rng.standard_normal((rows, v)) * 3.0).astype(np.float32)
+    for r in range(rows):
+        k = int(rng.integers(1, 6))
+        ids = rng.choice(v, k, replace=False)
+        x[r, ids] = (x[r].max() + rng.uniform(15, 55) - rng.uniform(0, 3, k)).astype(np.float32)
+    T = [1.0, 0.7, 0.5, 0.1] * 3 + [1e-45, 1e6, 0.05, 2.0]
+    K = [20, 50, 100, 20] * 3 + [20, 20, 40, 64]
+    P = [0.95, 0.9, 1.0, 0.8] * 3 + [0.9, 0.95, 0.99, 0.9]
+    U = rng.random(rows).astype(np.float32)
+    d = run_sample(ctx, x, T, K, P, U)
+    check_rows(oracle, x, T, K, P, U, d, label="tall peaks")
+
+
 def test_narrow_row_short_mask_and_bad_k(ctx):
     x = np.zeros((2, 1024), np.float32)
     d = run_sample(ctx, x, 1.0, 20, 0.95, 0.5, enc=1024, width=1000)

@@ -1862,19 +1862,20 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
   const int pc0 = pc;  // the chunk's first patch
 
   // Online reduction, one float4 at a time, branch-free.  The softmax partial
-  // is sum exp2(v*invL - cL), invL = rn(inv*log2e), one fma per term, with a
-  // per-lane offset cL = rn(g*invL), g the lane's first float4 max (cL = 0
-  // when g*inv is not finite).  Against the reference's terms e^(s - c),
-  // s = rn(v*inv) as softmax_in_place scales, a term's exponent differs by
-  // the rounding of s (at most an ulp of s, about 1e-6 relative at |s| < 32),
-  // well inside the 1e-5 relative bar on probabilities; the selection's
-  // probabilities are computed later from the exact s.  The lanes are
-  // combined at the wave max m with the factor 2^(cL - m*invL), the product
-  // split exactly (an fma), so the wave's largest term is exactly 1.  A lane
-  // whose later values could overflow a term (more than 60 above its first
-  // max) is summed again after the loop against its max.  A NaN, or a +inf
-  // value (inf - inf at the recount), makes the sum NaN: the stochastic NaN
-  // test.  The four terms of a float4 are added pairwise.
+  // is summed in the reference's scaled domain, s = v * inv rounded to f32 as
+  // softmax_in_place does (inv_e = 1 on rows with T = 1, where s = v: a
+  // uniform multiplier instead of a branch per float4), as sum
+  // exp2(s*log2e - cL) with a per-lane offset cL = rn(c*log2e), c the lane's
+  // first scaled float4 max (0 if that is not finite).  A lane whose max
+  // sits more than 40 above c is summed again after the loop against its max:
+  // that keeps the f32 exponent of a lane's largest term below 64, where half
+  // an ulp is 1.3e-6 relative (at 60, an LLM-like row whose top token stands
+  // far above the bulk reached 5e-6), and no term can overflow.  The lanes are
+  // combined at the wave max with the factor 2^(cL - c_w*log2e), its exponent
+  // formed in f64 (exact for the product of two floats) and applied as
+  // 2^n * 2^f, |f| <= 1/2, so it adds no rounding of its own.  A NaN, or a
+  // +inf value (inf - inf at the recount), makes the sum NaN: the stochastic
+  // NaN test.  The four terms of a float4 are added pairwise.
   //
   // The held_row partial (raw logits, f64 like the reference's denominator)
   // keeps its per-lane offset at the lane's running max instead, so the
@@ -1882,7 +1883,7 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
   // accumulate in f64 without being absorbed: ln of a near-1 sum stays
   // accurate to ~1e-15.
   const float inv = cfg.inv;
-  const float invL = cfg.scale ? inv * LOG2E : LOG2E;
+  const float inv_e = cfg.scale ? inv : 1.0f;
   float mr = -INFINITY;
   float gm[SPC];
   float sum = 0.0f, cL = 0.0f, c_s = 0.0f;
@@ -1934,14 +1935,13 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
     mr = vmax(mr, gm[j]);
     if (stoch) {
       if (j == 0) {
-        const float c = cfg.scale ? gm[0] * inv : gm[0];
-        const bool fin = c > -INFINITY && c < INFINITY;
-        c_s = fin ? c : 0.0f;
-        cL = fin ? gm[0] * invL : 0.0f;
+        const float c = gm[0] * inv_e;
+        c_s = (c > -INFINITY && c < INFINITY) ? c : 0.0f;
+        cL = c_s * LOG2E;
       }
       float t[4];
 #pragma unroll
-      for (int e = 0; e < 4; e++) t[e] = xexp2(__builtin_fmaf(x[e], invL, -cL));
+      for (int e = 0; e < 4; e++) t[e] = xexp2(__builtin_fmaf(x[e] * inv_e, LOG2E, -cL));
       sum += (t[0] + t[1]) + (t[2] + t[3]);
     } else {
 #pragma unroll
@@ -1961,12 +1961,13 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
   float c_w = 0.0f;  // offset of the published softmax partial
   uint32_t flags = 0;
   if (stoch) {
-    // lanes whose max sits more than 60 above their offset: recount against
+    // lanes whose max sits more than 40 above their offset: recount against
     // the max (rare; makes +inf a NaN)
-    const float ms = cfg.scale ? mr * inv : mr;
-    const bool redo = ms > c_s + 60.0f;
+    const float ms = mr * inv_e;
+    const bool redo = ms > c_s + 40.0f;
     if (__ballot(redo)) {
-      const float cLn = redo ? mr * invL : cL;
+      const float cn = redo ? ms : c_s;
+      const float cLn = cn * LOG2E;
       float s2 = 0.0f;
 #pragma unroll
       for (int j = 0; j < SPC; j++) {
@@ -1974,22 +1975,24 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
 #pragma unroll
         for (int e = 0; e < 4; e++) {
           const float xv = q4(q[j], e);
-          t[e] = xexp2(__builtin_fmaf(xv, invL, -cLn));
+          t[e] = xexp2(__builtin_fmaf(xv * inv_e, LOG2E, -cLn));
         }
         s2 += (t[0] + t[1]) + (t[2] + t[3]);
       }
       if (redo) {
         sum = s2;
+        c_s = cn;
         cL = cLn;
       }
     }
-    // lanes to the wave max: factor 2^(cL - m_w*invL), the product split into
-    // hi + lo exactly; the published offset is the scaled max c_w
-    c_w = cfg.scale ? m_w * inv : m_w;
-    const float hi = m_w * invL;
-    const float lo = __builtin_fmaf(m_w, invL, -hi);
-    const float d = (cL - hi) - lo;
-    const double part = (sum != 0.0f) ? (double)sum * (double)xexp2(d) : (double)sum;
+    // lanes to the wave's scaled max c_w: factor 2^(cL - c_w*log2e), that is
+    // e^(c_s - c_w) with cL's own rounding taken out (0 for a NaN or -inf
+    // exponent, which keeps a NaN sum NaN)
+    c_w = m_w * inv_e;
+    const double dd = (double)cL - (double)c_w * (double)LOG2E;
+    const double dn = ::fmin(::fmax(::rint(dd), -2100.0), 2100.0);
+    const double fac = (dd > -2100.0) ? ldexp((double)xexp2((float)(dd - dn)), (int)dn) : 0.0;
+    const double part = (sum != 0.0f) ? (double)sum * fac : (double)sum;
     P = red_sumd(part);
     if (P != P) flags |= 1u;
   } else if (red_or(nanl)) {
@@ -2519,11 +2522,11 @@ int xs_sample(xs_context* ctx, const xs_sample_args* in) {
   if (lse && (in->allowed || in->controls)) return XS_ERR_ARG;
   if (in->row_order) {  // a permutation of 0..rows-1
     if (in->rows > XS_ORDER_MAX) return XS_ERR_ARG;
-    std::vector<uint8_t> seen((size_t)in->rows, 0);
+    uint64_t seen[XS_ORDER_MAX / 64] = {};
     for (int64_t i = 0; i < in->rows; i++) {
       const int32_t r = in->row_order[i];
-      if (r < 0 || r >= in->rows || seen[(size_t)r]) return XS_ERR_ARG;
-      seen[(size_t)r] = 1;
+      if (r < 0 || r >= in->rows || ((seen[r >> 6] >> (r & 63)) & 1u)) return XS_ERR_ARG;
+      seen[r >> 6] |= 1ull << (r & 63);
     }
   }
   if (hipSetDevice(ctx->device) != hipSuccess) return XS_ERR_HIP;

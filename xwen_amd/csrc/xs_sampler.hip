@@ -198,9 +198,15 @@ XS_DEV double wave_sumd(double v) {
   for (int o = 32; o > 0; o >>= 1) v += xor_f64(v, o);
   return v;
 }
+// (written out: the unroller leaves a loop over these exchanges rolled, and a
+// rolled one selects its DPP pattern by comparisons at run time)
 XS_DEV uint32_t wave_or(uint32_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v |= xor_u32(v, o);
+  v |= xor_u32(v, 32);
+  v |= xor_u32(v, 16);
+  v |= xor_u32(v, 8);
+  v |= xor_u32(v, 4);
+  v |= xor_u32(v, 2);
+  v |= xor_u32(v, 1);
   return v;
 }
 
@@ -502,8 +508,12 @@ XS_DEV int wave_incl_scan(int v) {
   return v;
 }
 XS_DEV int wave_sumi(int v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += xor_lane(v, o);
+  v += xor_lane(v, 32);
+  v += xor_lane(v, 16);
+  v += xor_lane(v, 8);
+  v += xor_lane(v, 4);
+  v += xor_lane(v, 2);
+  v += xor_lane(v, 1);
   return v;
 }
 
@@ -576,7 +586,6 @@ constexpr int EPRE = 16;            // entries per sub-record read with the head
 constexpr int GMAX = 4;             // sub-record groups of 64 a finalizer handles
 constexpr int KGRP = 32;            // largest K' whose chunk bound comes from group maxima
 constexpr uint32_t KEY_NEG_INF = 0x007FFFFFu;  // fkey(-inf)
-constexpr double LN2D = 0.693147180559945309417;
 
 struct ChunkLds {
   uint32_t groupmax[BLOCK / 4];     // maxima of 4-lane groups

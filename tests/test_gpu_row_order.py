@@ -79,3 +79,51 @@ def test_bad_orders_are_argument_errors(ctx):
         xsm.sample_batch(big, x, pb, ub, order=np.arange(n))
     torch.cuda.synchronize()
     big.close()
+
+
+def test_ordered_call_in_a_graph():
+    """An ordered call captured in a HIP graph keeps its order (the table is
+    copied into the kernel's arguments at capture): every replay, with
+    unordered eager calls in between, equals the eager ordered call."""
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    wl = workloads.c5_heterogeneous(rows=64)
+    rows = 64
+    c = xsm.Context(max_rows=rows, vocab=V)
+    lg = torch.as_tensor(wl.logits).cuda()
+    p = xsm.params_tensor(wl.temperature, wl.top_k, wl.top_p, rows, "cuda")
+    u = torch.as_tensor(wl.u).cuda()
+    order = xsm.cost_order(wl.temperature, wl.top_k)
+    out = xsm.Draws(token=torch.empty(rows, dtype=torch.int32, device="cuda"),
+                    status=torch.empty(rows, dtype=torch.int32, device="cuda"),
+                    soft_sum=torch.empty(rows, dtype=torch.float32, device="cuda"),
+                    soft_max=torch.empty(rows, dtype=torch.float32, device="cuda"))
+    c.bind_current_stream()
+    xsm.sample_batch(c, lg, p, u, stats=True, out=out, order=order)
+    torch.cuda.synchronize()
+    want_tok = out.token.cpu().numpy().copy()
+    want_sum = out.soft_sum.cpu().numpy().copy()
+    assert (out.status.cpu().numpy() == 0).all()
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        c.bind_current_stream()
+        with torch.cuda.graph(g, stream=side):
+            c.bind_current_stream()
+            xsm.sample_batch(c, lg, p, u, stats=True, out=out, order=order)
+    c.bind_current_stream()
+    torch.cuda.synchronize()
+    for rep in range(4):
+        out.token.fill_(-7)
+        out.soft_sum.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert (out.token.cpu().numpy() == want_tok).all(), rep
+        assert (out.soft_sum.cpu().numpy().view(np.uint32) == want_sum.view(np.uint32)).all(), rep
+        # an unordered eager call on the same context in between
+        d = xsm.sample_batch(c, lg, p, u)
+        torch.cuda.synchronize()
+        assert (d.token.cpu().numpy() == want_tok).all(), rep
+    c.close()

@@ -127,3 +127,30 @@ def test_ordered_call_in_a_graph():
         torch.cuda.synchronize()
         assert (d.token.cpu().numpy() == want_tok).all(), rep
     c.close()
+
+
+def test_order_at_its_row_limit():
+    """ORDER_MAX rows (the whole argument table) of 4,096 ids: reversed and
+    shuffled orders give the natural order's draws row for row."""
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from xwen_amd import _lib
+    n, v = _lib.ORDER_MAX, 4096
+    rng = np.random.default_rng(1024)
+    x = torch.as_tensor(rng.normal(0.0, 3.0, (n, v)).astype(np.float32)).cuda()
+    T = rng.choice([0.0, 0.7, 1.0], n)
+    K = rng.choice([1, 20, 100], n)
+    p = xsm.params_tensor(T, K, 0.95, n, "cuda")
+    u = torch.as_tensor(rng.random(n).astype(np.float32)).cuda()
+    c = xsm.Context(max_rows=n, vocab=v)
+    c.bind_current_stream()
+    base = xsm.sample_batch(c, x, p, u, cand_k=100)
+    torch.cuda.synchronize()
+    want = {k: t.cpu().numpy() for k, t in vars(base).items() if t is not None}
+    assert (want["status"] == 0).all()
+    for order in (np.arange(n)[::-1], rng.permutation(n), xsm.cost_order(T, K)):
+        got = xsm.sample_batch(c, x, p, u, cand_k=100, order=order)
+        torch.cuda.synchronize()
+        for k, w in want.items():
+            assert (getattr(got, k).cpu().numpy().view(np.uint8) == w.view(np.uint8)).all(), k
+    c.close()

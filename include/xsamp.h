@@ -145,7 +145,8 @@ typedef struct {
   int32_t* status;       /* [rows] XS_ROW_* */
   int32_t* cand_id;      /* [rows, cand_ld] the candidate set in draw order, or NULL */
   float* cand_w;         /* [rows, cand_ld] post-top-p weights (zeros included), or NULL */
-  int32_t* n_cand;       /* [rows] candidates written (0 on greedy rows), or NULL */
+  int32_t* n_cand;       /* [rows] candidates written (0 on greedy rows), or NULL;
+                            entries past min(n_cand, cand_ld) are left as they were */
   int64_t cand_ld;       /* >= min(top_k, enc) of every row that writes candidates */
   float* soft_max;       /* [rows] max of the scaled, controlled row, or NULL */
   float* soft_sum;       /* [rows] softmax denominator used, or NULL */

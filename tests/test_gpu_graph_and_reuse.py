@@ -45,9 +45,12 @@ def test_shapes_change_between_calls_on_one_context():
         want = _call(fresh, x, 0.8, 20, 0.9, 0.37)
         fresh.close()
         assert (g["status"] == 0).all()
-        for k in ("token", "status", "cand_id", "n_cand"):
+        for k in ("token", "status", "n_cand"):
             assert (g[k] == want[k]).all(), k
-        assert (g["cand_w"].view(np.uint32) == want["cand_w"].view(np.uint32)).all()
+        for r in range(len(want["n_cand"])):  # entries past n_cand are not written
+            n = min(int(want["n_cand"][r]), want["cand_id"].shape[1])
+            assert (g["cand_id"][r, :n] == want["cand_id"][r, :n]).all(), r
+            assert (g["cand_w"][r, :n].view(np.uint32) == want["cand_w"][r, :n].view(np.uint32)).all(), r
 
 
 def test_graph_replays_match_the_eager_call():
@@ -169,7 +172,11 @@ def test_two_contexts_on_two_streams_run_concurrently():
         ref = seq[0]
         for o in seq + con:
             assert (o.token.cpu() == ref.token.cpu()).all()
-            assert (o.cand_id.cpu() == ref.cand_id.cpu()).all()
+            nc = ref.n_cand.cpu()
+            assert (o.n_cand.cpu() == nc).all()
+            for r in range(len(nc)):  # entries past n_cand are not written
+                n = min(int(nc[r]), ref.cand_id.shape[1])
+                assert (o.cand_id[r, :n].cpu() == ref.cand_id[r, :n].cpu()).all(), r
             assert (o.soft_sum.cpu().view(torch.int32) == ref.soft_sum.cpu().view(torch.int32)).all()
     ca.close()
     cb.close()

@@ -445,8 +445,12 @@ def test_repeat_calls_are_identical(ctx):
     a = run_sample(ctx, wl.logits, wl.temperature, wl.top_k, wl.top_p, wl.u)
     for _ in range(3):
         b = run_sample(ctx, wl.logits, wl.temperature, wl.top_k, wl.top_p, wl.u)
-        for key in ("token", "status", "cand_id", "cand_w", "soft_sum"):
+        for key in ("token", "status", "n_cand", "soft_sum"):
             np.testing.assert_array_equal(a[key], b[key])
+        for r in range(len(a["n_cand"])):  # entries past n_cand are not written
+            n = min(int(a["n_cand"][r]), a["cand_id"].shape[1])
+            for key in ("cand_id", "cand_w"):
+                np.testing.assert_array_equal(a[key][r, :n], b[key][r, :n])
 
 
 def test_draw_frequencies_follow_llamacpp_semantics(ctx, oracle, golden):

@@ -77,6 +77,10 @@ def test_bad_orders_are_argument_errors(ctx):
     for order in ([0, 1, 2, 3, 4, 5, 6, 6], [0, 1, 2, 3, 4, 5, 6, 8], [-1, 1, 2, 3, 4, 5, 6, 7]):
         with pytest.raises(_lib.XsError):
             xsm.sample_batch(ctx, lg, p, u, order=order)
+    # the host mirror checks the length (the library reads `rows` entries)
+    for order in ([0, 1, 2], list(range(9))):
+        with pytest.raises(ValueError):
+            xsm.sample_batch(ctx, lg, p, u, order=order)
     # more rows than an order may list
     n = _lib.ORDER_MAX + 1
     big = xsm.Context(max_rows=n, vocab=1024)

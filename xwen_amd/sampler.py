@@ -272,6 +272,8 @@ def sample_batch(ctx: Context, logits, params, uniforms, *, enc: int | None = No
     keep = None
     if order is not None:
         keep = np.ascontiguousarray(np.asarray(order, np.int32))  # alive through the call
+        if keep.shape != (rows,):  # the library reads exactly `rows` entries
+            raise ValueError(f"order must list each of the {rows} rows once, got shape {keep.shape}")
         a.row_order = keep.ctypes.data
     rc = ctx.lib.xs_sample(ctx.h, C.byref(a))
     del keep

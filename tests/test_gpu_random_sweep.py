@@ -1,0 +1,65 @@
+"""Seeded random parity sweep: batches of varied logit distributions (normal at
+several scales, Student-t, tall peaks over a bulk, values quantized so that
+exact ties are common, all-negative ties, Gumbel), random T / top_k / top_p
+per row (greedy rows, K' across the fast and general finalizers), some with
+random allow-masks, at three row widths; every row held to the oracle by the
+same bar as the configured cases."""
+import numpy as np
+import pytest
+
+from tests import workloads
+from tests.test_gpu_sampler import check_rows, run_sample
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from xwen_amd import sampler as xsm
+    c = xsm.Context(max_rows=64, vocab=workloads.V)
+    c.bind_current_stream()
+    yield c
+    c.close()
+
+
+def _batch(b):
+    rng = np.random.default_rng(90_000 + b)
+    v = int(rng.choice([4096, 65536, 248320]))
+    rows = 24
+    kind = b % 6
+    if kind == 0:
+        x = rng.normal(0, rng.choice([0.5, 1, 3, 8]), (rows, v))
+    elif kind == 1:
+        x = rng.standard_t(3, (rows, v)) * 2
+    elif kind == 2:
+        x = rng.normal(0, 3, (rows, v))
+        for r in range(rows):
+            ids = rng.choice(v, int(rng.integers(1, 6)), replace=False)
+            x[r, ids] = x[r].max() + rng.uniform(5, 50, len(ids))
+    elif kind == 3:
+        x = np.round(rng.normal(0, 2, (rows, v)) * 4) / 4
+    elif kind == 4:
+        x = np.round(rng.normal(0, 1, (rows, v)), 1) - 30.0
+    else:
+        x = rng.gumbel(0, 1.5, (rows, v))
+    x = x.astype(np.float32)
+    T = rng.choice([0.0, 0.05, 0.3, 0.7, 1.0, 1.5, 2.0], rows)
+    K = rng.choice([1, 2, 5, 20, 50, 64, 65, 100, 127], rows)
+    P = rng.choice([0.3, 0.8, 0.95, 0.999, 1.0], rows)
+    U = rng.random(rows).astype(np.float32)
+    mask = None
+    if b % 4 == 3:
+        allow = rng.random((rows, v)) < rng.choice([0.01, 0.1, 0.5])
+        allow[np.arange(rows), rng.integers(0, v, rows)] = True
+        mask = workloads.pack_mask(allow)
+    return x, T, K, P, U, mask, f"sweep batch {b} kind {kind} v {v}"
+
+
+@pytest.mark.parametrize("b", range(18))
+def test_random_batch(ctx, oracle, b):
+    x, T, K, P, U, mask, label = _batch(b)
+    d = run_sample(ctx, x, T, K, P, U, mask=mask)
+    check_rows(oracle, x, T, K, P, U, d, mask=mask, label=label)

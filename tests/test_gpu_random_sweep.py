@@ -63,3 +63,46 @@ def test_random_batch(ctx, oracle, b):
     x, T, K, P, U, mask, label = _batch(b)
     d = run_sample(ctx, x, T, K, P, U, mask=mask)
     check_rows(oracle, x, T, K, P, U, d, mask=mask, label=label)
+
+
+def _control_batch(b):
+    from xwen_amd import sampler as xsm
+    rng = np.random.default_rng(70_000 + b)
+    v = int(rng.choice([4096, 65536, 248320]))
+    rows = 24
+    x = rng.standard_t(3, (rows, v)) * 2 if b % 2 else rng.normal(0, 3, (rows, v))
+    if b % 3 == 2:
+        x = np.round(x * 2) / 2
+    x = x.astype(np.float32)
+    T = rng.choice([0.0, 0.3, 0.7, 1.0, 1.5], rows)
+    K = rng.choice([1, 5, 20, 64, 100], rows)
+    P = rng.choice([0.5, 0.9, 1.0], rows)
+    U = rng.random(rows).astype(np.float32)
+    ctls = []
+    for r in range(rows):
+        if rng.integers(0, 6) == 0:
+            ctls.append(None)
+            continue
+        banned = [int(i) for i in rng.choice(v + 50, int(rng.integers(0, 40)))]  # some past the vocabulary
+        if rng.random() < 0.5:
+            banned.append(int(np.argmax(x[r])))
+        bias = [(int(i), float(rng.normal(0, 4))) for i in rng.choice(v, int(rng.integers(0, 30)))]
+        pull = (int(rng.integers(0, v)), float(rng.choice([0.25, 0.5, 1.0, 1.5]))) if rng.random() < 0.4 else None
+        force = int(rng.integers(0, v + 3)) if rng.random() < 0.15 else None
+        ctls.append(xsm.SampleControl(banned=banned, bias=bias, pull=pull, force=force))
+    mask = None
+    if b % 4 == 3:
+        allow = rng.random((rows, v)) < rng.choice([0.02, 0.3])
+        allow[np.arange(rows), rng.integers(0, v, rows)] = True
+        mask = workloads.pack_mask(allow)
+    return x, T, K, P, U, ctls, mask, f"control sweep batch {b} v {v}"
+
+
+@pytest.mark.parametrize("b", range(6))
+def test_random_controls_batch(ctx, oracle, b):
+    """Random sparse controls per row: bans (some past the vocabulary, some of
+    the argmax), biases, pulls up to alpha 1.5 and forces (some out of range),
+    with and without an allow-mask."""
+    x, T, K, P, U, ctls, mask, label = _control_batch(b)
+    d = run_sample(ctx, x, T, K, P, U, ctls=ctls, mask=mask)
+    check_rows(oracle, x, T, K, P, U, d, ctls=ctls, mask=mask, label=label)

@@ -106,3 +106,45 @@ def test_random_controls_batch(ctx, oracle, b):
     x, T, K, P, U, ctls, mask, label = _control_batch(b)
     d = run_sample(ctx, x, T, K, P, U, ctls=ctls, mask=mask)
     check_rows(oracle, x, T, K, P, U, d, ctls=ctls, mask=mask, label=label)
+
+
+@pytest.mark.parametrize("b", range(8))
+def test_random_verify_block(ctx, oracle, b):
+    """xs_verify over a random block: 1-8 sequences of span 1-8, drafts that are
+    the row's argmax, its sampled token or a random id, random budgets (0
+    included) and EOG ids taken from the sampled tokens; the walk must equal
+    accept_drafts (src/generate.rs:4020-4046) over the same row tokens."""
+    from xwen_amd import sampler as xsm
+    rng = np.random.default_rng(50_000 + b)
+    seqs, span = int(rng.integers(1, 9)), int(rng.integers(1, 9))
+    rows, v = seqs * span, int(rng.choice([4096, 65536, 248320]))
+    x = (rng.normal(0, 3, (rows, v)) if b % 2 else rng.standard_t(3, (rows, v)) * 2).astype(np.float32)
+    T = rng.choice([0.0, 0.7, 1.0], rows)
+    K = rng.choice([1, 20, 50], rows)
+    P = rng.choice([0.9, 1.0], rows)
+    U = rng.random(rows).astype(np.float32)
+    d = run_sample(ctx, x, T, K, P, U)
+    check_rows(oracle, x, T, K, P, U, d, label=f"verify sweep {b}", margins=False)
+    tok = d["token"].reshape(seqs, span)
+    arg = np.argmax(x, axis=1).reshape(seqs, span)
+    pick = rng.integers(0, 3, (seqs, span))
+    drafts = np.where(pick == 0, arg, np.where(pick == 1, tok, rng.integers(0, v, (seqs, span))))
+    drafts = np.ascontiguousarray(drafts[:, :max(span - 1, 1)].astype(np.int32))
+    eog = [int(t) for t in rng.choice(tok.ravel(), min(2, rows), replace=False)]
+    budgets = rng.integers(0, span + 2, seqs).astype(np.int32)
+    lg = torch.as_tensor(x).cuda()
+    p = xsm.params_tensor(T, K, P, rows, "cuda")
+    u = torch.as_tensor(U).cuda()
+    out = xsm.verify_batch(ctx, lg, seqs, span, p, u, torch.as_tensor(drafts).cuda(),
+                           budget=torch.as_tensor(budgets).cuda(), eog=eog)
+    torch.cuda.synchronize()
+    row_tok = out.row_token.cpu().numpy()
+    np.testing.assert_array_equal(row_tok, d["token"])
+    acc, com = out.accepted.cpu().numpy(), out.committed.cpu().numpy()
+    ncom, sst = out.n_committed.cpu().numpy(), out.seq_status.cpu().numpy()
+    for s in range(seqs):
+        toks = list(row_tok[s * span:(s + 1) * span])
+        st, m, committed, _ = oracle.accept_drafts(list(drafts[s][:span - 1]), int(budgets[s]), toks,
+                                                   [t in eog for t in toks])
+        assert (sst[s], acc[s], ncom[s]) == (st, m, len(committed)), (b, s)
+        assert list(com[s, :ncom[s]]) == committed, (b, s)

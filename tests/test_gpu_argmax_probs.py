@@ -103,3 +103,29 @@ def test_keep_confident_over_device_probabilities(ctx):
     ids, probs = _run(ctx, x)
     kept = xsm.keep_confident(list(ids), probs, 0.5)
     assert kept == [1000, 1001]
+
+
+@pytest.mark.parametrize("b", range(6))
+def test_random_drafter_blocks(ctx, b):
+    """Seeded random blocks: 1-15 rows of width 17-V, normal, Student-t and
+    quantized (exact ties at the top) logits, some rows with a tall peak."""
+    rng = np.random.default_rng(3_000 + b)
+    n, width = int(rng.integers(1, 16)), int(rng.integers(17, V + 1))
+    ld = (width + 3) // 4 * 4
+    kind = b % 3
+    if kind == 0:
+        rows = rng.normal(0, rng.choice([0.3, 3.0]), (n, width))
+    elif kind == 1:
+        rows = rng.standard_t(3, (n, width)) * 2
+    else:
+        rows = np.round(rng.normal(0, 2, (n, width)) * 2) / 2
+    rows = rows.astype(np.float32)
+    for r in range(n):
+        if rng.random() < 0.4:
+            rows[r, rng.integers(0, width)] = rows[r].max() + np.float32(rng.uniform(1, 30))
+    x = np.full((n, ld), np.nan, np.float32)  # padding past `width` is never read
+    x[:, :width] = rows
+    ids, probs = _run(ctx, x, width=width)
+    want_ids, want_p = _want(rows)
+    assert (ids == want_ids).all()
+    np.testing.assert_allclose(probs, want_p, rtol=PROB_RTOL, atol=0)

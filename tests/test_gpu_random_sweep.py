@@ -153,22 +153,12 @@ def test_random_verify_block(ctx, oracle, b):
 @pytest.mark.parametrize("b", range(6))
 def test_random_held_row_statistics(ctx, oracle, b):
     """held_row (src/generate.rs:1871-1933) on the sweep's distributions (no
-    mask: held_row takes none): the row max bit-exact, the logsumexp and the
-    top-n log-probs within 1e-5 relative, the top-n ids in (logit desc, id asc)
-    order; the draws held to the oracle as every row."""
-    from tests import refimpl
+    mask: held_row takes none), checked as check_held_row states; the draws
+    held to the oracle as every row."""
+    from tests.test_gpu_sampler import check_held_row
     x, T, K, P, U, _, label = _batch(b)
     n_top = int(np.random.default_rng(b).choice([1, 8, 20, 64]))
     d = run_sample(ctx, x, T, K, P, U, n_top=n_top)
     check_rows(oracle, x, T, K, P, U, d, label=label + " held_row")
-    v = x.shape[1]
     for r in range(x.shape[0]):
-        st, mx, lse = oracle.held_row(x[r], v)
-        assert st == 0
-        assert np.float32(d["row_max"][r]) == np.float32(mx)
-        assert abs(d["row_lse"][r] - lse) <= 1e-5 * abs(lse) + 1e-12, (label, r)
-        order = refimpl.stable_desc_order(x[r])[:n_top]
-        assert list(d["top_id"][r]) == order.tolist(), (label, r)
-        want = x[r][order].astype(np.float64) - lse
-        np.testing.assert_allclose(d["top_logprob"][r].astype(np.float64), want, rtol=1e-5,
-                                   atol=1e-12, err_msg=f"{label} row {r}")
+        check_held_row(oracle, x[r], d, r, n_top, label=label)

@@ -13,9 +13,13 @@ Prints one JSON line (rank 0, N = 1):
              launch that rocprofv3's FETCH_SIZE + WRITE_SIZE counters measured
              (profiles/sample_kernel_c2_traffic.md)
   cpu_baseline  the CPU oracle's restatement of the reference sampler (serial
-             f32 softmax with libm expf, streaming top-k, top-p, WeightedIndex),
-             one thread, on a bounded sample of the same rows
+             f32 softmax with libm expf, streaming top-k, top-p, WeightedIndex)
+             on a bounded sample of the same rows: `value` on the host cores of
+             the box's share (one row per thread), `single_thread` one row at a
+             time, as the reference samples, both timed in this run
 
+Exactly `--steps` launches are timed, as one hipGraph replay (or eagerly with
+--no-graph), after `--warmup` untimed launches.
 `--workload c3|c4|c5` times the other measured configurations the same way
 (masked rows, a speculative verify block through xs_verify, a heterogeneous
 256-row batch with held_row statistics); their lines carry no traffic figure.
@@ -51,6 +55,15 @@ def cpu_model() -> str:
     except OSError:
         pass
     return "unknown CPU"
+
+
+def host_threads() -> int:
+    """Host cores this process may use, capped at the 16 a one-GPU share holds."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    return max(1, min(n, 16))
 
 
 def cpu_baseline(name: str, wl, seconds: float, threads: int) -> dict:
@@ -237,8 +250,9 @@ def main() -> int:
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of a hipGraph")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-threads", type=int, default=1,
-                    help="rows the CPU baseline samples at once (one per thread)")
+    ap.add_argument("--cpu-threads", type=int, default=0,
+                    help="rows the CPU baseline samples at once (one per thread); 0 = the "
+                         "host cores of this process's share (at most 16)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES")
     ap.add_argument("--workload", choices=["c1", "c1g", "c2", "c3", "c4", "c5"], default="c2",
                     help="c2 (default) is the headline configuration; c1/c1g one row (latency)")
@@ -276,10 +290,12 @@ def main() -> int:
     if st.any():
         raise RuntimeError(f"row errors in the warm-up batch: {st}")
 
+    # Exactly `steps` launches are timed: one hipGraph holding `steps` launches
+    # (cycling the rotating copies), replayed once after an untimed replay.
+    steps = max(1, args.steps)
+    nbuf = S["nbuf"]
     use_graph = not args.no_graph
     graph = None
-    nbuf = S["nbuf"]
-    per_graph = nbuf * 20 if nbuf <= 10 else nbuf  # every graph replay cycles all copies
     if use_graph:
         try:
             g = torch.cuda.CUDAGraph()
@@ -289,12 +305,11 @@ def main() -> int:
                 ctx.bind_current_stream()
                 with torch.cuda.graph(g, stream=side):
                     ctx.bind_current_stream()
-                    for i in range(per_graph):
+                    for i in range(steps):
                         step(i)
             ctx.bind_current_stream()
             torch.cuda.synchronize()
-            for _ in range(3):
-                g.replay()
+            g.replay()
             torch.cuda.synchronize()
             graph = g
         except Exception as e:  # graph capture unavailable: fall back to eager launches
@@ -304,18 +319,17 @@ def main() -> int:
             ctx.bind_current_stream()
             torch.cuda.synchronize()
 
-    steps = args.steps
-    if graph is not None:
-        steps = max(per_graph, (steps + per_graph - 1) // per_graph * per_graph)
     log(f"timing {steps} steps ({'hipGraph' if graph is not None else 'eager'})")
     torch.cuda.synchronize()
     t_start = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
     cur = torch.cuda.current_stream(dev)
+    # keep the GPU busy while the host enqueues the timed launches, so the
+    # region between the two events holds the launches and nothing else
+    torch.cuda._sleep(2_000_000)
     t_start.record(cur)
     if graph is not None:
-        for _ in range(steps // per_graph):
-            graph.replay()
+        graph.replay()
     else:
         for i in range(steps):
             step(i)
@@ -327,9 +341,9 @@ def main() -> int:
     achieved = alg_bytes / (ms_step / 1e3) / 1e9
     log(f"{ms_step * 1e3:.2f} us/step, {rows_per_s / 1e6:.3f} M rows/s, {achieved:.0f} GB/s")
 
-    # parity spot check of the timed outputs against the first warm-up batch
+    # parity spot check: every rotating copy written so far drew the same tokens
     tok0 = S["token_of"](outs[0]).cpu().numpy()
-    for o in outs[1:]:
+    for o in outs[1:min(len(outs), max(steps, args.warmup))]:
         assert (S["token_of"](o).cpu().numpy() == tok0).all(), "rotating buffers disagree"
 
     headline = args.workload == "c2"
@@ -359,8 +373,16 @@ def main() -> int:
                      "traffic": measured_traffic() if headline else None},
     }
     if not args.no_cpu_baseline:
-        log(f"CPU baseline (~{args.cpu_seconds:.0f} s, {args.cpu_threads} thread(s))")
-        result["cpu_baseline"] = cpu_baseline(args.workload, wl, args.cpu_seconds, args.cpu_threads)
+        # all host cores of the box's share (one row per thread), and one thread
+        # (rows one after another, as the reference samples), in the same run
+        threads = args.cpu_threads or host_threads()
+        log(f"CPU baseline (~{args.cpu_seconds:.0f} s on {threads} threads, then 1 thread)")
+        cb = cpu_baseline(args.workload, wl, args.cpu_seconds, threads)
+        if threads > 1:
+            one = cpu_baseline(args.workload, wl, args.cpu_seconds, 1)
+            cb["single_thread"] = {"value": one["value"], "unit": one["unit"], "cores": 1,
+                                   "sample": one["sample"]}
+        result["cpu_baseline"] = cb
     else:
         result["cpu_baseline"] = None
     del S

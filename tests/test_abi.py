@@ -88,6 +88,19 @@ def test_params_tensor_packs_xs_row_params():
     del torch
 
 
+def test_params_tensor_saturates_a_huge_top_k():
+    """The reference's top_k is a usize: 2^32, 2^32 + 20 and usize::MAX are all
+    at least the vocabulary (the whole-row candidate set).  Narrowing must not
+    wrap them to 0 (greedy), 20 or -1."""
+    pytest.importorskip("torch")
+    from xwen_amd import sampler as xsm
+    ks = [1 << 32, (1 << 32) + 20, (1 << 64) - 1, (1 << 31) - 1, 20]
+    raw = xsm.params_tensor(1.0, ks, 0.9, len(ks), "cpu").numpy()
+    p = (_lib.RowParams * len(ks)).from_buffer_copy(raw.tobytes())
+    assert [p[i].top_k for i in range(len(ks))] == [2**31 - 1] * 4 + [20]
+    assert not xsm.SamplerOptions(1.0, 1 << 32, 0.9).is_greedy()
+
+
 def test_keep_confident_through_the_abi(golden):
     from xwen_amd import sampler as xsm
     c = golden["keep_confident"]

@@ -147,3 +147,29 @@ def test_argmax_and_verify_argument_errors(setup):
     assert vf(drafts=None) == E                              # span > 1 needs drafts
     assert vf(accepted=None) == E
     assert vf(seqs=ROWS, span=4) == CAP                      # 32 rows > 8
+
+
+def test_top_k_above_the_contexts_k_max_is_a_row_error():
+    """xs_create's k_max bounds min(top_k, enc): a context made for k_max = 20
+    refuses top_k 21 (and a whole-row top_k on a wider row) per row, with
+    XS_ROW_BAD_PARAM, and draws the other rows; a row narrower than k_max may
+    ask for any top_k (its candidate set is the whole row)."""
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from xwen_amd import sampler as xsm
+    rng = np.random.default_rng(77)
+    ctx = xsm.Context(max_rows=4, vocab=4096, k_max=20)
+    ctx.bind_current_stream()
+    x = torch.as_tensor(rng.normal(0, 2, (4, 4096)).astype(np.float32)).cuda()
+    p = xsm.params_tensor(1.0, np.array([20, 21, 10**9, 0]), 0.9, 4, "cuda")
+    u = torch.full((4,), 0.3, dtype=torch.float32, device="cuda")
+    out = xsm.sample_batch(ctx, x, p, u)
+    torch.cuda.synchronize()
+    assert out.status.cpu().tolist() == [_lib.ROW_OK, _lib.ROW_BAD_PARAM, _lib.ROW_BAD_PARAM,
+                                         _lib.ROW_OK]
+    # 16 encodable ids: top_k 10^9 is the whole 16-id row, within k_max
+    small = torch.as_tensor(rng.normal(0, 2, (4, 16)).astype(np.float32)).cuda()
+    out = xsm.sample_batch(ctx, small, p, u)
+    torch.cuda.synchronize()
+    assert out.status.cpu().tolist() == [_lib.ROW_OK, _lib.ROW_OK, _lib.ROW_OK, _lib.ROW_OK]
+    ctx.close()

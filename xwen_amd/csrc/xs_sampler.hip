@@ -289,7 +289,7 @@ struct Cfg {
   bool greedy, scale, full, bad;
 };
 
-XS_DEV Cfg make_cfg(const xs_row_params& p, int64_t enc, int n_top) {
+XS_DEV Cfg make_cfg(const xs_row_params& p, int64_t enc, int n_top, int k_max) {
   Cfg c;
   c.greedy = (p.temperature <= 0.0) || (p.top_k <= 1);
   c.scale = p.temperature != 1.0;
@@ -309,7 +309,7 @@ XS_DEV Cfg make_cfg(const xs_row_params& p, int64_t enc, int n_top) {
     c.full = false;
   }
   if (n_top > 0) c.kp = max(c.kp, (int)min((int64_t)n_top, enc));
-  c.bad = c.kp > KSEL || (c.full && enc > KSEL);
+  c.bad = c.kp > KSEL || (c.full && enc > KSEL) || (!c.greedy && c.k > k_max);
   return c;
 }
 
@@ -396,6 +396,7 @@ struct Args {
   int32_t* row_ticket;  // [rows * TSTRIDE] workgroups of the row that have published (0 between calls)
   int32_t* seq_ticket;  // [seqs * TSTRIDE] rows of the sequence that are finalized (0 between calls)
   int32_t n_chunks, nslots;
+  int32_t k_max;     // the context's largest top_k (of min(top_k, enc)); larger is XS_ROW_BAD_PARAM
   uint64_t* rec;     // [rows, SRECW, nsp]: word i of sub-record s of a row at i * nsp + s
 };
 
@@ -1850,7 +1851,7 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
   }
   // The row's parameters are read only now, so that round trip overlaps the
   // loads instead of delaying them.
-  const Cfg cfg = a.greedy_all ? greedy_cfg() : make_cfg(a.params[row], a.enc, a.n_top);
+  const Cfg cfg = a.greedy_all ? greedy_cfg() : make_cfg(a.params[row], a.enc, a.n_top, a.k_max);
   const bool stoch = !cfg.greedy && !cfg.bad;
   const int kp = cfg.kp;
   // Sparse controls: the chunk's patches (final values written by
@@ -2446,6 +2447,7 @@ int launch(xs_context* ctx, xs::Args& a, int64_t rows, int span, bool mask, bool
   a.ctl_chunk = ctx->ctl_chunk;
   a.row_ticket = ctx->row_ticket;
   a.seq_ticket = ctx->seq_ticket;
+  a.k_max = ctx->k_max;
   const dim3 g1((unsigned)grid);
   if (ctl && mask) launch2<true, false, true>(ctx, a, rows, g1, order);
   else if (ctl) launch2<false, false, true>(ctx, a, rows, g1, order);

@@ -184,11 +184,16 @@ class Context:
 
 
 def params_tensor(temperature, top_k, top_p, rows: int, device):
-    """Pack per-row (temperature f64, top_k i32, top_p f32) as xs_row_params [rows]."""
+    """Pack per-row (temperature f64, top_k i32, top_p f32) as xs_row_params [rows].
+
+    top_k is the reference's usize: values past INT32_MAX saturate (every
+    such k is at least the vocabulary, the same whole-row candidate set), so
+    no client k wraps into a greedy or a small k."""
     torch = _torch()
     arr = np.zeros(rows, dtype=np.dtype([("t", "<f8"), ("k", "<i4"), ("p", "<f4")]))
     arr["t"] = np.broadcast_to(np.asarray(temperature, np.float64), (rows,))
-    arr["k"] = np.broadcast_to(np.asarray(top_k, np.int64), (rows,)).astype(np.int32)
+    k = np.broadcast_to(np.asarray(top_k, dtype=object), (rows,))
+    arr["k"] = np.asarray([min(max(int(v), -(1 << 31)), (1 << 31) - 1) for v in k], np.int64)
     arr["p"] = np.broadcast_to(np.asarray(top_p, np.float64), (rows,)).astype(np.float32)
     raw = np.frombuffer(arr.tobytes(), dtype=np.uint8).copy()
     return torch.from_numpy(raw).to(device)

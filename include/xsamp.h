@@ -178,6 +178,22 @@ typedef struct {
 
 int xs_sample(xs_context* ctx, const xs_sample_args* args);
 
+/* xs_sample without a context, for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference.  The workspace is one
+ * file-scope device array of XS_NOALLOC_BYTES (9.3 MiB) that each GPU the
+ * library runs on holds until the process ends; the call runs on the current
+ * device and on `hip_stream`, and allocates nothing.  Limits: rows <=
+ * XS_NOALLOC_ROWS and enc <= XS_NOALLOC_VOCAB (else XS_ERR_CAPACITY);
+ * min(top_k, enc) <= XS_K_MAX (else XS_ROW_BAD_PARAM for the row).  Every
+ * call on one GPU shares that GPU's array: calls that overlap on one GPU (two
+ * streams, two threads) race and must not be issued.  Each call clears the
+ * arrival tickets it uses before its launch. */
+#define XS_NOALLOC_ROWS 64
+#define XS_NOALLOC_VOCAB 262144
+#define XS_NOALLOC_BYTES 9722368
+int xs_sample_noalloc(const xs_sample_args* args, void* hip_stream);
+
 /* The speculative verify block: `seqs` sequences of `span` = D + 1 rows each
  * (D drafts plus the bonus position), laid out [seqs, span, ld].  Every row is
  * sampled as xs_sample would, with its own uniform; then each sequence runs

@@ -21,6 +21,9 @@ K_MAX = 127
 TOP_MAX = 128
 CTL_MAX = 2048
 ORDER_MAX = 1024
+NOALLOC_ROWS = 64
+NOALLOC_VOCAB = 262144
+NOALLOC_BYTES = 9722368
 
 _vp = C.c_void_p
 _i64 = C.c_int64
@@ -95,6 +98,8 @@ def load() -> C.CDLL:
     L.xs_set_stream.argtypes = [_vp, _vp]
     L.xs_sample.restype = C.c_int
     L.xs_sample.argtypes = [_vp, C.POINTER(SampleArgs)]
+    L.xs_sample_noalloc.restype = C.c_int
+    L.xs_sample_noalloc.argtypes = [C.POINTER(SampleArgs), _vp]
     L.xs_verify.restype = C.c_int
     L.xs_verify.argtypes = [_vp, C.POINTER(VerifyArgs)]
     L.xs_argmax_probs.restype = C.c_int

@@ -50,6 +50,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 #include <cstring>
 #include <vector>
 #include <math.h>
@@ -2361,12 +2362,44 @@ __global__ void fill_verify_kernel(const xs_verify_args a, int32_t st) {
   }
 }
 
+// Zeroes n ints (the arrival tickets of the no-allocation entry point; a
+// kernel rather than hipMemsetAsync, so a captured call records no memset node).
+__global__ void zero_kernel(int32_t* p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
 __global__ void exp_kernel(const float* x, float* y, int64_t n) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) y[i] = cr_expf(x[i], &xs::kExpT[0][0]);
 }
 
+// Layout of the no-allocation entry point's workspace (xs_sample_noalloc): a
+// context of NA_ROWS rows of up to NA_VOCAB ids with k_max = XS_K_MAX, carved
+// out of one file-scope device array in u64 words, each part 256-byte aligned.
+constexpr int64_t NA_ROWS = XS_NOALLOC_ROWS;
+constexpr int64_t NA_VOCAB = XS_NOALLOC_VOCAB;
+constexpr int64_t NA_CHUNKS = ((NA_VOCAB + SLOT - 1) / SLOT + SPC - 1) / SPC;
+constexpr int64_t NA_NSP = (NA_CHUNKS * NWAVE + 63) / 64 * 64;
+constexpr int64_t na_up(int64_t w) { return (w + 31) / 32 * 32; }
+constexpr int64_t NA_OFF_REC = 0;
+constexpr int64_t NA_OFF_PATCH = na_up(NA_OFF_REC + NA_ROWS * NA_NSP * SRECW);
+constexpr int64_t NA_OFF_CTLROW = na_up(NA_OFF_PATCH + NA_ROWS * CTL_MAX);
+constexpr int64_t NA_OFF_CTLCHUNK = na_up(NA_OFF_CTLROW + NA_ROWS * (int64_t)sizeof(CtlRow) / 8);
+constexpr int64_t NA_OFF_TICKET = na_up(NA_OFF_CTLCHUNK + (NA_ROWS * (NA_CHUNKS + 1) + 1) / 2);
+constexpr int64_t NA_TICKETS = NA_ROWS * TSTRIDE;  // ints
+constexpr int64_t NA_OFF_SEQ = na_up(NA_OFF_TICKET + NA_TICKETS / 2);
+constexpr int64_t NA_OFF_STATUS = na_up(NA_OFF_SEQ + NA_TICKETS / 2);
+constexpr int64_t NA_WORDS = na_up(NA_OFF_STATUS + NA_ROWS / 2);
+static_assert(sizeof(CtlRow) % 8 == 0, "CtlRow packs into u64 words");
+static_assert(NA_WORDS * 8 == XS_NOALLOC_BYTES, "XS_NOALLOC_BYTES states the array's size");
+
 }  // namespace xs
+
+// The no-allocation entry point's workspace.  Each GPU holds its own copy at
+// its own address until the process ends; host code never passes this name
+// to a kernel, only the address hipGetSymbolAddress returns for the device.
+static __device__ __align__(256) uint64_t scratch[xs::NA_WORDS];
 
 // ---------------------------------------------------------------------------
 // Host side: the context and the C ABI.
@@ -2520,7 +2553,14 @@ int xs_set_stream(xs_context* c, void* s) {
   return XS_OK;
 }
 
-int xs_sample(xs_context* ctx, const xs_sample_args* in) {
+namespace {
+int sample_impl(xs_context* ctx, const xs_sample_args* in, bool clear_tickets);
+}
+
+int xs_sample(xs_context* ctx, const xs_sample_args* in) { return sample_impl(ctx, in, false); }
+
+namespace {
+int sample_impl(xs_context* ctx, const xs_sample_args* in, bool clear_tickets) {
   if (!ctx || !in || !in->token || !in->status) return XS_ERR_ARG;
   const Call c{in->logits, in->rows, in->ld, in->width, in->enc, in->params, in->uniforms,
                in->allowed, in->allowed_words, in->allowed_ld};
@@ -2581,7 +2621,57 @@ int xs_sample(xs_context* ctx, const xs_sample_args* in) {
   a.n_chunks = chunks_for(in->enc);
   a.nslots = (int32_t)slots_for(in->enc);
   a.rec = ctx->rec;
+  if (clear_tickets && in->rows > 0) {
+    const int64_t n = in->rows * xs::TSTRIDE;
+    hipLaunchKernelGGL(xs::zero_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, ctx->stream,
+                       ctx->row_ticket, n);
+  }
   return launch(ctx, a, in->rows, 1, in->allowed != nullptr, lse, in->row_order);
+}
+}  // namespace
+
+// The device address of `scratch` on each device, looked up once per device
+// (with that device current) and kept for the process.
+namespace {
+constexpr int NA_MAX_DEVICES = 64;
+std::mutex na_mu;
+uint64_t* na_ptr[NA_MAX_DEVICES];
+
+uint64_t* noalloc_scratch(int dev) {
+  std::lock_guard<std::mutex> g(na_mu);
+  if (!na_ptr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return nullptr;
+    na_ptr[dev] = (uint64_t*)p;
+  }
+  return na_ptr[dev];
+}
+}  // namespace
+
+int xs_sample_noalloc(const xs_sample_args* in, void* hip_stream) {
+  if (!in) return XS_ERR_ARG;
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess) return XS_ERR_HIP;
+  if (dev < 0 || dev >= NA_MAX_DEVICES) return XS_ERR_CAPACITY;
+  uint64_t* base = noalloc_scratch(dev);
+  if (!base) return XS_ERR_HIP;
+  // a context on the host stack that describes the static workspace
+  xs_context c;
+  memset(&c, 0, sizeof(c));
+  c.device = dev;
+  c.stream = (hipStream_t)hip_stream;
+  c.max_rows = xs::NA_ROWS;
+  c.vocab = xs::NA_VOCAB;
+  c.k_max = XS_K_MAX;
+  c.max_chunks = (int32_t)xs::NA_CHUNKS;
+  c.rec = base + xs::NA_OFF_REC;
+  c.ctl_patch = base + xs::NA_OFF_PATCH;
+  c.ctl_row = reinterpret_cast<xs::CtlRow*>(base + xs::NA_OFF_CTLROW);
+  c.ctl_chunk = reinterpret_cast<int32_t*>(base + xs::NA_OFF_CTLCHUNK);
+  c.row_ticket = reinterpret_cast<int32_t*>(base + xs::NA_OFF_TICKET);
+  c.seq_ticket = reinterpret_cast<int32_t*>(base + xs::NA_OFF_SEQ);
+  c.row_status = reinterpret_cast<int32_t*>(base + xs::NA_OFF_STATUS);
+  return sample_impl(&c, in, true);
 }
 
 int xs_verify(xs_context* ctx, const xs_verify_args* in) {

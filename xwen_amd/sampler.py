@@ -224,6 +224,40 @@ def sample_batch(ctx: Context, logits, params, uniforms, *, enc: int | None = No
     params: the uint8 tensor from params_tensor; uniforms: float32 [rows];
     order: an optional host permutation of the rows (see cost_order), the
     order in which the launch starts them."""
+    a, out, keep = _sample_args(logits, params, uniforms, enc=enc, width=width, allowed=allowed,
+                                allowed_words=allowed_words, cand_k=cand_k, stats=stats,
+                                n_top=n_top, out=out, controls=controls, order=order)
+    rc = ctx.lib.xs_sample(ctx.h, C.byref(a))
+    del keep
+    if check:
+        _lib.check(rc, "xs_sample")
+    return out
+
+
+def sample_batch_noalloc(logits, params, uniforms, *, stream=None, check: bool = True,
+                         **kw) -> Draws:
+    """The same draw through xs_sample_noalloc: no context, the library's static
+    workspace on the current device (rows <= NOALLOC_ROWS, enc <= NOALLOC_VOCAB),
+    on `stream` (default: torch's current stream).  Returns (Draws, rc) when
+    check is False."""
+    torch = _torch()
+    lib = _lib.load()
+    a, out, keep = _sample_args(logits, params, uniforms, **kw)
+    s = torch.cuda.current_stream(logits.device) if stream is None else stream
+    rc = lib.xs_sample_noalloc(C.byref(a), C.c_void_p(s.cuda_stream))
+    del keep
+    if check:
+        _lib.check(rc, "xs_sample_noalloc")
+        return out
+    return out, rc
+
+
+def _sample_args(logits, params, uniforms, *, enc: int | None = None, width: int | None = None,
+                 allowed=None, allowed_words: int | None = None, cand_k: int = 0,
+                 stats: bool = False, n_top: int = 0, out: Draws | None = None,
+                 controls: Controls | None = None, order=None):
+    """xs_sample_args for one call, the output tensors, and the host arrays the
+    call reads (kept alive by the caller through the call)."""
     torch = _torch()
     rows, ld = logits.shape
     dev = logits.device
@@ -280,11 +314,7 @@ def sample_batch(ctx: Context, logits, params, uniforms, *, enc: int | None = No
         if keep.shape != (rows,):  # the library reads exactly `rows` entries
             raise ValueError(f"order must list each of the {rows} rows once, got shape {keep.shape}")
         a.row_order = keep.ctypes.data
-    rc = ctx.lib.xs_sample(ctx.h, C.byref(a))
-    del keep
-    if check:
-        _lib.check(rc, "xs_sample")
-    return out
+    return a, out, keep
 
 
 def cost_order(temperature, top_k, *, controlled=None) -> np.ndarray:

@@ -191,7 +191,7 @@ int xs_sample(xs_context* ctx, const xs_sample_args* args);
  * arrival tickets it uses before its launch. */
 #define XS_NOALLOC_ROWS 64
 #define XS_NOALLOC_VOCAB 262144
-#define XS_NOALLOC_BYTES 9722368
+#define XS_NOALLOC_BYTES 9787904
 int xs_sample_noalloc(const xs_sample_args* args, void* hip_stream);
 
 /* The speculative verify block: `seqs` sequences of `span` = D + 1 rows each

@@ -570,17 +570,21 @@ XS_DEV uint64_t pick64(const uint64_t (&x)[R], int i) {
 //   w1  c_s (f32 bits) | c_r (f32 bits) << 32: the partials' offsets
 //   w2  R (f64 bits): sum of e^(v - c_r) over the raw logits (held_row)
 //   w3  wave max (f32 bits) | flags << 32 (1 NaN seen, 2 a finite value
-//       seen, 4 entries in descending order)
+//       seen, 4 entries in descending order, 8 w8/w9 hold fold data)
 //   w4  entry count
 //   w5  bound keys 0 | 1 << 32;  w6  bound keys 2 | 3 << 32
 //   w7  the filter's floor (f32 bits): the entries are every element of the
 //       wave at or above it; +inf when they are not (an overflow)
-//   w8..  entries: pack(key, id) of the wave's candidates
+//   w8  held_row fold data (flag 8; see held_fold): in a chunk whose own max
+//       m_c dominates it, the f64 sum of this wave's terms exp(f64(v - m_c))
+//       before the chunk's first maximal id
+//   w9  and the sum (f64) of rint(2^52 * term) over its terms after that id
+//   w10.. entries: pack(key, id) of the wave's candidates
 // A row has n_chunks * NWAVE sub-records, chunk-major, stored transposed:
 // word i of sub-record s sits at i * nsp + s of the row's block (nsp = the
 // sub-record count rounded up to 64), so the finalizer's lanes read one word
 // of 64 sub-records with one coalesced load.
-constexpr int SHDR = 8;
+constexpr int SHDR = 10;
 constexpr int CAPW = 256;           // entries per sub-record
 constexpr int SRECW = SHDR + CAPW;
 constexpr int NHW = 7;              // header words the finalizer reads
@@ -593,6 +597,25 @@ struct ChunkLds {
   uint32_t groupmax[BLOCK / 4];     // maxima of 4-lane groups
   uint32_t lanemax[BLOCK];          // lane maxima
   int32_t last;                     // this workgroup took the row's last ticket
+  // held_row launches: each wave's max, f64 partial (offset: that max) and
+  // first maximal id, for the chunk's own fold data
+  float wmax[NWAVE];
+  uint32_t wtop[NWAVE];
+  uint32_t wprev[NWAVE];            // the row's running max key before each wave's update
+  double wr[NWAVE];
+};
+// What the finalizing wave leaves for held_row's fold (held_fold), which the
+// whole workgroup runs after it: the row statistics and the top-n logits.
+struct HeldLds {
+  double R_d;                       // exactly summed denominator
+  double pre[4];                    // per wave: terms before the argmax
+  long long post[4];                // per wave: 2^-52 units of the terms after it
+  float m_v;                        // row max
+  uint32_t top;                     // first maximal id
+  int32_t ok;                       // statistics defined (no NaN, finite max)
+  int32_t can_fold;                 // the argmax is known (not a row refused for its top_k)
+  int32_t n_have;                   // top-n entries below
+  float vals[XS_TOP_MAX];           // top-n logits, (logit desc, id asc)
 };
 struct FinLds {
   uint64_t list[SURV];              // gathered survivors
@@ -600,6 +623,7 @@ struct FinLds {
   uint64_t psel[KSEL];              // the candidate set in draw order: (p bits << 32) | ~id
   double expt[64];                  // kExpT, flattened
   uint32_t keys[GMAX * 64 * 4];     // published bound keys (more than 64 sub-records)
+  HeldLds held;
 };
 // The chunk pass stages each wave's entries here before it publishes them;
 // after the hand-off only the row's last workgroup uses the memory again, as
@@ -850,6 +874,187 @@ XS_DEV double red_sumd(double v) {
 #undef XS_ROWRED
 
 // ---------------------------------------------------------------------------
+// held_row's denominator as the reference folds it (generate.rs:1931-1932):
+// the f64 terms exp(f64(v - max)) summed one after another in id order.
+//
+// Once the max's own term (exactly 1.0) is in, a running sum in [1, 2) rounds
+// every later term to its grid of 2^-52: a term below 2^-53 is absorbed, a
+// larger one lands on a multiple of 2^-52.  So while the sum stays below 2,
+// the fold equals rn(1 + pre) + 2^-52 * sum_i rint(t_i * 2^52) over the terms
+// t_i after the argmax, where pre is the sum of the terms before it -- an
+// integer sum, in any order.  On rows like that (a dominant token) the exact
+// sum of the same terms differs from the fold by up to the whole of
+// (denominator - 1), that is up to 100 % of the top log-prob; from 2 up the
+// fold's rounding moves lse by less than V * 2^-53 while |log-prob| >= ln 2,
+// and the exactly summed R_d stands.
+//
+// Every sub-record wholly before the argmax adds its f64 partial to pre.  The
+// argmax's own chunk, whose waves interleave ids before and after it, adds the
+// fold data its streaming pass published (taken at the chunk's max, which is
+// the row max there).  A sub-record after it whose max lies within 36.74 of
+// the row max may hold terms of 2^-53 or more: they come from its candidate
+// entries when its filter floor lies below them all; every other term there
+// is absorbed.  Only what none of this covers is read from the logits again.
+
+// Below this f32 difference v - max, exp(f64(v - max)) < 2^-53: a term that a
+// running sum in [1, 2) absorbs (ln 2^-53 = -36.7368).
+constexpr float LN_HALF_ULP1 = -36.74f;
+
+// exp(x) in f64 for x <= 0 (x >= -700; below, 0), to about 1e-16 relative:
+// the correctly rounded exp's reduction and table, without its final rounding.
+template <typename TAB>
+XS_DEV double exp_f64(double x, TAB T) {
+  if (!(x >= -700.0)) return 0.0;
+  const double kd = __builtin_rint(x * XS_EXP_INV_L);
+  const int k = (int)kd;
+  const double r1 = __builtin_fma(-kd, XS_EXP_L_HI, x);
+  const double r = r1 - kd * XS_EXP_L_LO;
+  double h = 1.0 / 5040.0;
+  h = __builtin_fma(h, r, 1.0 / 720.0);
+  h = __builtin_fma(h, r, 1.0 / 120.0);
+  h = __builtin_fma(h, r, 1.0 / 24.0);
+  h = __builtin_fma(h, r, 1.0 / 6.0);
+  h = __builtin_fma(h, r, 0.5);
+  const double em1 = __builtin_fma(r * r, h, r);  // exp(r) - 1
+  const int j = k & 31;
+  const int e = (k - j) / 32;
+  const double th = T[2 * j], tl = T[2 * j + 1];
+  const double v = th + __builtin_fma(th, em1, tl * (1.0 + em1));
+  return v * __longlong_as_double((long long)((uint64_t)(e + 1023) << 52));
+}
+
+// The workgroup's four waves share the re-reads (one sub-record each at a
+// time, all 16 slots' loads in flight); wave 0 adds the partials of the
+// sub-records wholly before the argmax.  Then wave 0 writes row_lse and the
+// top-n log-probs.  Contains barriers: all waves of the workgroup call it.
+template <int NW>
+XS_DEV void held_fold(const Args& a, int row, const float* rowp, const uint64_t* rowrec, int nsp,
+                      int nsub, FinLds& F) {
+  HeldLds& H = F.held;
+  const int lane = lane_id(), wave = wave_id();
+  const int enc = (int)a.enc;
+  const float m_v = H.m_v;
+  const double R_d = H.R_d;
+  const uint32_t top = H.top;
+  const bool fold = H.ok && H.can_fold && R_d < 2.0;
+  const double* T = F.expt;
+  double pre = 0.0;
+  long long post = 0;
+  if (fold) {
+    const int jc = (int)(top / (uint32_t)(SPC * SLOT));  // the argmax's chunk
+    int nth = 0;  // re-read sub-records met so far, dealt to the waves in turn
+    for (int g = 0; g * 64 < nsub; g++) {
+      const int s = g * 64 + lane;
+      const bool has = s < nsub;
+      const uint64_t h1 = has ? ld_agent(&rowrec[1 * nsp + s]) : 0ull;
+      const uint64_t h2 = has ? ld_agent(&rowrec[2 * nsp + s]) : 0ull;
+      const uint64_t h3 = has ? ld_agent(&rowrec[3 * nsp + s]) : 0ull;
+      const uint64_t h4 = has ? ld_agent(&rowrec[4 * nsp + s]) : 0ull;
+      const uint64_t h7 = has ? ld_agent(&rowrec[7 * nsp + s]) : 0ull;
+      const uint64_t h8 = has ? ld_agent(&rowrec[8 * nsp + s]) : 0ull;
+      const uint64_t h9 = has ? ld_agent(&rowrec[9 * nsp + s]) : 0ull;
+      const int c = s / NWAVE;
+      const float mw = __uint_as_float((uint32_t)h3);
+      const bool fold_data = ((h3 >> 32) & 8u) != 0;
+      // Wholly before the argmax: the wave's f64 partial joins pre (its terms
+      // carry ~2e-6 relative error, so pre does, and so does denominator - 1).
+      // The argmax's chunk: its own fold data, taken at its max, the row max.
+      // After it: absorbed when every term is below 2^-53; else the terms of
+      // 2^-53 or more come from the entries when the filter's floor lies below
+      // them all (e^-36.75 < 2^-53 with room for the f32 difference).
+      const bool after_big = has && c > jc && (mw - m_v) >= LN_HALF_ULP1;
+      const float fl = __uint_as_float((uint32_t)h7);
+      const bool from_entries = after_big && (fl - m_v) <= -36.75f;
+      const bool reread = has && ((c == jc && !fold_data) || (after_big && !from_entries));
+      if (wave == 0 && has && c < jc) {
+        const double r = __longlong_as_double((long long)h2);
+        if (r != 0.0) pre += r * (double)xexp2((__uint_as_float((uint32_t)(h1 >> 32)) - m_v) * LOG2E);
+      }
+      if (wave == 0 && has && c == jc && fold_data) {
+        pre += __longlong_as_double((long long)h8);
+        post += (long long)__longlong_as_double((long long)h9);
+      }
+      if (wave == 0 && from_entries) {
+        const int cnt = (int)min((uint32_t)h4, (uint32_t)CAPW);
+        for (int j = 0; j < cnt; j++) {
+          const float v = keyf(pk_key(ld_agent(&rowrec[(int64_t)(SHDR + j) * nsp + s])));
+          const float x = v - m_v;
+          if (x >= LN_HALF_ULP1) post += (long long)__builtin_rint(exp_f64((double)x, T) * 0x1p52);
+        }
+      }
+      uint64_t m = __ballot(reread);
+      while (m) {  // one sub-record's elements: wave w of chunk cc
+        const int sr = g * 64 + (int)__builtin_ctzll(m);
+        m &= m - 1ull;
+        if ((nth++ % NW) != wave) continue;
+        const int cc = sr / NWAVE, w = sr % NWAVE;
+        float4 v[SPC];
+#pragma unroll
+        for (int jj = 0; jj < SPC; jj++) {
+          const int id0 = ((cc * SPC + jj) * SLOT) + 4 * (w * 64 + lane);
+          v[jj] = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+          if (id0 < enc) v[jj] = reinterpret_cast<const float4*>(rowp)[id0 >> 2];
+        }
+#pragma unroll
+        for (int jj = 0; jj < SPC; jj++) {
+          const int id0 = ((cc * SPC + jj) * SLOT) + 4 * (w * 64 + lane);
+          const float xv[4] = {v[jj].x, v[jj].y, v[jj].z, v[jj].w};
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const int id = id0 + e;
+            const float x = xv[e] - m_v;  // f32, as the reference's v - max
+            if (id < enc && (uint32_t)id != top) {
+              if (x >= LN_HALF_ULP1) {  // a term of 2^-53 or more: exactly
+                const double t = exp_f64((double)x, T);
+                if ((uint32_t)id < top) pre += t;
+                else post += (long long)__builtin_rint(t * 0x1p52);
+              } else if ((uint32_t)id < top) {  // below it: only pre holds it, to ~2e-6
+                pre += (double)xexp2(x * LOG2E);
+              }
+            }
+          }
+        }
+      }
+    }
+    pre = wave_sumd(pre);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const long long lo = (long long)(uint32_t)xor_lane((int)(uint32_t)post, o);
+      const long long hi = (long long)xor_lane((int)(post >> 32), o);
+      post += (hi << 32) | lo;
+    }
+  }
+  if (lane == 0) {
+    H.pre[wave] = pre;
+    H.post[wave] = post;
+  }
+  if (NW > 1) __syncthreads();
+  if (wave != 0) return;
+  double D = R_d;
+  if (fold) {
+    double p4 = 0.0;
+    long long q4 = 0;
+#pragma unroll
+    for (int w = 0; w < NW; w++) {
+      p4 += H.pre[w];
+      q4 += H.post[w];
+    }
+    const double Dn = (1.0 + p4) + (double)q4 * 0x1p-52;
+    if (Dn < 2.0) D = Dn;
+  }
+  const double lse = H.ok ? (double)m_v + log(D) : __builtin_nan("");
+  if (lane == 0 && a.row_lse) a.row_lse[row] = lse;
+  if (a.top_logprob) {
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+      const int i = r * 64 + lane;
+      if (i < a.n_top)
+        a.top_logprob[(int64_t)row * a.top_ld + i] = i < H.n_have ? (float)((double)H.vals[i] - lse) : __builtin_nanf("");
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Row finalize, common case: at most 64 sub-records (one per lane), K' <= 64,
 // at most SURV survivors, and no boundary
 // tie that needs the id-ordered row scan.  Returns false (having written
@@ -857,7 +1062,8 @@ XS_DEV double red_sumd(double v) {
 // does the row.  Same arithmetic, in the same order, as the general path.
 template <bool HAS_MASK, bool WANT_LSE>
 XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, int nsub, const uint64_t (&h)[NHW],
-                     const uint64_t (&E)[EPRE], const uint64_t* rowrec, int nsp, FinLds& F) {
+                     const uint64_t (&E)[EPRE], const uint64_t* rowrec, int nsp, const float* rowp,
+                     FinLds& F) {
   const int lane = lane_id();
   const bool live = lane < nsub;
   const bool stoch = !cfg.greedy;
@@ -1063,6 +1269,22 @@ XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, int nsub, const uin
     tok = (int)pk_id(rdl64(sel, 0));
   }
 
+  // held_row: the statistics for held_fold, which writes row_lse and the
+  // top-n log-probs once the workgroup has folded the denominator
+  const bool lse_ok = !nan_seen && !__builtin_isinf(m_v);
+  if (WANT_LSE && (a.row_lse || a.n_top > 0)) {
+    const int nh = min(min(a.n_top, (int)a.enc), nsel);
+    if (lane == 0) {
+      F.held.R_d = R_d;
+      F.held.m_v = m_v;
+      F.held.top = pk_id(rdl64(sel, 0));
+      F.held.ok = lse_ok ? 1 : 0;
+      F.held.can_fold = 1;
+      F.held.n_have = nh;
+    }
+    if (lane < nh) F.held.vals[lane] = keyf(pk_key(sel));
+  }
+
   // Outputs.
   if (lane == 0) {
     st_agent(&a.token[row], st == XS_ROW_OK ? tok : -1);
@@ -1072,8 +1294,7 @@ XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, int nsub, const uin
     if (a.soft_sum) a.soft_sum[row] = S;
     if (WANT_LSE) {
       if (a.row_max) a.row_max[row] = m_v;
-      if (a.row_lse) a.row_lse[row] = (!nan_seen && !__builtin_isinf(m_v)) ? (double)m_v + log(R_d) : __builtin_nan("");
-      if (a.p_max) a.p_max[row] = (!nan_seen && !__builtin_isinf(m_v)) ? (float)(1.0 / R_d) : __builtin_nanf("");
+      if (a.p_max) a.p_max[row] = lse_ok ? (float)(1.0 / R_d) : __builtin_nanf("");
     }
   }
   if (want_cands && stoch && st == XS_ROW_OK) {
@@ -1083,19 +1304,12 @@ XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, int nsub, const uin
       if (a.cand_w) a.cand_w[(int64_t)row * a.cand_ld + lane] = w;
     }
   }
-  if (WANT_LSE && a.n_top > 0) {
-    const bool ok = !nan_seen && !__builtin_isinf(m_v);
-    const double lse = ok ? (double)m_v + log(R_d) : __builtin_nan("");
+  if (WANT_LSE && a.n_top > 0 && a.top_id) {
     const int nt = min(a.n_top, (int)a.enc);
 #pragma unroll
     for (int r = 0; r < 2; r++) {
       const int i = r * 64 + lane;
-      if (i < a.n_top) {
-        const bool have = r == 0 && i < nt && i < nsel;
-        if (a.top_id) a.top_id[(int64_t)row * a.top_ld + i] = have ? (int32_t)pk_id(sel) : -1;
-        if (a.top_logprob)
-          a.top_logprob[(int64_t)row * a.top_ld + i] = have ? (float)((double)keyf(pk_key(sel)) - lse) : __builtin_nanf("");
-      }
+      if (i < a.n_top) a.top_id[(int64_t)row * a.top_ld + i] = (r == 0 && i < nt && i < nsel) ? (int32_t)pk_id(sel) : -1;
     }
   }
   return true;
@@ -1705,6 +1919,25 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
     }
   }
 
+  // held_row: the statistics for held_fold, which writes row_lse and the
+  // top-n log-probs once the workgroup has folded the denominator; a row
+  // refused for its top_k (no selection gathered) keeps the exact sum
+  const bool lse_ok = !nan_seen && !__builtin_isinf(m_v);
+  if (WANT_LSE && (a.row_lse || a.n_top > 0)) {
+    const int nh = cfg.bad ? 0 : min(min(a.n_top, enc), nsel);
+    if (lane == 0) {
+      F.held.R_d = R_d;
+      F.held.m_v = m_v;
+      F.held.top = cfg.bad ? 0u : rdl(pk_id(sel[0]), 0);
+      F.held.ok = lse_ok ? 1 : 0;
+      F.held.can_fold = cfg.bad ? 0 : 1;
+      F.held.n_have = nh;
+    }
+#pragma unroll
+    for (int r = 0; r < 2; r++)
+      if (r * 64 + lane < nh) F.held.vals[r * 64 + lane] = keyf(pk_key(sel[r]));
+  }
+
   // Outputs.
   if (lane == 0) {
     st_agent(&a.token[row], st == XS_ROW_OK ? tok : -1);
@@ -1714,11 +1947,7 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
     if (a.soft_sum) a.soft_sum[row] = S;
     if (WANT_LSE) {
       if (a.row_max) a.row_max[row] = m_v;
-      if (a.row_lse) {
-        const bool ok = !nan_seen && !__builtin_isinf(m_v);
-        a.row_lse[row] = ok ? (double)m_v + log(R_d) : __builtin_nan("");
-      }
-      if (a.p_max) a.p_max[row] = (!nan_seen && !__builtin_isinf(m_v)) ? (float)(1.0 / R_d) : __builtin_nanf("");
+      if (a.p_max) a.p_max[row] = lse_ok ? (float)(1.0 / R_d) : __builtin_nanf("");
     }
   }
   if (want_cands && stoch && st == XS_ROW_OK) {
@@ -1732,19 +1961,13 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
       }
     }
   }
-  if (WANT_LSE && a.n_top > 0) {
-    const bool ok = !nan_seen && !__builtin_isinf(m_v);
-    const double lse = ok ? (double)m_v + log(R_d) : __builtin_nan("");
+  if (WANT_LSE && a.n_top > 0 && a.top_id) {
     const int nt = min(a.n_top, enc);
 #pragma unroll
     for (int r = 0; r < 2; r++) {
       const int i = r * 64 + lane;
-      if (i < a.n_top) {
-        const bool have = i < nt && i < nsel && !cfg.bad;
-        if (a.top_id) a.top_id[(int64_t)row * a.top_ld + i] = have ? (int32_t)pk_id(sel[r]) : -1;
-        if (a.top_logprob)
-          a.top_logprob[(int64_t)row * a.top_ld + i] = have ? (float)((double)keyf(pk_key(sel[r])) - lse) : __builtin_nanf("");
-      }
+      if (i < a.n_top)
+        a.top_id[(int64_t)row * a.top_ld + i] = (i < nt && i < nsel && !cfg.bad) ? (int32_t)pk_id(sel[r]) : -1;
     }
   }
 
@@ -1770,7 +1993,7 @@ XS_DEV void finalize_row(const Args& a, const Cfg& cfg, int row, const uint64_t*
   CtlRow cr{};
   if (HAS_CTL) cr = a.ctl_row[row];
   const bool done = !(HAS_CTL && cr.active) && nsub <= 64 && cfg.kp <= 64 && !cfg.bad &&
-                    fin_fast<HAS_MASK, WANT_LSE>(a, cfg, row, nsub, h, E, rowrec, nsp, F);
+                    fin_fast<HAS_MASK, WANT_LSE>(a, cfg, row, nsub, h, E, rowrec, nsp, rowp, F);
   if (!done) fin_general<HAS_MASK, WANT_LSE, HAS_CTL>(a, cfg, row, rowrec, nsp, nsub, rowp, mrow, cr, h, E, F);
 
   if (a.span > 0) {
@@ -2045,6 +2268,17 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
     if ((lane & 3) == 0) Lc.groupmax[wave * 16 + (lane >> 2)] = g;
     Lc.lanemax[tid] = km;
   }
+  // held_row launches: the wave's max and f64 partial, and the row's running
+  // max key (a relaxed atomic max, slot 1 of the row's ticket line) as it was
+  // before this wave's update: a chunk that sees a larger max already
+  // published cannot hold the row's argmax, and skips its fold data
+  const bool held = WANT_LSE && (a.row_lse != nullptr || a.n_top > 0);
+  if (held && lane == 0) {
+    uint32_t* const rmax = reinterpret_cast<uint32_t*>(&a.row_ticket[row * TSTRIDE + 1]);
+    Lc.wprev[wave] = __hip_atomic_fetch_max(rmax, fkey(m_w), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    Lc.wmax[wave] = m_w;
+    Lc.wr[wave] = R;
+  }
   __syncthreads();
   uint32_t tk = 0;
   // Keys this sub-record publishes for the row's survivor bound, keys of
@@ -2086,6 +2320,89 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
         for (int r = 0; r < 4; r++) n += (int)__popcll(__ballot(all[r] >= c));
         if (n >= kp) tk = c;
       }
+    }
+  }
+
+  // held_row fold data (held_fold reads it for the row's argmax chunk): when
+  // the chunk's own terms relative to its max m_c sum below 2 -- every chunk
+  // that can hold the argmax of a row whose fold applies -- and no larger max
+  // was published before it, this wave's terms before the chunk's first
+  // maximal id top_c go to an f64 sum and its terms of 2^-53 or more after
+  // top_c to integer units of 2^-52 (an f64 sum of integers, exact below
+  // 2^53).  The terms are f32 exps with the argument split in two, about
+  // 2e-7 relative: within that of the reference's f64 terms, and for a term
+  // after top_c rint(2^52 t) moves by at most 2e-7 of its own size plus a
+  // rare flip of one unit at a half, so both sums, and denominator - 1, stay
+  // within ~1e-6 of the reference's.
+  uint64_t hw8 = 0, hw9 = 0;
+  if (held) {
+    float m_c = Lc.wmax[0];
+    uint32_t prev = Lc.wprev[0];
+#pragma unroll
+    for (int w = 1; w < NWAVE; w++) {
+      m_c = fmaxf(m_c, Lc.wmax[w]);
+      prev = max(prev, Lc.wprev[w]);
+    }
+    double D_c = 0.0;
+#pragma unroll
+    for (int w = 0; w < NWAVE; w++) {
+      const double r = Lc.wr[w];
+      if (r != 0.0) D_c += r * (double)xexp2((Lc.wmax[w] - m_c) * LOG2E);
+    }
+    if (__builtin_isfinite(m_c) && D_c < 2.0 && prev <= fkey(m_c)) {  // uniform in the workgroup
+      // the chunk's first maximal id: the wave's first (ids rise with the
+      // slot, then the lane, then the element), then the least of the waves'
+      uint32_t fid = 0xFFFFFFFFu;
+      if (m_w == m_c) {
+        if (mr == m_c) {
+#pragma unroll
+          for (int j = SPC - 1; j >= 0; j--)
+#pragma unroll
+            for (int e = 3; e >= 0; e--)
+              fid = (q4(q[j], e) == m_c) ? (uint32_t)((s0 + j) * SLOT + 4 * tid + e) : fid;
+        }
+        fid = ~((uint32_t)red_maxi((int)(~fid ^ 0x80000000u)) ^ 0x80000000u);
+      }
+      if (lane == 0) Lc.wtop[wave] = fid;
+      __syncthreads();
+      uint32_t top_c = Lc.wtop[0];
+#pragma unroll
+      for (int w = 1; w < NWAVE; w++) top_c = min(top_c, Lc.wtop[w]);
+      const int jt = (int)(top_c / (uint32_t)SLOT) - s0;  // top_c's slot in the chunk
+      const int rt = (int)(top_c % (uint32_t)SLOT);       // and its place in that slot
+      // exp(d), d <= 0, as exp2 of d*log2e carried in two parts
+      auto ex = [&](float d0) __attribute__((always_inline)) -> float {
+        const float d = fmaxf(d0, -200.0f);  // -inf (an absent id) gives 0, not a NaN
+        const float hi = d * LOG2E;
+        const float lo = __builtin_fmaf(d, LOG2E, -hi) + d * 1.925963033500011e-08f;
+        const float e2 = xexp2(hi);
+        return e2 + e2 * (lo * 0.6931471805599453f);
+      };
+      double pre = 0.0, post = 0.0;
+#pragma unroll
+      for (int j = 0; j < SPC; j++) {
+        const float x4[4] = {q[j].x, q[j].y, q[j].z, q[j].w};
+        if (j < jt) {  // before top_c
+          pre += (double)((ex(x4[0] - m_c) + ex(x4[1] - m_c)) + (ex(x4[2] - m_c) + ex(x4[3] - m_c)));
+        } else if (j == jt) {  // the slot of top_c: before it, then after it
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const int o = 4 * tid + e;
+            const float d = x4[e] - m_c;
+            if (o < rt) pre += (double)ex(d);
+            else if (o > rt && d >= LN_HALF_ULP1) post += (double)__builtin_rintf(ex(d) * 0x1p52f);
+          }
+        } else if (__ballot((gm[j] - m_c) >= LN_HALF_ULP1)) {  // after top_c: terms of 2^-53 or more
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const float d = x4[e] - m_c;
+            if (d >= LN_HALF_ULP1) post += (double)__builtin_rintf(ex(d) * 0x1p52f);
+          }
+        }
+      }
+      hw8 = (uint64_t)__double_as_longlong(red_sumd(pre));
+      hw9 = (uint64_t)__double_as_longlong(red_sumd(post));
+      flags |= 8u;
     }
   }
 
@@ -2162,6 +2479,8 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
       v = i == 5 ? w5 : v;
       v = i == 6 ? w6 : v;
       v = i == 7 ? w7 : v;
+      v = i == 8 ? hw8 : v;
+      v = i == 9 ? hw9 : v;
       if (i >= SHDR) v = stg[i - SHDR];
       st_agent(sub + (uint32_t)i * (uint32_t)nsp, v);
     }
@@ -2175,11 +2494,18 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
   if (tid == 0) {
     const int t = __hip_atomic_fetch_add(&a.row_ticket[row * TSTRIDE], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     Lc.last = (t == nc - 1) ? 1 : 0;
-    if (t == nc - 1) st_agent(&a.row_ticket[row * TSTRIDE], 0);
+    if (t == nc - 1) {
+      st_agent(&a.row_ticket[row * TSTRIDE], 0);
+      st_agent(&a.row_ticket[row * TSTRIDE + 1], 0);  // held_row's running max key
+    }
   }
   __syncthreads();
-  if (!Lc.last || wave != 0) return;
+  if (!Lc.last) return;
+  // held_row outputs: after the row is finalized, its finalizing wave folds
+  // the denominator as the reference does (held_fold)
+  if (wave != 0) return;
   finalize_row<HAS_MASK, WANT_LSE, HAS_CTL>(a, cfg, row, rowrec, nsp, nc * NWAVE, rowp, mrow, Tl.fin);
+  if (held) held_fold<1>(a, row, rowp, rowrec, nsp, nc * NWAVE, Tl.fin);
 }
 
 // ---------------------------------------------------------------------------

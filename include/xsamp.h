@@ -54,9 +54,9 @@ extern "C" {
  *   XS_ROW_FORCE_OOR   forced id outside the vocabulary (:472-477)
  *   XS_ROW_ZERO_WEIGHT WeightedIndex saw no probability mass (:238-240)
  *   XS_ROW_NARROW      logit row narrower than the encodable bound (:196-200)
- *   XS_ROW_BAD_PARAM   top_k larger than the context's k_max, or a control list
- *                      past XS_CTL_MAX entries (no reference counterpart: the
- *                      reference has no such limits)
+ *   XS_ROW_BAD_PARAM   min(top_k, enc) larger than the context's k_max, or a
+ *                      control list past XS_CTL_MAX entries (no reference
+ *                      counterpart: the reference has no such limits)
  *   XS_ROW_INTERNAL    reserved; this build never reports it               */
 #define XS_ROW_OK 0
 #define XS_ROW_NAN 1
@@ -68,7 +68,11 @@ extern "C" {
 #define XS_ROW_BAD_PARAM 7
 #define XS_ROW_INTERNAL 8
 
-/* Largest top_k a context supports (the selection keeps top_k + 1 entries). */
+/* Largest top_k the streaming selection serves (it keeps top_k + 1 entries).
+ * A context created with k_max above it serves every top_k up to k_max --
+ * top_k >= enc included, the reference's whole-row candidate set
+ * (sampler.rs:322-338) -- through the whole-row path: every probability,
+ * a (p desc, id asc) sort of the row and the serial f32 top-p and draw. */
 #define XS_K_MAX 127
 /* Largest number of held_row log-probs per row. */
 #define XS_TOP_MAX 128
@@ -86,8 +90,10 @@ typedef struct {
 } xs_row_params;
 
 /* Sampler::new's allocation side: a context on `device` for up to `max_rows`
- * rows of up to `vocab` encodable ids (<= 1,048,576) and top_k <= k_max
- * (<= XS_K_MAX).
+ * rows of up to `vocab` encodable ids (<= 1,048,576) and min(top_k, enc) <=
+ * k_max (any k_max >= 0; the reference's top_k is an unbounded usize, and
+ * INT32_MAX serves every top_k).  k_max above XS_K_MAX adds the whole-row
+ * path's buffers, 16 bytes per row and id (32 MB for 8 rows of 248,320).
  * Allocates the device workspace once; calls allocate nothing afterwards. */
 int xs_create(int device, int64_t max_rows, int64_t vocab, int32_t k_max, xs_context** out);
 int xs_destroy(xs_context* ctx);

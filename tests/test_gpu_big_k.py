@@ -1,0 +1,116 @@
+"""top_k past the streaming selection: 128 and up, and top_k >= the vocabulary
+(candidate_set's whole-row branch, sampler.rs:322-338, xwen's only
+top-p-only mode since top_k <= 1 is greedy).  The whole-row path computes
+every probability, sorts the row by (p desc, id asc) and runs the serial f32
+top-p and WeightedIndex chains; its tokens, candidate ids and weights must
+equal the oracle's bit for bit given the device's softmax denominator, at full
+width, with masks, sparse controls and in a verify block."""
+import numpy as np
+import pytest
+
+from tests import workloads
+from tests.test_gpu_sampler import check_rows, run_sample
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+V = workloads.V
+KS = [128, 500, 1000, V, 10**6]
+
+
+@pytest.fixture(scope="module")
+def bigctx():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from xwen_amd import sampler as xsm
+    c = xsm.Context(max_rows=12, vocab=V, k_max=2**31 - 1)
+    c.bind_current_stream()
+    yield c
+    c.close()
+
+
+def _rows(seed, n):
+    rng = np.random.default_rng(seed)
+    x = rng.normal(0, 3, (n, V)).astype(np.float32)
+    for r in range(n):
+        x[r, rng.integers(0, V, 8)] = rng.uniform(8, 14, 8).astype(np.float32)
+    return x, rng
+
+
+def test_large_top_k_at_full_width(bigctx, oracle):
+    x, rng = _rows(8128, 10)
+    K = np.array([k for k in KS for _ in (0, 1)])
+    P = np.array([0.8, 1.0] * len(KS))
+    T = np.array([1.0, 0.7, 1.3, 1.0, 0.7, 1.0, 1.0, 0.6, 1.0, 1.0])
+    U = workloads.uniforms(rng, 10)
+    d = run_sample(bigctx, x, T, K, P, U, cand_k=V)
+    assert (d["status"] == 0).all(), d["status"]
+    assert list(d["n_cand"]) == [min(k, V) for k in K]
+    thin = check_rows(oracle, x, T, K, P, U, d, label="big-k")
+    print(f"big-k: {thin} of 10 rows below the decision margin")
+
+
+def test_top_p_only_under_masks_and_controls(bigctx, oracle):
+    """Grammar-masked rows with top_k >= V (the masked ids carry p = 0 and sit
+    at the end of the candidate list in id order), a one-id mask, and bans,
+    biases and a pull on a whole-row draw."""
+    from xwen_amd import sampler as xsm
+    x, rng = _rows(9128, 6)
+    allow = np.zeros((6, V), bool)
+    allow[0, 1000:3500] = True                    # ~1 %, one range
+    allow[1] = rng.random(V) < 0.10
+    allow[2] = rng.random(V) < 0.50
+    allow[3, 77_777] = True                       # exactly one id: forced
+    allow[4] = rng.random(V) < 0.30
+    allow[5] = True
+    mask = workloads.pack_mask(allow)
+    K = np.array([10**6, V, 10**6, 10**6, 700, 10**6])
+    P = np.array([0.95, 1.0, 0.8, 0.95, 0.9, 1.0])
+    T = np.array([1.0, 1.0, 0.7, 1.0, 1.0, 1.3])
+    U = workloads.uniforms(rng, 6)
+    d = run_sample(bigctx, x, T, K, P, U, mask=mask, cand_k=V)
+    assert (d["status"] == 0).all(), d["status"]
+    assert d["token"][3] == 77_777
+    check_rows(oracle, x, T, K, P, U, d, mask=mask, label="big-k masked")
+    ctls = [None] * 6
+    ctls[0] = xsm.SampleControl(banned=tuple(int(i) for i in np.argsort(-x[0])[:5]))
+    ctls[2] = xsm.SampleControl(bias=((11, 6.0), (12, -3.0), (11, 1.5)))
+    ctls[5] = xsm.SampleControl(pull=(4242, 0.7), banned=(5, 6, 7))
+    d = run_sample(bigctx, x, T, K, P, U, cand_k=V, ctls=ctls)
+    assert (d["status"] == 0).all(), d["status"]
+    check_rows(oracle, x, T, K, P, U, d, ctls=ctls, label="big-k controlled")
+
+
+def test_large_top_k_in_a_verify_block(bigctx, oracle):
+    """xs_verify rows with top_k 500 and top_k >= V walk as accept_drafts."""
+    from xwen_amd import sampler as xsm
+    seqs, span = 3, 4
+    x, rng = _rows(10128, seqs * span)
+    K = np.array([500, 10**6, 300] * span).reshape(span, seqs).T.reshape(-1)
+    T = np.full(seqs * span, 1.0)
+    P = np.full(seqs * span, 0.95)
+    U = workloads.uniforms(rng, seqs * span)
+    # the draws row by row through the oracle, then the drafts: two matches
+    # then a mismatch in sequence 0, all matches in 1, a mismatch at once in 2
+    tok = []
+    for r in range(seqs * span):
+        d = run_sample(bigctx, x[r:r + 1], T[r], K[r], P[r], U[r:r + 1], cand_k=0)
+        tok.append(int(d["token"][0]))
+    tok = np.array(tok).reshape(seqs, span)
+    drafts = tok[:, :span - 1].copy()
+    drafts[0, 2] = (drafts[0, 2] + 1) % V
+    drafts[2, 0] = (drafts[2, 0] + 1) % V
+    lg = torch.as_tensor(x).cuda()
+    p = xsm.params_tensor(T, K, P, seqs * span, "cuda")
+    u = torch.as_tensor(U).cuda()
+    out = xsm.verify_batch(bigctx, lg, seqs, span, p, u,
+                           torch.as_tensor(drafts.astype(np.int32)).cuda())
+    torch.cuda.synchronize()
+    assert (out.row_token.cpu().numpy().reshape(seqs, span) == tok).all()
+    assert out.accepted.cpu().tolist() == [2, 3, 0]
+    assert out.n_committed.cpu().tolist() == [3, 4, 1]
+    for r in range(seqs * span):
+        o = oracle.sample_controlled(x[r], V, float(T[r]), int(K[r]), float(P[r]), u=float(U[r]),
+                                     sum_mode=oracle.SUM_SEQ_F32, margins=True)
+        if min(o.margin_order, o.margin_cut, o.margin_draw) > 1e-5:
+            assert o.token == tok.reshape(-1)[r], r

@@ -286,8 +286,10 @@ struct Cfg {
   float inv;     // (float)(1/T)  (softmax_in_place, sampler.rs:291)
   float top_p;
   int k;         // candidates drawn from (0 on greedy rows)
-  int kp;        // selection size K'
+  int kp;        // selection size K' the streaming pass keeps per chunk
   bool greedy, scale, full, bad;
+  bool big;      // more candidates than the streaming selection holds: the
+                 // whole-row path (big_finalize) draws the row
 };
 
 XS_DEV Cfg make_cfg(const xs_row_params& p, int64_t enc, int n_top, int k_max) {
@@ -309,8 +311,13 @@ XS_DEV Cfg make_cfg(const xs_row_params& p, int64_t enc, int n_top, int k_max) {
     c.kp = p.top_k + 1;
     c.full = false;
   }
+  // K' past KSEL (top_k >= 128, or a whole row wider than KSEL): the streaming
+  // pass keeps only what the argmax and held_row need, and big_finalize sorts
+  // the whole row
+  c.big = !c.greedy && (c.kp > KSEL || (c.full && enc > KSEL));
+  if (c.big) c.kp = 1;
   if (n_top > 0) c.kp = max(c.kp, (int)min((int64_t)n_top, enc));
-  c.bad = c.kp > KSEL || (c.full && enc > KSEL) || (!c.greedy && c.k > k_max);
+  c.bad = !c.greedy && c.k > k_max;
   return c;
 }
 
@@ -321,7 +328,7 @@ XS_DEV Cfg greedy_cfg() {
   c.k = 0;
   c.kp = 1;
   c.greedy = true;
-  c.scale = c.full = c.bad = false;
+  c.scale = c.full = c.bad = c.big = false;
   return c;
 }
 
@@ -398,6 +405,8 @@ struct Args {
   int32_t* seq_ticket;  // [seqs * TSTRIDE] rows of the sequence that are finalized (0 between calls)
   int32_t n_chunks, nslots;
   int32_t k_max;     // the context's largest top_k (of min(top_k, enc)); larger is XS_ROW_BAD_PARAM
+  uint64_t* big;     // [rows, 2, big_ld]: big_finalize's sort buffers (contexts with k_max > XS_K_MAX)
+  int64_t big_ld;
   uint64_t* rec;     // [rows, SRECW, nsp]: word i of sub-record s of a row at i * nsp + s
 };
 
@@ -617,6 +626,12 @@ struct HeldLds {
   int32_t n_have;                   // top-n entries below
   float vals[XS_TOP_MAX];           // top-n logits, (logit desc, id asc)
 };
+// What the finalizing wave leaves for big_finalize.
+struct BigStash {
+  float m_s, S;                     // scaled max and softmax denominator of the row
+  int32_t defer;                    // the row is drawn by big_finalize
+  int32_t pad;
+};
 struct FinLds {
   uint64_t list[SURV];              // gathered survivors
   uint64_t srt[SURV];               // survivors in (logit desc, id asc) order
@@ -624,6 +639,13 @@ struct FinLds {
   double expt[64];                  // kExpT, flattened
   uint32_t keys[GMAX * 64 * 4];     // published bound keys (more than 64 sub-records)
   HeldLds held;
+  BigStash big;
+};
+// big_finalize's workspace: the exp table and the radix sort's counters.
+struct BigLds {
+  double expt[64];
+  uint32_t cnt[16][BLOCK];          // per digit, per thread: count, then write position
+  int32_t s4[NWAVE];
 };
 // The chunk pass stages each wave's entries here before it publishes them;
 // after the hand-off only the row's last workgroup uses the memory again, as
@@ -631,6 +653,7 @@ struct FinLds {
 union TailLds {
   uint64_t stage[NWAVE][CAPW];
   FinLds fin;
+  BigLds big;
 };
 // p = rn(e / S) of one controlled logit v (the reference's softmax_in_place:
 // v *= inv unless T == 1, then exp(v - max), then / sum; sampler.rs:289-310).
@@ -1520,7 +1543,7 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
   const float vL = nsel > 0 ? keyf(pk_key(last_sel)) : -INFINITY;
   float pbelow = 0.0f;
   bool lazy_order = false;  // the (p desc, id asc) repair left to the draw
-  if (stoch && st == XS_ROW_OK) {
+  if (stoch && st == XS_ROW_OK && !cfg.big) {
     const bool need_below = !cfg.full && vL != -INFINITY;
 #pragma unroll
     for (int r = 0; r < 2; r++) {
@@ -1811,7 +1834,10 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
   w[0] = __uint_as_float((uint32_t)(pk[0] >> 32));
   w[1] = __uint_as_float((uint32_t)(pk[1] >> 32));
   int tok = -1;
-  if (st == XS_ROW_OK) {
+  // a row with more candidates than the selection holds is drawn by the
+  // whole workgroup afterwards (big_finalize); here only its statistics
+  const bool defer = cfg.big && stoch && st == XS_ROW_OK;
+  if (st == XS_ROW_OK && !defer) {
     if (!stoch) {
       tok = (int)rdl(pk_id(sel[0]), 0);
     } else {
@@ -1940,17 +1966,22 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
 
   // Outputs.
   if (lane == 0) {
-    st_agent(&a.token[row], st == XS_ROW_OK ? tok : -1);
-    st_agent(&a.status[row], st);
-    if (a.n_cand) a.n_cand[row] = (stoch && st == XS_ROW_OK) ? k : 0;
+    if (!defer) {
+      st_agent(&a.token[row], st == XS_ROW_OK ? tok : -1);
+      st_agent(&a.status[row], st);
+      if (a.n_cand) a.n_cand[row] = (stoch && st == XS_ROW_OK) ? k : 0;
+    }
     if (a.soft_max) a.soft_max[row] = m_s;
     if (a.soft_sum) a.soft_sum[row] = S;
     if (WANT_LSE) {
       if (a.row_max) a.row_max[row] = m_v;
       if (a.p_max) a.p_max[row] = lse_ok ? (float)(1.0 / R_d) : __builtin_nanf("");
     }
+    F.big.defer = defer ? 1 : 0;
+    F.big.m_s = m_s;
+    F.big.S = S;
   }
-  if (want_cands && stoch && st == XS_ROW_OK) {
+  if (want_cands && stoch && st == XS_ROW_OK && !defer) {
     const int kw = (int)min((int64_t)k, a.cand_ld);  // a short cand_ld truncates the list
 #pragma unroll
     for (int r = 0; r < 2; r++) {
@@ -1992,46 +2023,279 @@ XS_DEV void finalize_row(const Args& a, const Cfg& cfg, int row, const uint64_t*
   for (int j = 0; j < EPRE; j++) E[j] = live ? ld_agent(&rowrec[(SHDR + j) * nsp + lane]) : 0ull;
   CtlRow cr{};
   if (HAS_CTL) cr = a.ctl_row[row];
-  const bool done = !(HAS_CTL && cr.active) && nsub <= 64 && cfg.kp <= 64 && !cfg.bad &&
+  const bool done = !(HAS_CTL && cr.active) && nsub <= 64 && cfg.kp <= 64 && !cfg.bad && !cfg.big &&
                     fin_fast<HAS_MASK, WANT_LSE>(a, cfg, row, nsub, h, E, rowrec, nsp, rowp, F);
   if (!done) fin_general<HAS_MASK, WANT_LSE, HAS_CTL>(a, cfg, row, rowrec, nsp, nsub, rowp, mrow, cr, h, E, F);
 
-  if (a.span > 0) {
-    drain();  // this row's token and status are acknowledged
-    const int seq = row / a.span;
-    int t = 0;
-    if (lane == 0) t = __hip_atomic_fetch_add(&a.seq_ticket[seq * TSTRIDE], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    t = __builtin_amdgcn_readfirstlane(t);
-    if (t == a.span - 1 && lane == 0) {
-      st_agent(&a.seq_ticket[seq * TSTRIDE], 0);
-      // accept_drafts (generate.rs:4020-4046) over the sequence's rows
-      const int span = a.span, D = span - 1;
-      const int64_t r0 = (int64_t)seq * span;
-      const int bud = a.budget ? a.budget[seq] : 0x7FFFFFFF;
-      int mcount = 0, ncom = 0, sst = XS_ROW_OK;
-      for (int i = 0; i < span; i++) {
-        if (ncom >= bud) break;
-        const int rs = ld_agent(&a.status[r0 + i]);
-        if (rs != XS_ROW_OK) {
-          sst = rs;
+}
+
+// The speculative walk: a finalized row of a verify block takes its sequence's
+// ticket, and the sequence's last finalized row walks accept_drafts
+// (generate.rs:4020-4046) over the sequence's rows.  One wave, after the row's
+// token and status are written.
+XS_DEV void verify_walk(const Args& a, int row) {
+  const int lane = lane_id();
+  drain();  // this row's token and status are acknowledged
+  const int seq = row / a.span;
+  int t = 0;
+  if (lane == 0) t = __hip_atomic_fetch_add(&a.seq_ticket[seq * TSTRIDE], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  t = __builtin_amdgcn_readfirstlane(t);
+  if (t == a.span - 1 && lane == 0) {
+    st_agent(&a.seq_ticket[seq * TSTRIDE], 0);
+    const int span = a.span, D = span - 1;
+    const int64_t r0 = (int64_t)seq * span;
+    const int bud = a.budget ? a.budget[seq] : 0x7FFFFFFF;
+    int mcount = 0, ncom = 0, sst = XS_ROW_OK;
+    for (int i = 0; i < span; i++) {
+      if (ncom >= bud) break;
+      const int rs = ld_agent(&a.status[r0 + i]);
+      if (rs != XS_ROW_OK) {
+        sst = rs;
+        break;
+      }
+      const int s = ld_agent(&a.token[r0 + i]);
+      const bool matched = i < D && s == a.drafts[(int64_t)seq * D + i];
+      a.committed[(int64_t)seq * span + ncom] = s;
+      ncom++;
+      if (matched) mcount++;
+      bool eog = false;
+      for (int e = 0; e < a.n_eog; e++) eog |= (s == a.eog[e]);
+      // a draft that completes the grammar ends the walk like an EOG
+      // (generate.rs:2452-2459): the caller computed it along the drafts
+      if (matched && a.done_after && a.done_after[r0 + i]) eog = true;
+      if (!matched || eog) break;
+    }
+    for (int i = ncom; i < span; i++) a.committed[(int64_t)seq * span + i] = -1;
+    a.accepted[seq] = mcount;
+    a.n_committed[seq] = ncom;
+    a.seq_status[seq] = sst;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// The whole-row path: rows whose candidate set is larger than the streaming
+// selection holds -- top_k of 128 or more, and top_k >= enc, the reference's
+// candidate_set branch that sorts the whole row (sampler.rs:322-338), which is
+// xwen's only top-p-only mode because top_k <= 1 means greedy.  The row's last
+// workgroup, all four waves, after its first wave found the row's max and
+// softmax denominator:
+//   1. p = rn(exp(s - max) / S) of every id, the same correctly rounded f32
+//      arithmetic as the selection path, into the row's sort buffer as
+//      (p bits << 32 | id), in id order;
+//   2. a stable LSD radix sort by p descending (4-bit digits, eight passes,
+//      per-thread contiguous segments), so equal p keep ascending ids: the
+//      (p desc, id asc) order of top_k_desc and of the stable whole-row sort;
+//   3. the first min(top_k, enc) entries are the candidates; truncate_top_p
+//      (sampler.rs:401-429) and WeightedIndex (:235-243, rand 0.9) run as the
+//      reference's serial f32 chains, by one wave, every lane adding the same
+//      weights in order.
+
+// Stable LSD radix sort of n u64 entries by their high 32 bits, descending;
+// src holds the result afterwards (an even number of passes).  All waves.
+XS_DEV void radix_sort_desc(uint64_t* src, uint64_t* dst, int n, BigLds& B) {
+  const int t = threadIdx.x;
+  const int L = (n + BLOCK - 1) / BLOCK;
+  const int i0 = min(n, t * L), i1 = min(n, i0 + L);
+#pragma unroll 1
+  for (int pass = 0; pass < 8; pass++) {
+    const int sh = 4 * pass;
+#pragma unroll
+    for (int d = 0; d < 16; d++) B.cnt[d][t] = 0u;
+#pragma unroll 4
+    for (int i = i0; i < i1; i++) B.cnt[((~(uint32_t)(src[i] >> 32)) >> sh) & 15u][t]++;
+    __syncthreads();
+    // exclusive scan in (digit, thread) order: thread t owns flat entries 16t..16t+15
+    uint32_t* flat = &B.cnt[0][0];
+    uint32_t loc[16], sum = 0;
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+      loc[j] = flat[16 * t + j];
+      sum += loc[j];
+    }
+    int total;
+    uint32_t run = (uint32_t)block_excl_scan((int)sum, B.s4, &total);
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+      flat[16 * t + j] = run;
+      run += loc[j];
+    }
+    __syncthreads();
+#pragma unroll 4
+    for (int i = i0; i < i1; i++) {
+      const uint64_t e = src[i];
+      const uint32_t d = ((~(uint32_t)(e >> 32)) >> sh) & 15u;
+      dst[B.cnt[d][t]++] = e;
+    }
+    __syncthreads();
+    uint64_t* const tmp = src;
+    src = dst;
+    dst = tmp;
+  }
+}
+
+template <bool HAS_MASK, bool HAS_CTL>
+XS_DEV void big_finalize(const Args& a, const Cfg& cfg, int row, const float* rowp, const uint32_t* mrow,
+                         TailLds& Tl) {
+  __syncthreads();                 // the first wave has finalized the row and left its stash
+  const BigStash bs = Tl.fin.big;  // read before the workgroup reuses the memory
+  __syncthreads();
+  if (!bs.defer) return;
+  BigLds& B = Tl.big;
+  const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
+  const int enc = (int)a.enc;
+  uint64_t* const A = a.big + (int64_t)row * 2 * a.big_ld;
+  uint64_t* const A2 = A + a.big_ld;
+  if (tid < 64) B.expt[tid] = (&kExpT[0][0])[tid];
+  CtlRow cr{};
+  const uint64_t* pl = nullptr;
+  if (HAS_CTL) {
+    cr = a.ctl_row[row];
+    pl = a.patch + (int64_t)row * CTL_MAX;
+  }
+  const bool ctl_on = HAS_CTL && cr.active;
+  __syncthreads();
+
+  // 1. p of every id, in id order; one slot (BLOCK float4s) per round, the
+  // controls applied as the streaming pass applies them
+  int pc = 0;
+#pragma unroll 1
+  for (int f0 = 0; 4 * f0 < enc; f0 += BLOCK) {
+    const int f = f0 + tid;
+    const int sb = 4 * f0;
+    float4 q = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+    if (4 * f < enc) q = reinterpret_cast<const float4*>(rowp)[f];
+    float x[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const int id = 4 * f + e;
+      if (HAS_MASK && id < enc && !((mrow[id >> 5] >> (id & 31)) & 1u)) x[e] = -INFINITY;
+    }
+    if (ctl_on) {
+      if (cr.force_id >= 0) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) x[e] = (4 * f + e == cr.force_id) ? cr.force_val : -INFINITY;
+      } else {
+        while (pc < cr.n_patch) {
+          const uint64_t pe = pl[pc];
+          const int off = (int)(uint32_t)(pe >> 32) - sb;
+          if (off >= SLOT) break;
+          if ((off >> 2) == tid) {
+            const float pv = __uint_as_float((uint32_t)pe);
+#pragma unroll
+            for (int e = 0; e < 4; e++) x[e] = ((off & 3) == e) ? pv : x[e];
+          }
+          pc++;
+        }
+        const int pt = cr.pull_id - sb;
+        if (pt >= 0 && pt < SLOT && (pt >> 2) == tid) {
+#pragma unroll
+          for (int e = 0; e < 4; e++) x[e] = ((pt & 3) == e) ? cr.pull_val : x[e];
+        }
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const int id = 4 * f + e;
+      if (id < enc) {
+        const float pe = exact_p(x[e], cfg, bs.m_s, bs.S, B.expt);
+        A[id] = ((uint64_t)__float_as_uint(pe + 0.0f) << 32) | (uint32_t)id;
+      }
+    }
+  }
+  __syncthreads();
+
+  // 2. (p desc, id asc)
+  radix_sort_desc(A, A2, enc, B);
+  if (wave != 0) return;
+
+  // 3. the candidates A[0..kk): truncate_top_p and the draw, serial f32
+  const int kk = min(cfg.k, enc);
+  const bool renorm = !(cfg.top_p >= 1.0f);
+  float* const cum = reinterpret_cast<float*>(A2);  // serial prefixes, the sort's spare buffer
+  auto wt = [&](int i) __attribute__((always_inline)) -> float {
+    const float w = __uint_as_float((uint32_t)(A[min(i, kk - 1)] >> 32));  // (clamped: never past the row)
+    return i < kk ? w : 0.0f;
+  };
+  int st = XS_ROW_OK;
+  float sum = 1.0f;
+  int keep = kk;
+  if (renorm) {
+    // sum of every candidate weight, folded from -0.0 as Rust's f32 Sum does
+    float acc = -0.0f;
+#pragma unroll 1
+    for (int b0 = 0; b0 < kk; b0 += 64) {
+      const float w = wt(b0 + lane);
+#pragma unroll 16
+      for (int u = 0; u < 64; u++) acc = acc + rdlf(w, u);
+    }
+    sum = acc;
+    if (!(sum > 0.0f)) st = XS_ROW_ZERO_WEIGHT;  // weights left unchanged: no mass to draw
+  }
+  if (st == XS_ROW_OK) {
+    // renormalised weights (or the raw ones at top_p >= 1), their serial
+    // prefix from 0 (truncate_top_p's cumsum, the same sums as WeightedIndex's
+    // cumulative weights) until the cut
+    float acc = 0.0f;
+    bool cut = false;
+#pragma unroll 1
+    for (int b0 = 0; b0 < kk && !cut; b0 += 64) {
+      const int i = b0 + lane;
+      float w = wt(i);
+      if (renorm) w = __fdiv_rn(w, sum);
+      float mine = 0.0f;
+#pragma unroll 16
+      for (int u = 0; u < 64; u++) {
+        acc = acc + rdlf(w, u);
+        mine = (lane == u) ? acc : mine;
+      }
+      if (i < kk) cum[i] = mine;
+      if (renorm) {
+        const uint64_t bm = __ballot(i < kk && mine >= cfg.top_p);
+        if (bm) {
+          keep = b0 + (int)__builtin_ctzll(bm) + 1;
+          cut = true;
+        }
+      }
+    }
+    wave_lds_sync();  // (cum is read back by other lanes below)
+    __builtin_amdgcn_s_waitcnt(0);
+    const float tot = cum[keep - 1];
+    if (!(tot > 0.0f)) {
+      st = XS_ROW_ZERO_WEIGHT;
+    } else {
+      const float u_row = a.uniforms[row];
+      const float x_draw = u_row * tot + 0.0f;
+      // the index: the cumulative weights (prefix through i, i < kk - 1; the
+      // total from keep - 1 on) at or below x
+      int idx = keep - 1;
+#pragma unroll 1
+      for (int b0 = 0; b0 < keep - 1; b0 += 64) {
+        const int i = b0 + lane;
+        const float c = cum[min(i, keep - 1)];
+        const uint64_t bm = __ballot(i < keep - 1 && c > x_draw);
+        if (bm) {
+          idx = b0 + (int)__builtin_ctzll(bm);
           break;
         }
-        const int s = ld_agent(&a.token[r0 + i]);
-        const bool matched = i < D && s == a.drafts[(int64_t)seq * D + i];
-        a.committed[(int64_t)seq * span + ncom] = s;
-        ncom++;
-        if (matched) mcount++;
-        bool eog = false;
-        for (int e = 0; e < a.n_eog; e++) eog |= (s == a.eog[e]);
-        // a draft that completes the grammar ends the walk like an EOG
-        // (generate.rs:2452-2459): the caller computed it along the drafts
-        if (matched && a.done_after && a.done_after[r0 + i]) eog = true;
-        if (!matched || eog) break;
       }
-      for (int i = ncom; i < span; i++) a.committed[(int64_t)seq * span + i] = -1;
-      a.accepted[seq] = mcount;
-      a.n_committed[seq] = ncom;
-      a.seq_status[seq] = sst;
+      const int tok = (int)(uint32_t)A[idx];
+      if (lane == 0) st_agent(&a.token[row], tok);
+    }
+  }
+  if (lane == 0) {
+    if (st != XS_ROW_OK) st_agent(&a.token[row], -1);
+    st_agent(&a.status[row], st);
+    if (a.n_cand) a.n_cand[row] = st == XS_ROW_OK ? kk : 0;
+  }
+  if (st == XS_ROW_OK && (a.cand_id || a.cand_w)) {
+    const int kw = (int)min((int64_t)kk, a.cand_ld);
+#pragma unroll 1
+    for (int i = lane; i < kw; i += 64) {
+      const uint64_t e = A[i];
+      float w = __uint_as_float((uint32_t)(e >> 32));
+      if (renorm) w = i < keep ? __fdiv_rn(w, sum) : 0.0f;
+      if (a.cand_id) a.cand_id[(int64_t)row * a.cand_ld + i] = (int32_t)(uint32_t)e;
+      if (a.cand_w) a.cand_w[(int64_t)row * a.cand_ld + i] = w;
     }
   }
 }
@@ -2501,11 +2765,18 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
   }
   __syncthreads();
   if (!Lc.last) return;
-  // held_row outputs: after the row is finalized, its finalizing wave folds
-  // the denominator as the reference does (held_fold)
-  if (wave != 0) return;
-  finalize_row<HAS_MASK, WANT_LSE, HAS_CTL>(a, cfg, row, rowrec, nsp, nc * NWAVE, rowp, mrow, Tl.fin);
-  if (held) held_fold<1>(a, row, rowp, rowrec, nsp, nc * NWAVE, Tl.fin);
+  // The first wave finalizes the row; held_row outputs then get the reference's
+  // serial fold (held_fold); a row with more candidates than the selection
+  // holds is drawn by the whole workgroup (big_finalize); a verify block's
+  // rows then walk accept_drafts (verify_walk).
+  const bool big_row = cfg.big && !cfg.bad;  // uniform in the workgroup
+  if (wave != 0 && !big_row) return;
+  if (wave == 0) {
+    finalize_row<HAS_MASK, WANT_LSE, HAS_CTL>(a, cfg, row, rowrec, nsp, nc * NWAVE, rowp, mrow, Tl.fin);
+    if (held) held_fold<1>(a, row, rowp, rowrec, nsp, nc * NWAVE, Tl.fin);
+  }
+  if (big_row) big_finalize<HAS_MASK, HAS_CTL>(a, cfg, row, rowp, mrow, Tl);
+  if (wave == 0 && a.span > 0) verify_walk(a, row);
 }
 
 // ---------------------------------------------------------------------------
@@ -2743,6 +3014,7 @@ struct xs_context {
   int32_t* ctl_chunk;   // [max_rows, max_chunks + 1]
   int32_t* row_ticket;  // [max_rows * TSTRIDE] arrival tickets, zero between calls
   int32_t* seq_ticket;  // [max_rows * TSTRIDE]
+  uint64_t* big;        // [max_rows, 2, vocab] whole-row sort buffers (k_max > XS_K_MAX), or null
 };
 
 namespace {
@@ -2807,6 +3079,8 @@ int launch(xs_context* ctx, xs::Args& a, int64_t rows, int span, bool mask, bool
   a.row_ticket = ctx->row_ticket;
   a.seq_ticket = ctx->seq_ticket;
   a.k_max = ctx->k_max;
+  a.big = ctx->big;
+  a.big_ld = ctx->vocab;
   const dim3 g1((unsigned)grid);
   if (ctl && mask) launch2<true, false, true>(ctx, a, rows, g1, order);
   else if (ctl) launch2<false, false, true>(ctx, a, rows, g1, order);
@@ -2823,7 +3097,7 @@ extern "C" {
 const char* xs_version(void) { return "xsamp 0.1 gfx950"; }
 
 int xs_create(int device, int64_t max_rows, int64_t vocab, int32_t k_max, xs_context** out) {
-  if (!out || max_rows < 1 || vocab < 1 || k_max < 0 || k_max > XS_K_MAX) return XS_ERR_ARG;
+  if (!out || max_rows < 1 || vocab < 1 || k_max < 0) return XS_ERR_ARG;
   *out = nullptr;
   if (hipSetDevice(device) != hipSuccess) return XS_ERR_HIP;
   const int32_t mc = chunks_for(vocab);
@@ -2849,6 +3123,8 @@ int xs_create(int device, int64_t max_rows, int64_t vocab, int32_t k_max, xs_con
   ok = ok && hipMalloc((void**)&c->seq_ticket, tbytes) == hipSuccess;
   ok = ok && hipMemset(c->row_ticket, 0, tbytes) == hipSuccess;
   ok = ok && hipMemset(c->seq_ticket, 0, tbytes) == hipSuccess;
+  if (k_max > XS_K_MAX)  // top_k past the streaming selection: the whole-row path's buffers
+    ok = ok && hipMalloc((void**)&c->big, (size_t)max_rows * 2 * vocab * sizeof(uint64_t)) == hipSuccess;
   ok = ok && hipDeviceSynchronize() == hipSuccess;
   if (!ok) {
     xs_destroy(c);
@@ -2869,6 +3145,7 @@ int xs_destroy(xs_context* c) {
   (void)hipFree(c->ctl_chunk);
   (void)hipFree(c->row_ticket);
   (void)hipFree(c->seq_ticket);
+  if (c->big) (void)hipFree(c->big);
   free(c);
   return XS_OK;
 }

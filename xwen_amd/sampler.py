@@ -46,8 +46,8 @@ ROW_STATUS_NAMES = {
     _lib.ROW_FORCE_OOR: "forced token id is outside the vocabulary",
     _lib.ROW_ZERO_WEIGHT: "no candidate carries any probability mass after top-k/top-p filtering",
     _lib.ROW_NARROW: "logit row is narrower than the encodable ids the sampler draws over",
-    _lib.ROW_BAD_PARAM: "top_k exceeds the sampler context's k_max, or a control list "
-                        "holds more than XS_CTL_MAX entries",
+    _lib.ROW_BAD_PARAM: "top_k exceeds the sampler context's k_max (create the context with a "
+                        "larger k_max), or a control list holds more than XS_CTL_MAX entries",
     _lib.ROW_INTERNAL: "internal error (reserved)",
 }
 
@@ -435,7 +435,10 @@ class Sampler:
         self.eog = list(eog_tokens)
         self.encodable_ = encodable
         self.rng = np.random.default_rng(opts.seed)
-        self.ctx = Context(max_rows, encodable, device=device)
+        # a top_k past the streaming selection (or the whole row) needs the
+        # context's whole-row buffers, which only a larger k_max allocates
+        k_max = _lib.K_MAX if opts.top_k <= _lib.K_MAX else min(int(opts.top_k), encodable)
+        self.ctx = Context(max_rows, encodable, k_max=max(k_max, _lib.K_MAX), device=device)
         self.device = f"cuda:{device}"
 
     def encodable(self) -> int:

@@ -15,7 +15,9 @@ from dataclasses import dataclass
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "_build", "libxs_oracle.so")
+# XS_ORACLE_LIB names another build of the same library (the sanitized one of
+# `make -C oracle asan`, for tests/test_sanitized.py)
+LIB_PATH = os.environ.get("XS_ORACLE_LIB") or os.path.join(HERE, "_build", "libxs_oracle.so")
 
 OK, NAN, NO_FINITE, MASK_SHORT, FORCE_OOR, ZERO_WEIGHT, NARROW = range(7)
 SUM_SEQ_F32, SUM_F64, SUM_GIVEN = 0, 1, 2

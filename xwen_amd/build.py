@@ -6,6 +6,7 @@ import subprocess
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 SRC = os.path.join(HERE, "csrc", "xs_sampler.hip")
+HOST_SRC = os.path.join(HERE, "csrc", "xs_host.cpp")  # host-only C ABI (also built alone for ASan)
 OUT = os.path.join(HERE, "libxsamp.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
@@ -22,7 +23,7 @@ FLAGS = [
 
 def build(verbose: bool = False) -> str:
     tmp = OUT + ".tmp"
-    cmd = [HIPCC, *FLAGS, SRC, "-o", tmp]
+    cmd = [HIPCC, *FLAGS, SRC, HOST_SRC, "-o", tmp]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed ({r.returncode}):\n{r.stderr[-4000:]}")

@@ -60,6 +60,7 @@
 
 #include "../../include/xsamp.h"
 #include "xs_exp_table.h"
+#include "xs_host.h"
 
 #define XS_DEV __device__ __forceinline__
 
@@ -3019,34 +3020,11 @@ struct xs_context {
 
 namespace {
 
-int64_t slots_for(int64_t enc) { return (enc + xs::SLOT - 1) / xs::SLOT; }
-int32_t chunks_for(int64_t enc) {
-  const int64_t ns = slots_for(enc);
-  return (int32_t)((ns + xs::SPC - 1) / xs::SPC);
-}
+using xs_host::chunks_for;
+using xs_host::slots_for;
+static_assert(xs_host::SLOT == xs::SLOT && xs_host::SPC == xs::SPC, "the host checks' chunk geometry");
 
-bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
-
-struct Call {
-  const float* logits;
-  int64_t rows, ld, width, enc;
-  const xs_row_params* params;
-  const float* uniforms;
-  const uint32_t* allowed;
-  int64_t allowed_words, allowed_ld;
-};
-
-int check_common(xs_context* ctx, const Call& c) {
-  if (!ctx || !c.logits || !c.params || !c.uniforms) return XS_ERR_ARG;
-  if (c.rows < 0 || c.enc < 1 || c.ld < 1) return XS_ERR_ARG;
-  if (c.rows > ctx->max_rows || c.enc > ctx->vocab) return XS_ERR_CAPACITY;
-  if (c.ld % 4 != 0 || !aligned16(c.logits)) return XS_ERR_ARG;
-  if (c.width > c.ld) return XS_ERR_ARG;
-  if (c.enc > c.ld && c.width >= c.enc) return XS_ERR_ARG;
-  if (c.allowed && (c.allowed_ld < c.allowed_words || c.allowed_words < 0)) return XS_ERR_ARG;
-  if (chunks_for(c.enc) > ctx->max_chunks) return XS_ERR_CAPACITY;
-  return XS_OK;
-}
+xs_host_limits limits_of(const xs_context* ctx) { return xs_host_limits{ctx->max_rows, ctx->vocab, ctx->max_chunks}; }
 
 // One sample_kernel launch over rows x n_chunks workgroups (it finalizes the
 // rows itself); a call with sparse controls runs control_kernel (one
@@ -3164,25 +3142,11 @@ int xs_sample(xs_context* ctx, const xs_sample_args* in) { return sample_impl(ct
 
 namespace {
 int sample_impl(xs_context* ctx, const xs_sample_args* in, bool clear_tickets) {
-  if (!ctx || !in || !in->token || !in->status) return XS_ERR_ARG;
-  const Call c{in->logits, in->rows, in->ld, in->width, in->enc, in->params, in->uniforms,
-               in->allowed, in->allowed_words, in->allowed_ld};
-  int rc = check_common(ctx, c);
+  if (!ctx) return XS_ERR_ARG;
+  const xs_host_limits lim = limits_of(ctx);
+  const int rc = xs_host_check_sample(&lim, in);
   if (rc) return rc;
-  if ((in->cand_id || in->cand_w) && in->cand_ld < 1) return XS_ERR_ARG;
-  if (in->n_top < 0 || in->n_top > XS_TOP_MAX) return XS_ERR_ARG;
-  if ((in->top_id || in->top_logprob) && in->top_ld < in->n_top) return XS_ERR_ARG;
   const bool lse = in->row_max || in->row_lse || in->top_id || in->top_logprob;
-  if (lse && (in->allowed || in->controls)) return XS_ERR_ARG;
-  if (in->row_order) {  // a permutation of 0..rows-1
-    if (in->rows > XS_ORDER_MAX) return XS_ERR_ARG;
-    uint64_t seen[XS_ORDER_MAX / 64] = {};
-    for (int64_t i = 0; i < in->rows; i++) {
-      const int32_t r = in->row_order[i];
-      if (r < 0 || r >= in->rows || ((seen[r >> 6] >> (r & 63)) & 1u)) return XS_ERR_ARG;
-      seen[r >> 6] |= 1ull << (r & 63);
-    }
-  }
   if (hipSetDevice(ctx->device) != hipSuccess) return XS_ERR_HIP;
   int32_t data_err = XS_ROW_OK;
   if (in->width < in->enc) data_err = XS_ROW_NARROW;
@@ -3278,16 +3242,11 @@ int xs_sample_noalloc(const xs_sample_args* in, void* hip_stream) {
 }
 
 int xs_verify(xs_context* ctx, const xs_verify_args* in) {
-  if (!ctx || !in || !in->row_token || !in->row_status || !in->accepted || !in->committed ||
-      !in->n_committed || !in->seq_status)
-    return XS_ERR_ARG;
-  if (in->seqs < 0 || in->span < 1 || in->n_eog < 0 || in->n_eog > 8) return XS_ERR_ARG;
-  if (in->span > 1 && !in->drafts) return XS_ERR_ARG;
-  const int64_t rows = in->seqs * in->span;
-  const Call c{in->logits, rows, in->ld, in->width, in->enc, in->params, in->uniforms,
-               in->allowed, in->allowed_words, in->allowed_ld};
-  int rc = check_common(ctx, c);
+  if (!ctx) return XS_ERR_ARG;
+  const xs_host_limits lim = limits_of(ctx);
+  const int rc = xs_host_check_verify(&lim, in);
   if (rc) return rc;
+  const int64_t rows = in->seqs * in->span;
   if (hipSetDevice(ctx->device) != hipSuccess) return XS_ERR_HIP;
   int32_t data_err = XS_ROW_OK;
   if (in->width < in->enc) data_err = XS_ROW_NARROW;
@@ -3329,11 +3288,10 @@ int xs_verify(xs_context* ctx, const xs_verify_args* in) {
 }
 
 int xs_argmax_probs(xs_context* ctx, const xs_argmax_args* in) {
-  if (!ctx || !in || !in->logits || !in->ids || !in->probs) return XS_ERR_ARG;
-  if (in->rows < 0 || in->width < 1 || in->ld < in->width) return XS_ERR_ARG;
-  if (in->rows > ctx->max_rows || in->width > ctx->vocab) return XS_ERR_CAPACITY;
-  if (in->ld % 4 != 0 || !aligned16(in->logits)) return XS_ERR_ARG;
-  if (chunks_for(in->width) > ctx->max_chunks) return XS_ERR_CAPACITY;
+  if (!ctx) return XS_ERR_ARG;
+  const xs_host_limits lim = limits_of(ctx);
+  const int rc = xs_host_check_argmax(&lim, in);
+  if (rc) return rc;
   if (hipSetDevice(ctx->device) != hipSuccess) return XS_ERR_HIP;
   xs::Args a;
   memset(&a, 0, sizeof(a));
@@ -3348,83 +3306,6 @@ int xs_argmax_probs(xs_context* ctx, const xs_argmax_args* in) {
   a.nslots = (int32_t)slots_for(in->width);
   a.rec = ctx->rec;
   return launch(ctx, a, in->rows, 1, false, true);
-}
-
-int32_t xs_select_option(const double* scores, int64_t n, double temperature, int64_t top_k,
-                         double top_p, double u, int64_t* index) {
-  if (!scores || !index || n < 1) return XS_ERR_ARG;
-  if (temperature <= 0.0 || top_k <= 1) {  // argmax_index: the first maximal score
-    double best = -INFINITY;
-    int64_t at = 0;
-    for (int64_t i = 0; i < n; i++)
-      if (scores[i] > best) {
-        best = scores[i];
-        at = i;
-      }
-    *index = at;
-    return XS_ROW_OK;
-  }
-  // renormalize at the temperature: f64 softmax (the f64::max fold skips NaN)
-  std::vector<double> p((size_t)n);
-  double mx = -INFINITY;
-  for (int64_t i = 0; i < n; i++) {
-    p[i] = scores[i] / temperature;
-    if (p[i] > mx) mx = p[i];
-  }
-  double total = -0.0;
-  for (double& v : p) {
-    v = std::exp(v - mx);
-    total += v;
-  }
-  for (double& v : p) v = v / total;
-  // rank by probability (f64::total_cmp, descending), ties to the lower index
-  auto key = [](double d) {
-    uint64_t b;
-    memcpy(&b, &d, 8);
-    return (b >> 63) ? ~b : (b | 0x8000000000000000ull);
-  };
-  std::vector<int64_t> order((size_t)n);
-  for (int64_t i = 0; i < n; i++) order[i] = i;
-  std::stable_sort(order.begin(), order.end(), [&](int64_t x, int64_t y) { return key(p[x]) > key(p[y]); });
-  const int64_t kept_k = std::min(top_k, n);
-  // the nucleus over the survivors' own mass; the crossing option stays
-  int64_t keep = kept_k;
-  if (!(top_p >= 1.0)) {
-    double mass = -0.0;
-    for (int64_t i = 0; i < kept_k; i++) mass += p[order[i]];
-    if (!(mass <= 0.0)) {
-      double run = 0.0;
-      for (int64_t i = 0; i < kept_k; i++) {
-        run += p[order[i]] / mass;
-        if (run >= top_p) {
-          keep = i + 1;
-          break;
-        }
-      }
-    }
-  }
-  // WeightedIndex<f64> (rand 0.9): cumulative weights before each later
-  // weight, the draw x = u * total, the count of cumulative weights <= x
-  double acc = p[order[0]];
-  if (!(acc >= 0.0)) return XS_ROW_ZERO_WEIGHT;
-  std::vector<double> cum;
-  for (int64_t i = 1; i < keep; i++) {
-    const double w = p[order[i]];
-    if (!(w >= 0.0)) return XS_ROW_ZERO_WEIGHT;
-    cum.push_back(acc);
-    acc += w;
-  }
-  if (acc == 0.0 || !std::isfinite(acc)) return XS_ROW_ZERO_WEIGHT;
-  const double x = u * acc + 0.0;
-  const int64_t c = std::upper_bound(cum.begin(), cum.end(), x) - cum.begin();
-  *index = order[c];
-  return XS_ROW_OK;
-}
-
-int64_t xs_keep_confident(const float* probs, int64_t n, float p_min) {
-  int64_t kept = 0;
-  while (kept < n && probs[kept] >= p_min) kept++;
-  return kept;
 }
 
 int xs_test_exp(const float* x, float* y, int64_t n, void* s) {

@@ -131,7 +131,20 @@ typedef struct {
 
 /* One batched Sampler::sample_controlled + draw over `rows` independent rows.
  * All pointers are device pointers.  Required: logits, params, uniforms, token,
- * status.  Everything else may be NULL. */
+ * status.  Everything else may be NULL.
+ *
+ * The softmax denominator: a controlled row (an allow-mask or an active
+ * xs_row_control) sums its terms serially in f32 in the reference
+ * (softmax_in_place, sampler.rs:301-305), other rows through candle's softmax.
+ * Where that sum reaches an output -- a stochastic controlled row at
+ * top_p >= 1, whose weights are p = e / sum unrenormalized, in a call that
+ * asks for cand_id, cand_w or soft_sum -- it is reproduced bit for bit (a
+ * second kernel per call).  Everywhere else the denominator is the exact sum of
+ * the same correctly rounded terms, within 2e-6 of either reference sum; it
+ * cancels from renormalized weights, and a token drawn with it differs from
+ * the serial sum's only where the uniform falls within rounding of a
+ * cumulative-weight boundary.  xs_verify, whose outputs are tokens, always
+ * reproduces it on its controlled rows at top_p >= 1. */
 typedef struct {
   const float* logits;   /* [rows, ld] row-major f32; 16-byte aligned, ld % 4 == 0 */
   int64_t rows;
@@ -187,7 +200,7 @@ int xs_sample(xs_context* ctx, const xs_sample_args* args);
 /* xs_sample without a context, for callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc).  No counterpart in the reference.  The workspace is one
- * file-scope device array of XS_NOALLOC_BYTES (9.3 MiB) that each GPU the
+ * file-scope device array of XS_NOALLOC_BYTES (14.3 MiB) that each GPU the
  * library runs on holds until the process ends; the call runs on the current
  * device and on `hip_stream`, and allocates nothing.  Limits: rows <=
  * XS_NOALLOC_ROWS and enc <= XS_NOALLOC_VOCAB (else XS_ERR_CAPACITY);
@@ -197,7 +210,7 @@ int xs_sample(xs_context* ctx, const xs_sample_args* args);
  * arrival tickets it uses before its launch. */
 #define XS_NOALLOC_ROWS 64
 #define XS_NOALLOC_VOCAB 262144
-#define XS_NOALLOC_BYTES 9787904
+#define XS_NOALLOC_BYTES 15030784
 int xs_sample_noalloc(const xs_sample_args* args, void* hip_stream);
 
 /* The speculative verify block: `seqs` sequences of `span` = D + 1 rows each

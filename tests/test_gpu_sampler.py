@@ -14,6 +14,11 @@ How each row is checked:
   * against the literal reference order (serial f32 sum, sampler.rs:301-305),
     tokens must agree on every row whose decision margins exceed MARGIN_EPS;
     rows below it are counted and reported, never re-seeded away.
+  * controlled rows (an allow-mask or sparse controls) at top_p >= 1, whose
+    weights p = e / sum reach the caller unrenormalized: the device
+    denominator must be the reference's serial f32 sum bit for bit (oracle
+    SUM_SEQ_F32), so the token and every weight equal the literal reference's
+    with no margin rule.
 """
 import math
 import os
@@ -31,6 +36,7 @@ PROB_RTOL = 1e-5       # probabilities and log-probs (north star)
 MARGIN_EPS = 1e-5      # decision margin below which the serial-f32 order may flip a draw
 V = workloads.V
 WORST = {}  # largest deviations seen, printed at the end of the module
+SERIAL_ROWS = [0]  # rows checked against the serial f32 denominator
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -82,6 +88,14 @@ def oracle_row(oracle, row, enc, T, k, p, u, mask_row=None, ctl=None, **kw):
                                     **kw)
 
 
+def serial_row(T, K, P, mask_row, ctl) -> bool:
+    """A row whose denominator is the serial f32 sum on the device: stochastic,
+    controlled (sample_controlled's non-noop branch, sampler.rs:222-229), and
+    top_p >= 1."""
+    controlled = mask_row is not None or (ctl is not None and not ctl.is_noop())
+    return not (T <= 0.0 or K <= 1) and P >= 1.0 and controlled
+
+
 def check_rows(oracle, logits, T, K, P, U, d, *, enc=None, mask=None, rows=None, margins=True,
                label="", ctls=None):
     """Compare device outputs `d` with the oracle row by row; returns the count of
@@ -124,6 +138,16 @@ def check_rows(oracle, logits, T, K, P, U, d, *, enc=None, mask=None, rows=None,
         o64 = oracle_row(oracle, logits[r], enc, T[r], K[r], P[r], U[r], mrow,
                          sum_mode=oracle.SUM_F64, **kw)
         rel = abs(float(S) - float(o64.ssum)) / float(o64.ssum)
+        if serial_row(T[r], K[r], P[r], mrow, kw.get("ctl")):
+            # the literal reference: its serial f32 sum, bit for bit
+            oseq = oracle_row(oracle, logits[r], enc, T[r], K[r], P[r], U[r], mrow,
+                              sum_mode=oracle.SUM_SEQ_F32, **kw)
+            assert np.float32(S).view(np.uint32) == np.float32(oseq.ssum).view(np.uint32), \
+                (tag, "serial sum", float(S), float(oseq.ssum))
+            assert d["token"][r] == oseq.token, (tag, "serial-f32 token")
+            WORST["serial_vs_exact"] = max(WORST.get("serial_vs_exact", 0.0), rel)
+            SERIAL_ROWS[0] += 1
+            continue
         WORST["denominator"] = max(WORST.get("denominator", 0.0), rel)
         assert rel <= DENOM_RTOL, (tag, float(S), o64.ssum, rel)
         if margins:
@@ -413,6 +437,30 @@ def test_tall_peaks_and_extreme_temperatures(ctx, oracle):
     U = rng.random(rows).astype(np.float32)
     d = run_sample(ctx, x, T, K, P, U)
     check_rows(oracle, x, T, K, P, U, d, label="tall peaks")
+
+
+def test_huge_finite_logits_are_ordinary_values(ctx, oracle):
+    """Finite logits of huge magnitude (-1e30 standing for a masked id, as
+    some producers write it) are ordinary values to the reference: exp(s - max)
+    is 0 below a moderate max, and 1 for every id equal to a huge max.  A
+    lane whose softmax offset is that large must not turn its partial into
+    inf (and then NaN once scaled by 0)."""
+    rng = np.random.default_rng(4343)
+    rows = 6
+    x = (rng.standard_normal((rows, V)) * 3.0).astype(np.float32)
+    x[0, rng.random(V) < 0.3] = -1e30             # scattered
+    x[1, : V // 2] = -1e30                        # whole chunks and waves of them
+    x[2, :] = -1e30                               # every id ties at a huge max
+    x[3, :] = np.where(rng.random(V) < 0.5, -1e30, -2e30)
+    x[4, rng.random(V) < 0.9] = -3.4e38           # near -FLT_MAX
+    x[5, ::7] = 1e30                              # huge positive values tie at the max
+    T = [1.0, 0.7, 1.0, 1.0, 0.5, 1.0]
+    K = [20, 50, 20, 100, 20, 20]
+    P = [0.95, 0.9, 0.95, 1.0, 0.9, 0.8]
+    U = rng.random(rows).astype(np.float32)
+    d = run_sample(ctx, x, T, K, P, U)
+    assert (d["status"] == 0).all(), d["status"]
+    check_rows(oracle, x, T, K, P, U, d, label="huge finite logits")
 
 
 def test_narrow_row_short_mask_and_bad_k(ctx):

@@ -242,6 +242,29 @@ def test_softmax_against_f64_closed_form(oracle):
         np.testing.assert_allclose(got_seq, ref, rtol=2e-4, atol=0)
 
 
+def test_serial_sum_spread_on_the_workload_rows(oracle):
+    """How far the reference's serial f32 denominator (controlled rows,
+    sampler.rs:301-305) lies from the exact sum of the same f32 terms on rows
+    shaped like C2, C3 and C5: ~1e-4 and more, far past the 1e-5 bar, so a
+    device that used the exact sum on controlled rows at top_p >= 1 would miss
+    the reference's weights; the serial sum has to be reproduced itself."""
+    from tests import workloads
+    spread = {}
+    for name, wl in (("C2", workloads.c2_batch(rows=8)), ("C3", workloads.c3_masked(rows=9)),
+                     ("C5", workloads.c5_heterogeneous(rows=8))):
+        rows, V = wl.logits.shape
+        T = np.where(wl.temperature > 0, wl.temperature, 1.0)  # every row stochastic here
+        kw = dict(mask=wl.mask) if wl.mask is not None else {}
+        seq = oracle.sample_rows(wl.logits, V, T, 20, 1.0, wl.u, sum_mode=oracle.SUM_SEQ_F32, **kw)
+        ex = oracle.sample_rows(wl.logits, V, T, 20, 1.0, wl.u, sum_mode=oracle.SUM_F64, **kw)
+        ok = (seq["status"] == 0) & (ex["status"] == 0)
+        rel = np.abs(seq["ssum"][ok].astype(np.float64) / ex["ssum"][ok] - 1.0)
+        spread[name] = (float(np.median(rel)), float(rel.max()))
+    print("serial f32 sum vs exact (median, max):", spread)
+    assert spread["C2"][0] > 1e-5 and spread["C3"][1] > 1e-5
+    assert all(mx < 5e-3 for _, mx in spread.values())
+
+
 # --- the draw ----------------------------------------------------------------
 
 def test_weighted_index_boundaries(oracle):

@@ -23,7 +23,7 @@ CTL_MAX = 2048
 ORDER_MAX = 1024
 NOALLOC_ROWS = 64
 NOALLOC_VOCAB = 262144
-NOALLOC_BYTES = 9787904
+NOALLOC_BYTES = 15030784
 
 _vp = C.c_void_p
 _i64 = C.c_int64

@@ -202,6 +202,15 @@ XS_DEV double wave_sumd(double v) {
 }
 // (written out: the unroller leaves a loop over these exchanges rolled, and a
 // rolled one selects its DPP pattern by comparisons at run time)
+XS_DEV uint32_t wave_sum_u32(uint32_t v) {
+  v += xor_u32(v, 32);
+  v += xor_u32(v, 16);
+  v += xor_u32(v, 8);
+  v += xor_u32(v, 4);
+  v += xor_u32(v, 2);
+  v += xor_u32(v, 1);
+  return v;
+}
 XS_DEV uint32_t wave_or(uint32_t v) {
   v |= xor_u32(v, 32);
   v |= xor_u32(v, 16);
@@ -408,6 +417,12 @@ struct Args {
   int32_t k_max;     // the context's largest top_k (of min(top_k, enc)); larger is XS_ROW_BAD_PARAM
   uint64_t* big;     // [rows, 2, big_ld]: big_finalize's sort buffers (contexts with k_max > XS_K_MAX)
   int64_t big_ld;
+  // the serial denominator (serial_kernel): set on calls with a mask or
+  // controls, whose rows at top_p >= 1 serial_kernel finalizes
+  int32_t serial;
+  uint64_t* ser_sum;  // [rows, ser_ld, 2]: segment summaries
+  uint64_t* ser_e;    // [rows, SER_NB, SEG / 2]: kept segments' terms, two f32 per word
+  int64_t ser_ld;     // segments per row of ser_sum
   uint64_t* rec;     // [rows, SRECW, nsp]: word i of sub-record s of a row at i * nsp + s
 };
 
@@ -639,6 +654,7 @@ struct FinLds {
   uint64_t psel[KSEL];              // the candidate set in draw order: (p bits << 32) | ~id
   double expt[64];                  // kExpT, flattened
   uint32_t keys[GMAX * 64 * 4];     // published bound keys (more than 64 sub-records)
+  uint32_t zmap[KSEL / 32];         // a whole short row: the ids with p > 0
   HeldLds held;
   BigStash big;
 };
@@ -1087,7 +1103,7 @@ XS_DEV void held_fold(const Args& a, int row, const float* rowp, const uint64_t*
 template <bool HAS_MASK, bool WANT_LSE>
 XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, int nsub, const uint64_t (&h)[NHW],
                      const uint64_t (&E)[EPRE], const uint64_t* rowrec, int nsp, const float* rowp,
-                     FinLds& F) {
+                     FinLds& F, float S_ser) {
   const int lane = lane_id();
   const bool live = lane < nsub;
   const bool stoch = !cfg.greedy;
@@ -1112,7 +1128,7 @@ XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, int nsub, const uin
   }
   const double S_d = red_sumd(part);
   const double R_d = WANT_LSE ? red_sumd(rpart) : 0.0;
-  const float S = (float)S_d;
+  const float S = S_ser >= 0.0f ? S_ser : (float)S_d;  // a controlled row's serial sum, when given
   int st = XS_ROW_OK;
   if (HAS_MASK && !finite_seen) st = XS_ROW_NO_FINITE;
   else if (cfg.greedy) st = nan_seen ? XS_ROW_NAN : (m_v == -INFINITY ? XS_ROW_NO_FINITE : XS_ROW_OK);
@@ -1196,10 +1212,13 @@ XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, int nsub, const uin
     sel = F.srt[lane];
   }
   const int nsel = min(M, kp);
+  const bool want_cands = a.cand_id != nullptr || a.cand_w != nullptr;
+  // a whole short row with ids the selection never holds (-inf): the
+  // general path lists them
+  if (cfg.full && stoch && nsel < k && want_cands) return false;
 
   // Probabilities of the selection (lanes < nsel) and, on lane nsel, of the
   // largest value below the last selected logit (the boundary proof).
-  const bool want_cands = a.cand_id != nullptr || a.cand_w != nullptr;
   const double* T = F.expt;
   float pw = 0.0f;
   uint64_t pk = 0ull;
@@ -1348,7 +1367,7 @@ XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, int nsub, const uin
 template <bool HAS_MASK, bool WANT_LSE, bool HAS_CTL>
 XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* rowrec,
                         int nsp, int nsub, const float* rowp, const uint32_t* mrow, const CtlRow& cr,
-                        const uint64_t (&h)[NHW], const uint64_t (&E)[EPRE], FinLds& F) {
+                        const uint64_t (&h)[NHW], const uint64_t (&E)[EPRE], FinLds& F, float S_ser) {
   const int lane = lane_id();
   const int kp = cfg.kp, enc = (int)a.enc;
   const bool stoch = !cfg.greedy && !cfg.bad;
@@ -1395,7 +1414,7 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
   }
   S_d = wave_sumd(S_d);
   if (WANT_LSE) R_d = wave_sumd(R_d);
-  const float S = (float)S_d;
+  const float S = S_ser >= 0.0f ? S_ser : (float)S_d;  // a controlled row's serial sum, when given
   const bool nan_seen = fl & 1u;
   const bool finite_seen = fl & 2u;
 
@@ -1984,12 +2003,49 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
   }
   if (want_cands && stoch && st == XS_ROW_OK && !defer) {
     const int kw = (int)min((int64_t)k, a.cand_ld);  // a short cand_ld truncates the list
+    // k >= enc on a row of at most KSEL ids, some of which the selection never
+    // holds (-inf: masked or banned): the sort-everything branch lists every
+    // id (candidate_set, sampler.rs:322-332), those at p = 0 in id order
+    // after the g entries with p > 0
+    const bool fill = cfg.full && nsel < k;
+    int g = kw;
+    if (fill) {
+      if (lane < KSEL / 32) F.zmap[lane] = 0u;
+      wave_lds_sync();
+      int npos = 0;
+#pragma unroll
+      for (int r = 0; r < 2; r++) {
+        const bool pos = r * 64 + lane < nsel && (uint32_t)(pk[r] >> 32) != 0u;
+        if (pos) {
+          const uint32_t id = 0xFFFFFFFFu - (uint32_t)pk[r];
+          atomicOr(&F.zmap[id >> 5], 1u << (id & 31));
+        }
+        npos += __popcll(__ballot(pos));
+      }
+      wave_lds_sync();
+      g = min(npos, kw);
+    }
 #pragma unroll
     for (int r = 0; r < 2; r++) {
       const int i = r * 64 + lane;
-      if (i < kw) {
+      if (i < g) {
         if (a.cand_id) a.cand_id[(int64_t)row * a.cand_ld + i] = (int32_t)(0xFFFFFFFFu - (uint32_t)pk[r]);
         if (a.cand_w) a.cand_w[(int64_t)row * a.cand_ld + i] = w[r];
+      }
+    }
+    if (fill) {
+      int below = 0;  // p = 0 ids of the earlier rounds
+#pragma unroll
+      for (int r = 0; r < 2; r++) {
+        const int i = r * 64 + lane;
+        const bool zero = i < enc && !((F.zmap[i >> 5] >> (i & 31)) & 1u);
+        const uint64_t zb = __ballot(zero);
+        const int at = g + below + lanes_below(zb);
+        if (zero && at < kw) {
+          if (a.cand_id) a.cand_id[(int64_t)row * a.cand_ld + at] = i;
+          if (a.cand_w) a.cand_w[(int64_t)row * a.cand_ld + at] = 0.0f;
+        }
+        below += __popcll(zb);
       }
     }
   }
@@ -2014,7 +2070,8 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
 // (accept_drafts).
 template <bool HAS_MASK, bool WANT_LSE, bool HAS_CTL>
 XS_DEV void finalize_row(const Args& a, const Cfg& cfg, int row, const uint64_t* rowrec, int nsp,
-                         int nsub, const float* rowp, const uint32_t* mrow, FinLds& F) {
+                         int nsub, const float* rowp, const uint32_t* mrow, FinLds& F,
+                         float S_ser = -1.0f) {
   const int lane = lane_id();
   uint64_t h[NHW], E[EPRE];
   const bool live = lane < nsub;
@@ -2025,8 +2082,8 @@ XS_DEV void finalize_row(const Args& a, const Cfg& cfg, int row, const uint64_t*
   CtlRow cr{};
   if (HAS_CTL) cr = a.ctl_row[row];
   const bool done = !(HAS_CTL && cr.active) && nsub <= 64 && cfg.kp <= 64 && !cfg.bad && !cfg.big &&
-                    fin_fast<HAS_MASK, WANT_LSE>(a, cfg, row, nsub, h, E, rowrec, nsp, rowp, F);
-  if (!done) fin_general<HAS_MASK, WANT_LSE, HAS_CTL>(a, cfg, row, rowrec, nsp, nsub, rowp, mrow, cr, h, E, F);
+                    fin_fast<HAS_MASK, WANT_LSE>(a, cfg, row, nsub, h, E, rowrec, nsp, rowp, F, S_ser);
+  if (!done) fin_general<HAS_MASK, WANT_LSE, HAS_CTL>(a, cfg, row, rowrec, nsp, nsub, rowp, mrow, cr, h, E, F, S_ser);
 
 }
 
@@ -2302,6 +2359,259 @@ XS_DEV void big_finalize(const Args& a, const Cfg& cfg, int row, const float* ro
 }
 
 // ---------------------------------------------------------------------------
+// The serial denominator.  On a controlled row (an allow-mask or active sparse
+// controls) the reference adds the softmax terms one at a time in f32, in id
+// order, from +0 (softmax_in_place, sampler.rs:301-305), and at top_p >= 1
+// the candidate weights p = e / sum reach the caller unrenormalized: that sum
+// is reproduced bit for bit.
+//
+// The terms are >= 0, so the running sum s never falls, and while s stays in
+// one binade [2^b, 2^(b+1)) every addition rounds its term to that binade's
+// grid 2^(b-23): fl(s + e) = s + rn(e / grid) * grid, which adds an integer to
+// s's bit pattern (subnormal s: the grid 2^-149).  serial_kernel cuts the row
+// into segments of SEG ids (one wave's float4s of one slot) and sums, per
+// segment, its terms in grid units of the binade the exact sum before the
+// segment lies in -- and of the binade below too when that sum lies within
+// SER_DELTA above a power of two: the serial sum stays within a fraction of a
+// percent of the exact one -- noting any term exactly half-way between two
+// grid points, whose rounding (half to even) depends on s itself.  A term's
+// units come from a short f32 exp whose error bound settles almost all of
+// them; a term the bound leaves open, or a subnormal one, is recomputed
+// correctly rounded.  The row's last workgroup walks the segments in order: a
+// segment whose summary holds s's binade, with no half-way term, and whose
+// units keep s below the next binade adds them to s's bits; any other
+// segment adds units up to its first term that carries or ties, and from
+// there its terms one at a time in f32, as the reference does.  Segments
+// where the exact sum may pass a power of two, or that hold a half-way term,
+// keep their correctly rounded terms in a side buffer for that.
+constexpr int SEG = 256;               // ids per segment
+constexpr uint32_t GSAT = 1u << 23;    // grid units that always carry into the next binade
+constexpr int SER_NB = 64;             // segments per row whose terms are kept
+constexpr int SER_WIN = 1024;          // segment summaries the walk stages at a time
+constexpr int SER_LDS = 32;            // kept segments staged in LDS
+constexpr int SER_QCAP = 128;          // per wave: terms queued for the correctly rounded exp
+constexpr double SER_DELTA = 1.0 / 512;  // margin on the exact prefix for a binade change
+constexpr float LOG2E_LO = 1.925963033500011e-08f;  // log2(e) - LOG2E
+constexpr float LN2F = 0.6931471805599453f;
+// summary word 1, high half: the lower binade's exponent field, a half-way
+// term at it (bit 8) or at the next binade (9), units of that next binade
+// present (10), every term +0 (11), and 1 + the kept-terms slot (16..)
+constexpr uint32_t SM_TIE0 = 1u << 8, SM_TIE1 = 1u << 9, SM_TWO = 1u << 10, SM_ZERO = 1u << 11;
+
+// A row whose denominator is the serial sum and reaches the caller:
+// stochastic, controlled, top_p >= 1 (the weights are not renormalized).
+template <bool HAS_MASK, bool HAS_CTL>
+XS_DEV bool serial_row(const Args& a, const Cfg& cfg, int row) {
+  if (cfg.greedy || cfg.bad || !(cfg.top_p >= 1.0f)) return false;
+  if (HAS_MASK) return true;
+  return HAS_CTL && a.ctl_row[row].active != 0;
+}
+
+// rn(e / grid) of a term e >= 0 (bits eb) at the grid of binade field F
+// (the f32 exponent field, 0 for subnormals), saturated at GSAT; *tie when e
+// lies exactly half-way between two grid points.  Branch-free.
+XS_DEV uint32_t grid_units(uint32_t eb, int F, bool& tie) {
+  const int c = (int)(eb >> 23);
+  const uint32_t M = (eb & 0x7FFFFFu) | (c ? 0x800000u : 0u);
+  const int k = max(F, 1) - max(c, 1);     // bits of e below the grid
+  const int ks = min(max(k, 1), 31);
+  const uint32_t half = 1u << (ks - 1);
+  const uint32_t rem = M & ((half << 1) - 1u);
+  const uint32_t rq = (M >> ks) + (rem > half ? 1u : 0u);  // 0 once k > 24
+  tie = k >= 1 && rem == half;
+  return min(k < 0 ? GSAT : (k == 0 ? M : rq), GSAT);
+}
+
+XS_DEV int f32_field(float f) { return (int)(__float_as_uint(f) >> 23); }
+
+// exp(d), d <= 0: within 2^-21 of the correctly rounded f32 value for
+// d >= -87 (d * log2e split in two, v_exp_f32 on the high part, a first-order
+// correction for the low one)
+XS_DEV float fast_expf(float d) {
+  const float dc = fmaxf(d, -200.0f);  // -inf: 0, not a NaN
+  const float hi = dc * LOG2E;
+  const float lo = __builtin_fmaf(dc, LOG2E, -hi) + dc * LOG2E_LO;
+  const float e2 = xexp2(hi);
+  return e2 + e2 * (lo * LN2F);
+}
+
+// rn(e / grid) at binade field F from an estimate ef within 2^-21 of e; false
+// when that bound cannot settle it (a value near a grid midpoint, or 2^20
+// units and more)
+XS_DEV bool fast_units(float ef, int F, uint32_t& r) {
+  const float u = __builtin_ldexpf(ef, 150 - max(F, 1));
+  const float fl = __builtin_floorf(u);
+  const float fr = u - fl;
+  r = (uint32_t)fminf(fl, (float)GSAT) + (fr > 0.5f ? 1u : 0u);
+  return u < 0x1p20f && __builtin_fabsf(fr - 0.5f) > u * 0x1p-19f + 0x1p-60f;
+}
+
+// The sparse controls of one slot (first id sb) on the thread whose float4
+// is pos: the forced id alone, or the slot's patches (final values, sorted by
+// id, read from pc on; patches of earlier slots are passed over) and then the
+// pulled id.
+XS_DEV void ctl_slot(float (&x)[4], int sb, int pos, const uint64_t* pl, int& pc, int phi, int pull,
+                     float pval, int force, float fval) {
+  if (force >= 0) {
+#pragma unroll
+    for (int e = 0; e < 4; e++) x[e] = (sb + 4 * pos + e == force) ? fval : -INFINITY;
+    return;
+  }
+  while (pc < phi) {
+    const uint64_t pe = pl[pc];
+    const int off = (int)(uint32_t)(pe >> 32) - sb;
+    if (off >= SLOT) break;
+    if (off >= 0 && (off >> 2) == pos) {
+      const float pv = __uint_as_float((uint32_t)pe);
+#pragma unroll
+      for (int e = 0; e < 4; e++) x[e] = ((off & 3) == e) ? pv : x[e];
+    }
+    pc++;
+  }
+  const int pt = pull - sb;
+  if (pt >= 0 && pt < SLOT && (pt >> 2) == pos) {
+#pragma unroll
+    for (int e = 0; e < 4; e++) x[e] = ((pt & 3) == e) ? pval : x[e];
+  }
+}
+
+// The softmax terms of segment g, this lane's four: exp(v * inv - max) of the
+// masked and controlled values, correctly rounded (the walk's rare recount of
+// a segment whose terms were not kept).
+template <bool HAS_MASK, bool HAS_CTL>
+XS_DEV void seg_terms(const Args& a, const Cfg& cfg, int row, int g, float m_s, const double* T,
+                      float (&ev)[4]) {
+  const int lane = lane_id();
+  const int enc = (int)a.enc;
+  const int slot = g >> 2, w = g & 3;
+  const int sb = slot * SLOT, pos = 64 * w + lane, id0 = sb + 4 * pos;
+  const float* rowp = a.logits + (int64_t)row * a.ld;
+  const int f = min(id0 >> 2, (enc - 1) >> 2);
+  const float4 q = reinterpret_cast<const float4*>(rowp)[f];
+  float x[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    const int id = id0 + e;
+    if (id >= enc) x[e] = -INFINITY;
+    else if (HAS_MASK && !((a.allowed[(int64_t)row * a.allowed_ld + (id >> 5)] >> (id & 31)) & 1u)) x[e] = -INFINITY;
+  }
+  if (HAS_CTL) {
+    const CtlRow cr = a.ctl_row[row];
+    if (cr.active) {
+      const int chunk = slot / SPC;
+      int pc = a.ctl_chunk[(int64_t)row * (a.n_chunks + 1) + chunk];
+      const int phi = a.ctl_chunk[(int64_t)row * (a.n_chunks + 1) + chunk + 1];
+      ctl_slot(x, sb, pos, a.patch + (int64_t)row * CTL_MAX, pc, phi, cr.pull_id, cr.pull_val, cr.force_id,
+               cr.force_val);
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 4; e++) ev[e] = cr_expf((cfg.scale ? x[e] * cfg.inv : x[e]) - m_s, T);
+}
+
+// One segment added to the running sum's bits sb, its SEG terms at evp (LDS,
+// in id order): grid units up to the first term that carries into the next
+// binade or lies half-way, and from there the terms one at a time by f32 adds
+// (the reference's own operation).  One wave.
+XS_DEV uint32_t ser_segment(uint32_t sb, const float* evp) {
+  const int lane = lane_id();
+  const float4 e4 = reinterpret_cast<const float4*>(evp)[lane];
+  const float ev[4] = {e4.x, e4.y, e4.z, e4.w};
+  const uint32_t F = sb >> 23, m = F ? (sb & 0x7FFFFFu) : sb;
+  uint32_t p[4], P = 0;
+  bool tie[4];
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    P += grid_units(__float_as_uint(ev[k]), (int)F, tie[k]);
+    p[k] = P;
+  }
+  const uint32_t Pc = min(P, GSAT);
+  const uint32_t incl = (uint32_t)wave_incl_scan((int)Pc);
+  const uint32_t excl = incl - Pc;
+  int kf = 4;  // this lane's first term that carries or ties
+#pragma unroll
+  for (int k = 3; k >= 0; k--)
+    if (tie[k] || m + excl + p[k] >= GSAT) kf = k;
+  const uint64_t bm = __ballot(kf < 4);
+  if (!bm) return sb + rdl(incl, 63);
+  const int L = (int)__builtin_ctzll(bm);
+  uint32_t before = excl;  // units before that term
+#pragma unroll
+  for (int k = 1; k < 4; k++) before = (kf == k) ? excl + p[k - 1] : before;
+  sb += rdl(before, L);
+  const int start = 4 * L + (int)rdl((uint32_t)kf, L);
+  float s = __uint_as_float(sb);
+  if (lane == 0) {
+#pragma unroll 8
+    for (int i = start; i < SEG; i++) s = s + evp[i];
+  }
+  return (uint32_t)__builtin_amdgcn_readfirstlane((int)__float_as_uint(s));
+}
+
+// The walk over segments w0 .. w0 + wn - 1 of a row (their summaries staged
+// in sum), from the running sum's bits sb.  One wave; lane i holds the
+// summary of the i-th segment of each group of 64.  A segment added term by
+// term has its terms in LDS (evl[0 .. nbl)), or copied from the side buffer,
+// or recounted from the logits, into evl[SER_LDS].
+template <bool HAS_MASK, bool HAS_CTL>
+XS_DEV uint32_t ser_walk(const Args& a, const Cfg& cfg, int row, uint32_t sb, const uint64_t (*sum)[2], int w0,
+                         int wn, float (*evl)[SEG], int nbl, const uint64_t* skeep, float m_s, const double* T) {
+  const int lane = lane_id();
+#pragma unroll 1
+  for (int b0 = 0; b0 < wn; b0 += 64) {
+    const int i = b0 + lane;
+    const bool v = i < wn;
+    const uint64_t u01 = v ? sum[i][0] : 0ull, u1m = v ? sum[i][1] : 0ull;
+    const uint32_t meta = (uint32_t)(u1m >> 32);
+    const bool zero = (meta & SM_ZERO) != 0;  // a segment of +0 terms adds nothing at any grid
+    const int nl = min(64, wn - b0);
+    int cur = 0;  // the first segment of the group not yet added
+#pragma unroll 1
+    while (cur < nl) {
+      const uint32_t F = sb >> 23, m = F ? (sb & 0x7FFFFFu) : sb;
+      const int d = (int)F - (int)(meta & 0xFFu);
+      const bool okd = zero || (d == 0 && !(meta & SM_TIE0)) ||
+                       (d == 1 && (meta & SM_TWO) && !(meta & SM_TIE1));
+      uint32_t r = d == 0 ? (uint32_t)u01 : (uint32_t)(u01 >> 32);
+      r = zero ? 0u : (okd ? min(r, GSAT) : GSAT);
+      if (lane < cur || !v) r = 0;
+      const uint32_t inc = (uint32_t)wave_incl_scan((int)r);
+      const uint64_t bm = __ballot(v && lane >= cur && (!okd || m + inc >= GSAT));
+      if (!bm) {
+        sb += rdl(inc, 63);
+        break;
+      }
+      const int f = (int)__builtin_ctzll(bm);
+      if (f > 0) sb += rdl(inc, f - 1);
+      const int kept = (int)(rdl(meta, f) >> 16);
+      const float* evp;
+      if (kept > 0 && kept <= nbl) {
+        evp = evl[kept - 1];
+      } else {
+        float ev[4];
+        if (kept > 0) {
+          const uint64_t* src = skeep + (int64_t)(kept - 1) * (SEG / 2) + 2 * lane;
+          const uint64_t e01 = ld_agent(src), e23 = ld_agent(src + 1);
+          ev[0] = __uint_as_float((uint32_t)e01);
+          ev[1] = __uint_as_float((uint32_t)(e01 >> 32));
+          ev[2] = __uint_as_float((uint32_t)e23);
+          ev[3] = __uint_as_float((uint32_t)(e23 >> 32));
+        } else {
+          seg_terms<HAS_MASK, HAS_CTL>(a, cfg, row, w0 + b0 + f, m_s, T, ev);
+        }
+        reinterpret_cast<float4*>(evl[SER_LDS])[lane] = make_float4(ev[0], ev[1], ev[2], ev[3]);
+        wave_lds_sync();
+        evp = evl[SER_LDS];
+      }
+      sb = ser_segment(sb, evp);
+      wave_lds_sync();  // (the scratch row is rewritten by the next recount)
+      cur = f + 1;
+    }
+  }
+  return sb;
+}
+
+// ---------------------------------------------------------------------------
 // The kernel.  Grid: rows x n_chunks workgroups of BLOCK lanes; chunk c of a
 // row covers slots [c*SPC, c*SPC + SPC).  Every wave reduces its own share of
 // the chunk and publishes it as one sub-record; the row's last workgroup to
@@ -2460,13 +2770,16 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
   float c_w = 0.0f;  // offset of the published softmax partial
   uint32_t flags = 0;
   if (stoch) {
-    // lanes whose max sits more than 40 above their offset: recount against
-    // the max (rare; makes +inf a NaN)
+    // lanes whose max sits more than 40 above their offset, or whose offset
+    // is so large (|c_s| >= 2^20, e.g. -1e30 standing for a masked id) that
+    // rn(c_s * log2e) misses c_s * log2e by units and the terms above are
+    // garbage: recount against the lane max as exp2((s - max) * log2e), the
+    // difference taken first (rare; makes +inf a NaN)
     const float ms = mr * inv_e;
-    const bool redo = ms > c_s + 40.0f;
+    const bool redo = ms > c_s + 40.0f || !(__builtin_fabsf(c_s) < 0x1p20f);
+    bool exact_off = false;
     if (__ballot(redo)) {
       const float cn = redo ? ms : c_s;
-      const float cLn = cn * LOG2E;
       float s2 = 0.0f;
 #pragma unroll
       for (int j = 0; j < SPC; j++) {
@@ -2474,21 +2787,23 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
 #pragma unroll
         for (int e = 0; e < 4; e++) {
           const float xv = q4(q[j], e);
-          t[e] = xexp2(__builtin_fmaf(xv * inv_e, LOG2E, -cLn));
+          t[e] = xexp2((xv * inv_e - cn) * LOG2E);
         }
         s2 += (t[0] + t[1]) + (t[2] + t[3]);
       }
       if (redo) {
         sum = s2;
         c_s = cn;
-        cL = cLn;
+        exact_off = true;
       }
     }
-    // lanes to the wave's scaled max c_w: factor 2^(cL - c_w*log2e), that is
-    // e^(c_s - c_w) with cL's own rounding taken out (0 for a NaN or -inf
-    // exponent, which keeps a NaN sum NaN)
+    // lanes to the wave's scaled max c_w: factor e^(c_s - c_w), as
+    // 2^(cL - c_w*log2e) with cL's own rounding taken out on lanes summed
+    // against cL, as 2^((c_s - c_w)*log2e) on recounted ones (0 for a NaN or
+    // -inf exponent, which keeps a NaN sum NaN)
     c_w = m_w * inv_e;
-    const double dd = (double)cL - (double)c_w * (double)LOG2E;
+    const double dd = exact_off ? ((double)c_s - (double)c_w) * (double)LOG2E
+                                : (double)cL - (double)c_w * (double)LOG2E;
     const double dn = ::fmin(::fmax(::rint(dd), -2100.0), 2100.0);
     const double fac = (dd > -2100.0) ? ldexp((double)xexp2((float)(dd - dn)), (int)dn) : 0.0;
     const double part = (sum != 0.0f) ? (double)sum * fac : (double)sum;
@@ -2766,6 +3081,7 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
   }
   __syncthreads();
   if (!Lc.last) return;
+  if (a.serial && serial_row<HAS_MASK, HAS_CTL>(a, cfg, row)) return;  // serial_kernel finalizes it
   // The first wave finalizes the row; held_row outputs then get the reference's
   // serial fold (held_fold); a row with more candidates than the selection
   // holds is drawn by the whole workgroup (big_finalize); a verify block's
@@ -2777,6 +3093,340 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
     if (held) held_fold<1>(a, row, rowp, rowrec, nsp, nc * NWAVE, Tl.fin);
   }
   if (big_row) big_finalize<HAS_MASK, HAS_CTL>(a, cfg, row, rowp, mrow, Tl);
+  if (wave == 0 && a.span > 0) verify_walk(a, row);
+}
+
+// ---------------------------------------------------------------------------
+// serial_kernel: the serial denominator of a call's controlled rows at
+// top_p >= 1, launched after sample_kernel on calls with a mask or controls
+// that can observe it (sample_kernel's last workgroup leaves those rows
+// unfinalized).  Grid: rows x n_chunks workgroups, the chunks of
+// sample_kernel; other rows' return at once.  Each workgroup reads the row's
+// max and the exact sum before its chunk from the row's sub-record headers,
+// recomputes its chunk's terms, and writes one summary per segment (the grid
+// units, the half-way flags, and the kept terms where the exact prefix may
+// pass a power of two or a flag is set).  The row's last workgroup (the
+// arrival ticket, as in sample_kernel) walks the summaries and finalizes the
+// row with the serial sum as its denominator.
+struct SerLds {
+  double expt[64];
+  double segsum[SPC * NWAVE];  // exact sums of the chunk's segments, row order (short exp)
+  double segpre[SPC * NWAVE];  // the exact sum before each
+  double xc;                   // the exact sum before the chunk
+  uint32_t R[SPC * NWAVE][2];  // units at the segment's lower binade and the next
+  uint32_t meta[SPC * NWAVE];  // summary word 1's high half, without the kept slot
+  uint64_t kmask;              // segments of the chunk that keep their terms
+  float qd[NWAVE][SER_QCAP];   // per wave: exp arguments queued for the correctly rounded exp
+  uint8_t qt[NWAVE][SER_QCAP]; // and their segments
+  float m_s;
+  int32_t ok, last, nb, kbase;
+};
+union SerTail {
+  struct {
+    uint64_t sum[SER_WIN][2];    // staged summaries
+    float ev[SER_LDS + 1][SEG];  // staged kept terms, and a scratch segment
+  } w;
+  TailLds tl;
+};
+
+// The queued terms of one wave: each correctly rounded, its units and
+// half-way flags added to its segment's summary (LDS atomics: a segment's
+// fast units are added the same way).  Out of line: the pass calls it from
+// many places, and seldom.
+__device__ __attribute__((noinline)) void ser_flush(SerLds& L, int wave, int n, const double* T) {
+  const int lane = lane_id();
+  wave_lds_sync();  // the queue and the segments' binades are written
+  for (int i0 = 0; i0 < n; i0 += 64) {
+    const int i = i0 + lane;
+    if (i < n) {
+      const int t = L.qt[wave][i];
+      const float e = cr_expf(L.qd[wave][i], T);
+      const uint32_t mt = L.meta[t];
+      const int FB = (int)(mt & 0xFFu);
+      bool t0, t1 = false;
+      atomicAdd(&L.R[t][0], grid_units(__float_as_uint(e), FB, t0));
+      if (mt & SM_TWO) atomicAdd(&L.R[t][1], grid_units(__float_as_uint(e), FB + 1, t1));
+      if (t0 || t1) atomicOr(&L.meta[t], (t0 ? SM_TIE0 : 0u) | (t1 ? SM_TIE1 : 0u));
+    }
+  }
+  wave_lds_sync();
+}
+
+// Four terms correctly rounded, out of line (only kept segments need them).
+__device__ __attribute__((noinline)) float4 cr_exp4(float4 d, const double* T) {
+  return make_float4(cr_expf(d.x, T), cr_expf(d.y, T), cr_expf(d.z, T), cr_expf(d.w, T));
+}
+
+template <bool HAS_MASK, bool HAS_CTL>
+__global__ __launch_bounds__(BLOCK) void serial_kernel(Args a) {
+  __shared__ SerLds Ls;
+  __shared__ SerTail St;
+  const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
+  const int nc = a.n_chunks;
+  const int row = blockIdx.x / nc;
+  const int chunk = blockIdx.x - row * nc;
+  const Cfg cfg = make_cfg(a.params[row], a.enc, a.n_top, a.k_max);
+  if (!serial_row<HAS_MASK, HAS_CTL>(a, cfg, row)) return;
+  const int enc = (int)a.enc;
+  const int s0 = chunk * SPC;
+  const int ns = min(SPC, a.nslots - s0);
+  const float* rowp = a.logits + (int64_t)row * a.ld;
+  const v4f* rp4 = reinterpret_cast<const v4f*>(rowp);
+  const uint32_t* mrow = HAS_MASK ? a.allowed + (int64_t)row * a.allowed_ld : nullptr;
+  const int fmax = (enc - 1) >> 2;
+  const int nsp = ((nc * NWAVE + 63) >> 6) << 6;
+  const uint64_t* const rowrec = a.rec + (int64_t)row * SRECW * nsp;
+  const int nsub = nc * NWAVE;
+  // the row max (sample_kernel's headers) and the exact sum before this
+  // chunk: their loads go out first, the chunk's after them
+  uint64_t h0[GMAX], h1[GMAX], h3[GMAX];
+  if (wave == 0) {
+#pragma unroll
+    for (int gi = 0; gi < GMAX; gi++) {
+      const int sub = gi * 64 + lane;
+      const bool before = sub < chunk * NWAVE;
+      h3[gi] = sub < nsub ? ld_agent(&rowrec[3 * nsp + sub]) : 0ull;
+      h0[gi] = before ? ld_agent(&rowrec[sub]) : 0ull;
+      h1[gi] = before ? ld_agent(&rowrec[nsp + sub]) : 0ull;
+    }
+  }
+  v4f q[SPC];
+  uint32_t mw[SPC];
+#pragma unroll
+  for (int j = 0; j < SPC; j++) {
+    const int f = min((s0 + j) * BLOCK + tid, fmax);
+    q[j] = rp4[f];
+    if (HAS_MASK) mw[j] = mrow[f >> 3];
+  }
+  CtlRow cr{};
+  if (HAS_CTL) cr = a.ctl_row[row];
+  if (tid < 64) Ls.expt[tid] = (&kExpT[0][0])[tid];
+  if (wave == 0) {
+    float mv = -INFINITY;
+    uint32_t fw = 0;
+#pragma unroll
+    for (int gi = 0; gi < GMAX; gi++) {
+      if (gi * 64 + lane < nsub) {
+        mv = fmaxf(mv, __uint_as_float((uint32_t)h3[gi]));
+        fw |= (uint32_t)(h3[gi] >> 32);
+      }
+    }
+    const float m_v = wave_maxf(mv);
+    const uint32_t fl = wave_or(fw);
+    const float m_s = cfg.scale ? m_v * cfg.inv : m_v;
+    double xc = 0.0;
+#pragma unroll
+    for (int gi = 0; gi < GMAX; gi++) {
+      const double p = __longlong_as_double((long long)h0[gi]);
+      if (p != 0.0) xc += p * (double)xexp2((__uint_as_float((uint32_t)h1[gi]) - m_s) * LOG2E);
+    }
+    xc = wave_sumd(xc);
+    if (lane == 0) {
+      Ls.m_s = m_s;
+      Ls.xc = xc;
+      // the row draws (else the finalizer reports its status, and no sum is needed)
+      Ls.ok = ((fl & 2u) && !(fl & 1u) && !__builtin_isinf(m_s) &&
+               (!(HAS_CTL && cr.active) || cr.status == XS_ROW_OK)) ? 1 : 0;
+    }
+  }
+  __syncthreads();
+  const bool ok = Ls.ok != 0;  // uniform
+  const float m_s = Ls.m_s;
+  if (ok) {
+    // each term's exp argument d = s - max, the values masked and controlled
+    // as sample_kernel's pass does, and the segments' exact sums (short exp)
+    const bool ctl_on = HAS_CTL && cr.active;
+    int pc = 0, phi = 0;
+    const uint64_t* pl = nullptr;
+    if (ctl_on) {
+      pc = a.ctl_chunk[(int64_t)row * (nc + 1) + chunk];
+      phi = a.ctl_chunk[(int64_t)row * (nc + 1) + chunk + 1];
+      pl = a.patch + (int64_t)row * CTL_MAX;
+    }
+#pragma unroll
+    for (int j = 0; j < SPC; j++) {
+      float x[4] = {q[j].x, q[j].y, q[j].z, q[j].w};
+      if (HAS_MASK) {
+        const uint32_t bits = mw[j] >> ((((s0 + j) * BLOCK + tid) & 7) * 4);
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+          if (!((bits >> e) & 1u)) x[e] = -INFINITY;
+      }
+      if (j >= ns || (s0 + j + 1) * SLOT > enc) {
+        const int id0 = (s0 + j) * SLOT + 4 * tid;
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+          if (j >= ns || id0 + e >= enc) x[e] = -INFINITY;
+      }
+      if (ctl_on) ctl_slot(x, (s0 + j) * SLOT, tid, pl, pc, phi, cr.pull_id, cr.pull_val, cr.force_id, cr.force_val);
+      float dv[4], t = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        dv[e] = (cfg.scale ? x[e] * cfg.inv : x[e]) - m_s;
+        t += fast_expf(dv[e]);
+      }
+      q[j] = v4f{dv[0], dv[1], dv[2], dv[3]};
+      const double ssum = wave_sumd((double)t);
+      const bool any = __ballot(dv[0] >= -104.0f || dv[1] >= -104.0f || dv[2] >= -104.0f || dv[3] >= -104.0f) != 0;
+      if (lane == 0) {
+        Ls.segsum[j * NWAVE + wave] = ssum;
+        Ls.meta[j * NWAVE + wave] = any ? 0u : SM_ZERO;  // below -104 every term is +0
+      }
+    }
+  }
+  __syncthreads();
+  if (ok && wave == 0) {  // exact prefixes, in row order
+    const double v = Ls.segsum[lane];
+    double inc = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const double t = __shfl_up(inc, d);
+      if (lane >= d) inc += t;
+    }
+    const double ex = __shfl_up(inc, 1);
+    Ls.segpre[lane] = Ls.xc + (lane == 0 ? 0.0 : ex);
+  }
+  __syncthreads();
+  uint64_t* const ssum = a.ser_sum + (int64_t)row * a.ser_ld * 2;
+  uint64_t* const skeep = a.ser_e + (int64_t)row * SER_NB * (SEG / 2);
+  if (ok) {
+    // units per segment: each term's from the short exp where its error bound
+    // settles them, else queued for the correctly rounded exp (subnormal
+    // terms too: d in [-104, -87)); the settled units stay in registers until
+    // the queue is empty
+    int qn = 0;
+    uint32_t fr0[SPC], fr1[SPC];
+    if (lane < SPC) {
+      const int t = lane * NWAVE + wave;
+      Ls.R[t][0] = 0u;
+      Ls.R[t][1] = 0u;
+    }
+#pragma unroll
+    for (int j = 0; j < SPC; j++) {
+      fr0[j] = fr1[j] = 0u;
+      if (j < ns) {
+        const int t = j * NWAVE + wave;
+        const double X0 = Ls.segpre[t];
+        const int FB = f32_field((float)(X0 * (1.0 - SER_DELTA)));
+        const bool two = f32_field((float)(X0 * (1.0 + SER_DELTA))) != FB;
+        if (lane == 0) Ls.meta[t] |= (uint32_t)FB | (two ? SM_TWO : 0u);
+        const float dv[4] = {q[j].x, q[j].y, q[j].z, q[j].w};
+        uint32_t r0 = 0, r1 = 0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+          const float ef = fast_expf(dv[k]);
+          uint32_t u0, u1 = 0;
+          bool settled = fast_units(ef, FB, u0);
+          if (two) settled = fast_units(ef, FB + 1, u1) && settled;
+          const bool amb = !(dv[k] < -104.0f) && (!settled || dv[k] < -87.0f);
+          if (!amb) {
+            r0 += u0;
+            r1 += u1;
+          }
+          const uint64_t b = __ballot(amb);
+          if (b) {
+            if (qn + 64 > SER_QCAP) {
+              ser_flush(Ls, wave, qn, Ls.expt);
+              qn = 0;
+            }
+            const int pos = qn + lanes_below(b);
+            if (amb) {
+              Ls.qd[wave][pos] = dv[k];
+              Ls.qt[wave][pos] = (uint8_t)t;
+            }
+            qn += __popcll(b);
+          }
+        }
+        fr0[j] = wave_sum_u32(r0);
+        fr1[j] = wave_sum_u32(r1);
+      }
+    }
+    ser_flush(Ls, wave, qn, Ls.expt);
+    if (lane == 0) {
+#pragma unroll
+      for (int j = 0; j < SPC; j++) {
+        Ls.R[j * NWAVE + wave][0] += fr0[j];
+        Ls.R[j * NWAVE + wave][1] += fr1[j];
+      }
+    }
+  }
+  __syncthreads();
+  if (ok && tid == 0) {
+    // segments that keep their terms: nonzero ones where the exact sum may
+    // pass a power of two, or with a half-way term; one reservation of
+    // side-buffer slots for the workgroup
+    uint64_t km = 0ull;
+    for (int t = 0; t < SPC * NWAVE; t++) {
+      if (t / NWAVE >= ns) continue;
+      const uint32_t mt = Ls.meta[t];
+      const double X1 = Ls.segpre[t] + Ls.segsum[t];
+      const bool pass2 = f32_field((float)(X1 * (1.0 + SER_DELTA))) != (int)(mt & 0xFFu);
+      if (!(mt & SM_ZERO) && (pass2 || (mt & (SM_TIE0 | SM_TIE1)))) km |= 1ull << t;
+    }
+    Ls.kmask = km;
+    Ls.kbase = km ? __hip_atomic_fetch_add(&a.row_ticket[row * TSTRIDE + 2], __popcll(km), __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT)
+                  : 0;
+  }
+  __syncthreads();
+  if (ok) {
+    const uint64_t km = Ls.kmask;
+    const int kbase = Ls.kbase;
+#pragma unroll
+    for (int j = 0; j < SPC; j++) {
+      const int t = j * NWAVE + wave;
+      const int idx = kbase + __popcll(km & ((1ull << t) - 1ull));
+      if (j < ns && ((km >> t) & 1ull) && idx < SER_NB) {  // a kept segment: its terms correctly rounded
+        const float4 e = cr_exp4(make_float4(q[j].x, q[j].y, q[j].z, q[j].w), Ls.expt);
+        uint64_t* const dst = skeep + (int64_t)idx * (SEG / 2) + 2 * lane;
+        st_agent(dst, (uint64_t)__float_as_uint(e.x) | ((uint64_t)__float_as_uint(e.y) << 32));
+        st_agent(dst + 1, (uint64_t)__float_as_uint(e.z) | ((uint64_t)__float_as_uint(e.w) << 32));
+      }
+      if (j < ns && lane == 0) {
+        const int g = (s0 + j) * NWAVE + wave;  // the segment's place in the row
+        const int idx = kbase + __popcll(km & ((1ull << t) - 1ull));
+        const uint32_t kept = ((km >> t) & 1ull) && idx < SER_NB ? (uint32_t)idx + 1 : 0u;
+        st_agent(&ssum[2 * g], (uint64_t)Ls.R[t][0] | ((uint64_t)Ls.R[t][1] << 32));
+        st_agent(&ssum[2 * g + 1], (uint64_t)(Ls.meta[t] | (kept << 16)) << 32);
+      }
+    }
+  }
+  // hand-off, as in sample_kernel; slot 2 of the row's ticket line counts kept segments
+  drain();
+  __syncthreads();
+  if (tid == 0) {
+    const int t = __hip_atomic_fetch_add(&a.row_ticket[row * TSTRIDE], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    Ls.last = (t == nc - 1) ? 1 : 0;
+    if (t == nc - 1) {
+      Ls.nb = ld_agent(&a.row_ticket[row * TSTRIDE + 2]);
+      st_agent(&a.row_ticket[row * TSTRIDE], 0);
+      st_agent(&a.row_ticket[row * TSTRIDE + 2], 0);
+    }
+  }
+  __syncthreads();
+  if (!Ls.last) return;
+
+  float S_ser = -1.0f;
+  if (ok) {
+    const int nseg = a.nslots * NWAVE;
+    const int nbl = min(min(Ls.nb, SER_NB), SER_LDS);
+    for (int i = tid; i < nbl * (SEG / 2); i += BLOCK)
+      reinterpret_cast<uint64_t*>(&St.w.ev[0][0])[i] = ld_agent(&skeep[i]);
+    uint32_t sb = 0;  // the running sum's bits, from +0
+#pragma unroll 1
+    for (int w0 = 0; w0 < nseg; w0 += SER_WIN) {
+      const int wn = min(SER_WIN, nseg - w0);
+      for (int i = tid; i < 2 * wn; i += BLOCK) (&St.w.sum[0][0])[i] = ld_agent(&ssum[2 * (int64_t)w0 + i]);
+      __syncthreads();
+      if (wave == 0) sb = ser_walk<HAS_MASK, HAS_CTL>(a, cfg, row, sb, St.w.sum, w0, wn, St.w.ev, nbl, skeep, m_s, Ls.expt);
+      __syncthreads();
+    }
+    S_ser = __uint_as_float(sb);
+  }
+  const bool big_row = cfg.big && !cfg.bad;
+  if (wave != 0 && !big_row) return;
+  if (wave == 0) finalize_row<HAS_MASK, false, HAS_CTL>(a, cfg, row, rowrec, nsp, nsub, rowp, mrow, St.tl.fin, S_ser);
+  if (big_row) big_finalize<HAS_MASK, HAS_CTL>(a, cfg, row, rowp, mrow, St.tl);
   if (wave == 0 && a.span > 0) verify_walk(a, row);
 }
 
@@ -2988,7 +3638,9 @@ constexpr int64_t NA_OFF_TICKET = na_up(NA_OFF_CTLCHUNK + (NA_ROWS * (NA_CHUNKS 
 constexpr int64_t NA_TICKETS = NA_ROWS * TSTRIDE;  // ints
 constexpr int64_t NA_OFF_SEQ = na_up(NA_OFF_TICKET + NA_TICKETS / 2);
 constexpr int64_t NA_OFF_STATUS = na_up(NA_OFF_SEQ + NA_TICKETS / 2);
-constexpr int64_t NA_WORDS = na_up(NA_OFF_STATUS + NA_ROWS / 2);
+constexpr int64_t NA_OFF_SERSUM = na_up(NA_OFF_STATUS + NA_ROWS / 2);
+constexpr int64_t NA_OFF_SERE = na_up(NA_OFF_SERSUM + NA_ROWS * NA_CHUNKS * SPC * NWAVE * 2);
+constexpr int64_t NA_WORDS = na_up(NA_OFF_SERE + NA_ROWS * SER_NB * (SEG / 2));
 static_assert(sizeof(CtlRow) % 8 == 0, "CtlRow packs into u64 words");
 static_assert(NA_WORDS * 8 == XS_NOALLOC_BYTES, "XS_NOALLOC_BYTES states the array's size");
 
@@ -3016,6 +3668,8 @@ struct xs_context {
   int32_t* row_ticket;  // [max_rows * TSTRIDE] arrival tickets, zero between calls
   int32_t* seq_ticket;  // [max_rows * TSTRIDE]
   uint64_t* big;        // [max_rows, 2, vocab] whole-row sort buffers (k_max > XS_K_MAX), or null
+  uint64_t* ser_sum;    // [max_rows, max_chunks * SPC * NWAVE, 2] serial_kernel's segment summaries
+  uint64_t* ser_e;      // [max_rows, SER_NB, SEG / 2] its kept terms
 };
 
 namespace {
@@ -3040,11 +3694,13 @@ void launch2(xs_context* ctx, xs::Args& a, int64_t rows, dim3 g1, const int32_t*
     hipLaunchKernelGGL((xs::sample_kernel<M, S, C, false>), g1, dim3(xs::BLOCK), 0, ctx->stream, a,
                        xs::RowOrder<false>{});
   }
+  if ((M || C) && a.serial) hipLaunchKernelGGL((xs::serial_kernel<M, C>), g1, dim3(xs::BLOCK), 0, ctx->stream, a);
 }
 
 // order: null, or a host permutation of the rows (checked by the caller,
-// rows <= XS_ORDER_MAX)
-int launch(xs_context* ctx, xs::Args& a, int64_t rows, int span, bool mask, bool lse,
+// rows <= XS_ORDER_MAX).  serial: the call can observe the serial denominator
+// of its controlled rows at top_p >= 1 (serial_kernel then finalizes them).
+int launch(xs_context* ctx, xs::Args& a, int64_t rows, int span, bool mask, bool lse, bool serial,
            const int32_t* order = nullptr) {
   const bool ctl = a.controls != nullptr;
   const int64_t grid = rows * (int64_t)a.n_chunks;
@@ -3059,6 +3715,10 @@ int launch(xs_context* ctx, xs::Args& a, int64_t rows, int span, bool mask, bool
   a.k_max = ctx->k_max;
   a.big = ctx->big;
   a.big_ld = ctx->vocab;
+  a.serial = (serial && (mask || ctl)) ? 1 : 0;
+  a.ser_sum = ctx->ser_sum;
+  a.ser_e = ctx->ser_e;
+  a.ser_ld = (int64_t)ctx->max_chunks * xs::SPC * xs::NWAVE;
   const dim3 g1((unsigned)grid);
   if (ctl && mask) launch2<true, false, true>(ctx, a, rows, g1, order);
   else if (ctl) launch2<false, false, true>(ctx, a, rows, g1, order);
@@ -3101,6 +3761,9 @@ int xs_create(int device, int64_t max_rows, int64_t vocab, int32_t k_max, xs_con
   ok = ok && hipMalloc((void**)&c->seq_ticket, tbytes) == hipSuccess;
   ok = ok && hipMemset(c->row_ticket, 0, tbytes) == hipSuccess;
   ok = ok && hipMemset(c->seq_ticket, 0, tbytes) == hipSuccess;
+  const int64_t nseg = (int64_t)mc * xs::SPC * xs::NWAVE;
+  ok = ok && hipMalloc((void**)&c->ser_sum, max_rows * nseg * 2 * sizeof(uint64_t)) == hipSuccess;
+  ok = ok && hipMalloc((void**)&c->ser_e, max_rows * xs::SER_NB * (xs::SEG / 2) * sizeof(uint64_t)) == hipSuccess;
   if (k_max > XS_K_MAX)  // top_k past the streaming selection: the whole-row path's buffers
     ok = ok && hipMalloc((void**)&c->big, (size_t)max_rows * 2 * vocab * sizeof(uint64_t)) == hipSuccess;
   ok = ok && hipDeviceSynchronize() == hipSuccess;
@@ -3124,6 +3787,8 @@ int xs_destroy(xs_context* c) {
   (void)hipFree(c->row_ticket);
   (void)hipFree(c->seq_ticket);
   if (c->big) (void)hipFree(c->big);
+  (void)hipFree(c->ser_sum);
+  (void)hipFree(c->ser_e);
   free(c);
   return XS_OK;
 }
@@ -3193,7 +3858,12 @@ int sample_impl(xs_context* ctx, const xs_sample_args* in, bool clear_tickets) {
     hipLaunchKernelGGL(xs::zero_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, ctx->stream,
                        ctx->row_ticket, n);
   }
-  return launch(ctx, a, in->rows, 1, in->allowed != nullptr, lse, in->row_order);
+  // the serial denominator shows in the candidate list and weights and in
+  // soft_sum; a call that takes only tokens draws with the exact sum, whose
+  // token differs from the serial one's only where u falls within rounding
+  // of a cumulative-weight boundary
+  const bool serial = in->cand_id || in->cand_w || in->soft_sum;
+  return launch(ctx, a, in->rows, 1, in->allowed != nullptr, lse, serial, in->row_order);
 }
 }  // namespace
 
@@ -3238,6 +3908,8 @@ int xs_sample_noalloc(const xs_sample_args* in, void* hip_stream) {
   c.row_ticket = reinterpret_cast<int32_t*>(base + xs::NA_OFF_TICKET);
   c.seq_ticket = reinterpret_cast<int32_t*>(base + xs::NA_OFF_SEQ);
   c.row_status = reinterpret_cast<int32_t*>(base + xs::NA_OFF_STATUS);
+  c.ser_sum = base + xs::NA_OFF_SERSUM;
+  c.ser_e = base + xs::NA_OFF_SERE;
   return sample_impl(&c, in, true);
 }
 
@@ -3284,7 +3956,7 @@ int xs_verify(xs_context* ctx, const xs_verify_args* in) {
   a.n_chunks = chunks_for(in->enc);
   a.nslots = (int32_t)slots_for(in->enc);
   a.rec = ctx->rec;
-  return launch(ctx, a, rows, (int)in->span, in->allowed != nullptr, false);
+  return launch(ctx, a, rows, (int)in->span, in->allowed != nullptr, false, true);  // tokens are all it returns
 }
 
 int xs_argmax_probs(xs_context* ctx, const xs_argmax_args* in) {
@@ -3305,7 +3977,7 @@ int xs_argmax_probs(xs_context* ctx, const xs_argmax_args* in) {
   a.n_chunks = chunks_for(in->width);
   a.nslots = (int32_t)slots_for(in->width);
   a.rec = ctx->rec;
-  return launch(ctx, a, in->rows, 1, false, true);
+  return launch(ctx, a, in->rows, 1, false, true, false);
 }
 
 int xs_test_exp(const float* x, float* y, int64_t n, void* s) {

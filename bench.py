@@ -76,7 +76,7 @@ def cpu_baseline(name: str, wl, seconds: float, threads: int) -> dict:
     o.build()
     o.set_exp_mode(1)
     rows, V = wl.logits.shape
-    mask = wl.mask if name == "c3" else None
+    mask = wl.mask if name in ("c3", "c3p1") else None
     done, reps = 0, 0
     t0 = time.perf_counter()
     while True:
@@ -97,7 +97,7 @@ def cpu_baseline(name: str, wl, seconds: float, threads: int) -> dict:
     dt = time.perf_counter() - t0
     o.set_exp_mode(0)
     del np
-    extra = {"c3": " + allow-masks", "c4": " + the accept_drafts walks",
+    extra = {"c3": " + allow-masks", "c3p1": " + allow-masks", "c4": " + the accept_drafts walks",
              "c5": " + held_row (serial)"}.get(name, "")
     return {"value": round(done / dt, 2), "unit": "rows/s", "cores": threads, "kind": "port",
             "sample": f"{reps} passes over the {rows} rows of {name.upper()} (V=248,320){extra}, "
@@ -139,8 +139,10 @@ def setup(name, nbuf, dev, torch, workloads, xsm, _lib, lib) -> dict:
 
     log(f"generating the {name} workload")
     wl = {"c1": workloads.c1_single, "c1g": lambda: workloads.c1_single(greedy=True),
-          "c2": workloads.c2_batch, "c3": workloads.c3_masked, "c4": workloads.c4_verify,
-          "c5": workloads.c5_heterogeneous}[name]()
+          "c2": workloads.c2_batch, "c3": workloads.c3_masked, "c3p1": workloads.c3_masked,
+          "c4": workloads.c4_verify, "c5": workloads.c5_heterogeneous}[name]()
+    if name == "c3p1":  # C3 at top_p = 1: the serial denominator reaches the weights
+        wl.top_p = np.ones_like(wl.top_p)
     if name in ("c1", "c1g"):  # one 1 MB row: rotate enough copies to leave the Infinity Cache
         nbuf = max(nbuf, 300)
     rows, V = wl.logits.shape
@@ -177,9 +179,15 @@ def setup(name, nbuf, dev, torch, workloads, xsm, _lib, lib) -> dict:
         # a heterogeneous batch starts its costliest rows first (xs_sample's
         # row_order hint); the others run in their natural order
         order = xsm.cost_order(wl.temperature, wl.top_k) if name == "c5" else None
-        if name == "c3":
+        if name in ("c3", "c3p1"):
             extra["mask"] = torch.as_tensor(wl.mask.view(np.int32)).to(dev)
             row_bytes += 4 * wl.mask.shape[1]
+        if name == "c3p1":  # the top-20 candidate list and the denominator
+            for o in outs:
+                o.cand_id = torch.empty((rows, 20), **i32)
+                o.cand_w = torch.empty((rows, 20), dtype=torch.float32, device=dev)
+                o.n_cand = torch.empty(rows, **i32)
+                o.soft_sum = torch.empty(rows, dtype=torch.float32, device=dev)
         if name == "c5":
             for o in outs:
                 o.row_max = torch.empty(rows, dtype=torch.float32, device=dev)
@@ -196,6 +204,10 @@ def setup(name, nbuf, dev, torch, workloads, xsm, _lib, lib) -> dict:
             if "mask" in extra:
                 a.allowed = extra["mask"].data_ptr()
                 a.allowed_words = a.allowed_ld = wl.mask.shape[1]
+            if outs[i].cand_id is not None:
+                a.cand_id, a.cand_w = outs[i].cand_id.data_ptr(), outs[i].cand_w.data_ptr()
+                a.n_cand, a.cand_ld = outs[i].n_cand.data_ptr(), 20
+                a.soft_sum = outs[i].soft_sum.data_ptr()
             if outs[i].top_id is not None:
                 a.row_max, a.row_lse = outs[i].row_max.data_ptr(), outs[i].row_lse.data_ptr()
                 a.n_top, a.top_ld = wl.n_top, wl.n_top
@@ -218,7 +230,7 @@ def setup(name, nbuf, dev, torch, workloads, xsm, _lib, lib) -> dict:
              token_of=token_of, status_of=status_of, bufs=bufs, keep=(params, u, argv), nbuf=nbuf)
     if name == "c4":
         S["keep"] += (drafts,)
-    elif name == "c3":
+    elif name in ("c3", "c3p1"):
         S["keep"] += (extra["mask"],)
     elif name == "c5":
         S["keep"] += (order,)  # the launches read it on the host at each call
@@ -234,6 +246,8 @@ WORKLOAD_TEXT = {
           "one uniform per row",
     "c3": "C3 grammar-constrained sampling: 32 rows x V=248,320 fp32 + packed u32 allow-masks "
           "(1% / 10% / 50% dense, one one-hot), T 1.0 / top_k 20 / top_p 0.95",
+    "c3p1": "C3 at top_p 1.0 with the top-20 candidate list and the softmax denominator: the "
+            "controlled rows' serial f32 denominator (sample_kernel + serial_kernel)",
     "c4": "C4 speculative verify: 16 sequences x 16 positions x V=248,320 fp32, 15 drafts each, "
           "top_k 20 / top_p 0.95 / T 1.0, accept_drafts on the device",
     "c5": "C5 heterogeneous batch: 256 rows x V=248,320 fp32 Student-t(3)x2, per-row T/k/p, "
@@ -254,7 +268,7 @@ def main() -> int:
                     help="rows the CPU baseline samples at once (one per thread); 0 = the "
                          "host cores of this process's share (at most 16)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES")
-    ap.add_argument("--workload", choices=["c1", "c1g", "c2", "c3", "c4", "c5"], default="c2",
+    ap.add_argument("--workload", choices=["c1", "c1g", "c2", "c3", "c3p1", "c4", "c5"], default="c2",
                     help="c2 (default) is the headline configuration; c1/c1g one row (latency)")
     args = ap.parse_args()
     if args.gpus != 1:

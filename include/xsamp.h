@@ -55,7 +55,8 @@ extern "C" {
  *   XS_ROW_ZERO_WEIGHT WeightedIndex saw no probability mass (:238-240)
  *   XS_ROW_NARROW      logit row narrower than the encodable bound (:196-200)
  *   XS_ROW_BAD_PARAM   min(top_k, enc) larger than the context's k_max, or a
- *                      control list past XS_CTL_MAX entries (no reference
+ *                      control list past the context's ctl_max (XS_CTL_MAX by
+ *                      default, xs_create_ex) entries (no reference
  *                      counterpart: the reference has no such limits)
  *   XS_ROW_INTERNAL    reserved; this build never reports it               */
 #define XS_ROW_OK 0
@@ -96,6 +97,16 @@ typedef struct {
  * path's buffers, 16 bytes per row and id (32 MB for 8 rows of 248,320).
  * Allocates the device workspace once; calls allocate nothing afterwards. */
 int xs_create(int device, int64_t max_rows, int64_t vocab, int32_t k_max, xs_context** out);
+
+/* xs_create with room for control lists longer than XS_CTL_MAX: a row of a
+ * call may then list up to ctl_max bans plus biases (SampleControl's lists are
+ * unbounded slices, sampler.rs:85-121; a context is sized for the longest a
+ * caller will pass, as for k_max).  ctl_max <= XS_CTL_MAX is xs_create;
+ * above it the context holds 24 bytes per row and list entry (patch list and
+ * sort buffers: 48 MB for 256 rows of 8,192).  Lists up to XS_CTL_MAX are
+ * sorted in LDS, longer ones by a radix sort in those buffers. */
+int xs_create_ex(int device, int64_t max_rows, int64_t vocab, int32_t k_max, int32_t ctl_max,
+                 xs_context** out);
 int xs_destroy(xs_context* ctx);
 /* Bind the hipStream_t the context's kernels run on (NULL = the null stream). */
 int xs_set_stream(xs_context* ctx, void* hip_stream);
@@ -115,8 +126,8 @@ int xs_set_stream(xs_context* ctx, void* hip_stream);
  * id lists live in two device pools shared by a call's rows: banned ids are
  * ctl_ids[ban_off .. ban_off + n_ban), bias entry i is (ctl_ids[bias_off + i],
  * ctl_delta[bias_off + i]).  A row may list at most XS_CTL_MAX bans and
- * biases together; more (or a negative count or offset) is
- * XS_ROW_BAD_PARAM.  A row whose lists are empty and whose has_pull and
+ * biases together (the context's ctl_max for xs_create_ex); more (or a
+ * negative count or offset) is XS_ROW_BAD_PARAM.  A row whose lists are empty and whose has_pull and
  * has_force are 0 is uncontrolled. */
 #define XS_CTL_MAX 2048
 typedef struct {

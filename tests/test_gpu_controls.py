@@ -231,3 +231,60 @@ def test_controls_on_flat_rows_with_an_allow_mask(ctx, oracle):
     d = run_sample(ctx, x, T, K, P, U, mask=mask, ctls=ctls, cand_k=64)
     assert (d["status"] == 0).all(), d["status"]
     check_rows(oracle, x, T, K, P, U, d, mask=mask, ctls=ctls, margins=False, label="flat controls + mask")
+
+
+def test_control_lists_longer_than_xs_ctl_max(oracle):
+    """SampleControl's lists are unbounded in the reference (sampler.rs:85-121):
+    a context made with xs_create_ex(ctl_max) takes rows of up to ctl_max bans
+    plus biases, sorted by id in memory past XS_CTL_MAX.  Lists of 2,049 to
+    20,000 entries with repeated ids (bans of biased ids, several biases of one
+    id, applied in list order), with and without a mask, greedy and
+    stochastic, at top_p 0.9 and 1.0, against the oracle; a list one past
+    ctl_max is XS_ROW_BAD_PARAM."""
+    from xwen_amd import sampler as xsm
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    cap = 20_000
+    c = xsm.Context(max_rows=8, vocab=V, ctl_max=cap)
+    c.bind_current_stream()
+    try:
+        x, spikes, rng = _rows(8, 4747)
+        ctls = []
+        for r in range(7):
+            nb = int(rng.integers(1000, 2000)) if r == 0 else int(rng.integers(1000, 9000))
+            nbias = 2049 - nb if r == 0 else int(rng.integers(1000, cap - nb))  # row 0: exactly 2,049
+            banned = [int(i) for i in rng.integers(0, V + 100, nb)]  # some past the vocabulary
+            if r % 2:
+                banned.append(int(spikes[r][0]))                      # the top token
+            ids = rng.integers(0, V, nbias)
+            ids[: nbias // 4] = spikes[r][rng.integers(0, 6, nbias // 4)]  # many biases of few ids
+            bias = [(int(i), float(rng.normal(0, 1.5))) for i in ids]
+            pull = (int(spikes[r][3]), 0.5) if r % 3 == 0 else None
+            ctls.append(xsm.SampleControl(banned=banned[: cap - len(bias)], bias=bias, pull=pull))
+        ctls.append(xsm.SampleControl(banned=list(range(cap + 1))))  # one past the context's ctl_max
+        T = [1.0, 0.7, 0.0, 1.3, 1.0, 0.8, 1.0, 1.0]
+        K = [20, 50, 1, 20, 100, 40, 20, 20]
+        P = [0.9, 1.0, 1.0, 0.95, 1.0, 0.9, 1.0, 0.9]
+        U = rng.random(8).astype(np.float32)
+        assert all(len(ct.banned) + len(ct.bias) > 2048 for ct in ctls)
+        d = run_sample(c, x, T, K, P, U, ctls=ctls, cand_k=100)
+        assert d["status"][7] == _lib_bad()
+        assert (d["status"][:7] == 0).all(), d["status"]
+        check_rows(oracle, x[:7], T[:7], K[:7], P[:7], U[:7],
+                   {k: (None if v is None else v[:7]) for k, v in d.items()},
+                   ctls=ctls[:7], label="long control lists")
+        allow = rng.random((8, V)) < 0.5
+        allow[np.arange(8), spikes[:, 1]] = True
+        mask = workloads.pack_mask(allow)
+        d = run_sample(c, x, T, K, P, U, ctls=ctls, mask=mask, cand_k=100)
+        assert (d["status"][:7] == 0).all(), d["status"]
+        check_rows(oracle, x[:7], T[:7], K[:7], P[:7], U[:7],
+                   {k: (None if v is None else v[:7]) for k, v in d.items()},
+                   ctls=ctls[:7], mask=mask[:7], label="long control lists + mask")
+    finally:
+        c.close()
+
+
+def _lib_bad():
+    from xwen_amd import _lib
+    return _lib.ROW_BAD_PARAM

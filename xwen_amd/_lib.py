@@ -92,6 +92,8 @@ def load() -> C.CDLL:
     L = C.CDLL(LIB_PATH)
     L.xs_create.restype = C.c_int
     L.xs_create.argtypes = [C.c_int, _i64, _i64, _i32, C.POINTER(_vp)]
+    L.xs_create_ex.restype = C.c_int
+    L.xs_create_ex.argtypes = [C.c_int, _i64, _i64, _i32, _i32, C.POINTER(_vp)]
     L.xs_destroy.restype = C.c_int
     L.xs_destroy.argtypes = [_vp]
     L.xs_set_stream.restype = C.c_int

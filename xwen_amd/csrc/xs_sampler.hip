@@ -407,7 +407,9 @@ struct Args {
   const xs_row_control* controls;
   const uint32_t* ctl_ids;
   const float* ctl_delta;
-  uint64_t* patch;
+  uint64_t* patch;      // [rows, ctl_cap]
+  uint64_t* ctl_keys;   // [rows, 2, ctl_cap]: control_kernel's sort buffers for lists past CTL_MAX, or null
+  int32_t ctl_cap;      // the context's largest control list (bans plus biases of one row)
   CtlRow* ctl_row;
   int32_t* ctl_chunk;
   // geometry + workspace
@@ -1777,7 +1779,7 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
           }
         }
         int sc = 0;  // next patch (the list is sorted by id, as the scan runs)
-        const uint64_t* pl = HAS_CTL ? a.patch + (int64_t)row * CTL_MAX : nullptr;
+        const uint64_t* pl = HAS_CTL ? a.patch + (int64_t)row * a.ctl_cap : nullptr;
         for (int base = 0; base < enc && need > 0; base += 256) {
           const int f = base / 4 + lane;
           float4 qv = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
@@ -2208,7 +2210,7 @@ XS_DEV void big_finalize(const Args& a, const Cfg& cfg, int row, const float* ro
   const uint64_t* pl = nullptr;
   if (HAS_CTL) {
     cr = a.ctl_row[row];
-    pl = a.patch + (int64_t)row * CTL_MAX;
+    pl = a.patch + (int64_t)row * a.ctl_cap;
   }
   const bool ctl_on = HAS_CTL && cr.active;
   __syncthreads();
@@ -2501,7 +2503,7 @@ XS_DEV void seg_terms(const Args& a, const Cfg& cfg, int row, int g, float m_s, 
       const int chunk = slot / SPC;
       int pc = a.ctl_chunk[(int64_t)row * (a.n_chunks + 1) + chunk];
       const int phi = a.ctl_chunk[(int64_t)row * (a.n_chunks + 1) + chunk + 1];
-      ctl_slot(x, sb, pos, a.patch + (int64_t)row * CTL_MAX, pc, phi, cr.pull_id, cr.pull_val, cr.force_id,
+      ctl_slot(x, sb, pos, a.patch + (int64_t)row * a.ctl_cap, pc, phi, cr.pull_id, cr.pull_val, cr.force_id,
                cr.force_val);
     }
   }
@@ -2662,7 +2664,7 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
     const CtlRow cr = a.ctl_row[row];
     pc = a.ctl_chunk[(int64_t)row * (nc + 1) + chunk];
     phi = a.ctl_chunk[(int64_t)row * (nc + 1) + chunk + 1];
-    pl = a.patch + (int64_t)row * CTL_MAX;
+    pl = a.patch + (int64_t)row * a.ctl_cap;
     ctl_pull = cr.pull_id;
     ctl_pval = cr.pull_val;
     ctl_force = cr.force_id;
@@ -3241,7 +3243,7 @@ __global__ __launch_bounds__(BLOCK) void serial_kernel(Args a) {
     if (ctl_on) {
       pc = a.ctl_chunk[(int64_t)row * (nc + 1) + chunk];
       phi = a.ctl_chunk[(int64_t)row * (nc + 1) + chunk + 1];
-      pl = a.patch + (int64_t)row * CTL_MAX;
+      pl = a.patch + (int64_t)row * a.ctl_cap;
     }
 #pragma unroll
     for (int j = 0; j < SPC; j++) {
@@ -3441,8 +3443,9 @@ __global__ __launch_bounds__(BLOCK) void serial_kernel(Args a) {
 // sample_kernel overwrites exactly these elements before anything reads them.
 template <bool HAS_MASK>
 __global__ __launch_bounds__(BLOCK) void control_kernel(Args a) {
-  __shared__ uint64_t keys[CTL_MAX];  // (id << 32 | list position), sorted
-  __shared__ uint64_t pl[CTL_MAX];    // the patch list
+  __shared__ uint64_t lkeys[CTL_MAX];  // (id << 32 | list position), sorted (lists of CTL_MAX or fewer)
+  __shared__ uint64_t lpl[CTL_MAX];    // the patch list (idem)
+  __shared__ BigLds B;                 // the radix sort's counters (longer lists)
   __shared__ int s4[NWAVE];
   __shared__ float wmax[NWAVE];
   const int row = blockIdx.x, tid = threadIdx.x, lane = lane_id(), wave = wave_id();
@@ -3451,14 +3454,14 @@ __global__ __launch_bounds__(BLOCK) void control_kernel(Args a) {
   const float* rowp = a.logits + (int64_t)row * a.ld;
   const uint32_t* mrow = HAS_MASK ? a.allowed + (int64_t)row * a.allowed_ld : nullptr;
   int32_t* cb = a.ctl_chunk + (int64_t)row * (nc + 1);
-  uint64_t* patch = a.patch + (int64_t)row * CTL_MAX;
+  uint64_t* patch = a.patch + (int64_t)row * a.ctl_cap;
   auto allowed = [&](int id) __attribute__((always_inline)) {
     return !HAS_MASK || ((mrow[id >> 5] >> (id & 31)) & 1u);
   };
   const bool active = c.n_ban != 0 || c.n_bias != 0 || c.has_pull != 0 || c.has_force != 0;
   const int64_t n64 = (int64_t)c.n_ban + (int64_t)c.n_bias;
   int status = XS_ROW_OK;
-  if (c.n_ban < 0 || c.n_bias < 0 || c.ban_off < 0 || c.bias_off < 0 || n64 > CTL_MAX ||
+  if (c.n_ban < 0 || c.n_bias < 0 || c.ban_off < 0 || c.bias_off < 0 || n64 > a.ctl_cap ||
       (n64 > 0 && !a.ctl_ids) || (c.n_bias > 0 && !a.ctl_delta))
     status = XS_ROW_BAD_PARAM;
   if (!active || status != XS_ROW_OK) {
@@ -3467,41 +3470,62 @@ __global__ __launch_bounds__(BLOCK) void control_kernel(Args a) {
     return;
   }
 
-  // Sort the listed ids, each tagged with its list position (bans first).
+  // Sort the listed ids, each tagged with its list position (bans first):
+  // a list of CTL_MAX or fewer in LDS (bitonic), a longer one in the
+  // context's sort buffers (the stable LSD radix sort of the whole-row path,
+  // by ~id descending, which keeps equal ids in list order); the patch list
+  // then goes straight to the row's patch array.
   const int n = (int)n64;
-  int np2 = 1;
-  while (np2 < n) np2 <<= 1;
-  for (int i = tid; i < np2; i += BLOCK) {
-    uint64_t k = ~0ull;
-    if (i < n) {
-      const uint32_t id = i < c.n_ban ? a.ctl_ids[c.ban_off + i] : a.ctl_ids[c.bias_off + (i - c.n_ban)];
-      k = ((uint64_t)id << 32) | (uint32_t)i;
-    }
-    keys[i] = k;
-  }
-  __syncthreads();
-  for (int size = 2; size <= np2; size <<= 1) {  // bitonic, ascending
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      for (int i = tid; i < np2 / 2; i += BLOCK) {
-        const int lo = 2 * i - (i & (stride - 1)), hi = lo + stride;
-        const bool asc = (lo & size) == 0;
-        const uint64_t x = keys[lo], y = keys[hi];
-        if ((x > y) == asc) {
-          keys[lo] = y;
-          keys[hi] = x;
-        }
+  const bool lds = n <= CTL_MAX;
+  uint64_t* const gk = lds ? nullptr : a.ctl_keys + (int64_t)row * 2 * a.ctl_cap;
+  uint64_t* const pl = lds ? lpl : patch;
+  if (lds) {
+    int np2 = 1;
+    while (np2 < n) np2 <<= 1;
+    for (int i = tid; i < np2; i += BLOCK) {
+      uint64_t k = ~0ull;
+      if (i < n) {
+        const uint32_t id = i < c.n_ban ? a.ctl_ids[c.ban_off + i] : a.ctl_ids[c.bias_off + (i - c.n_ban)];
+        k = ((uint64_t)id << 32) | (uint32_t)i;
       }
-      __syncthreads();
+      lkeys[i] = k;
     }
+    __syncthreads();
+    for (int size = 2; size <= np2; size <<= 1) {  // bitonic, ascending
+      for (int stride = size >> 1; stride > 0; stride >>= 1) {
+        for (int i = tid; i < np2 / 2; i += BLOCK) {
+          const int lo = 2 * i - (i & (stride - 1)), hi = lo + stride;
+          const bool asc = (lo & size) == 0;
+          const uint64_t x = lkeys[lo], y = lkeys[hi];
+          if ((x > y) == asc) {
+            lkeys[lo] = y;
+            lkeys[hi] = x;
+          }
+        }
+        __syncthreads();
+      }
+    }
+  } else {
+    for (int i = tid; i < n; i += BLOCK) {
+      const uint32_t id = i < c.n_ban ? a.ctl_ids[c.ban_off + i] : a.ctl_ids[c.bias_off + (i - c.n_ban)];
+      gk[i] = ((uint64_t)(0xFFFFFFFFu - id) << 32) | (uint32_t)i;
+    }
+    __syncthreads();
+    radix_sort_desc(gk, gk + a.ctl_cap, n, B);  // (every pass ends in a barrier)
   }
+  auto keys = [&](int i) __attribute__((always_inline)) -> uint64_t {  // (id << 32 | list position)
+    if (lds) return lkeys[i];
+    const uint64_t k = gk[i];
+    return ((uint64_t)(0xFFFFFFFFu - (uint32_t)(k >> 32)) << 32) | (uint32_t)k;
+  };
 
   // One patch per distinct id < enc: the run of its entries holds its bans
   // (lower positions) and then its biases in list order.
   const int seg = (n + BLOCK - 1) / BLOCK;
   const int b0 = min(n, tid * seg), b1 = min(n, b0 + seg);
   auto starts = [&](int i) __attribute__((always_inline)) {
-    const uint32_t id = (uint32_t)(keys[i] >> 32);
-    return id < (uint32_t)enc && (i == 0 || (uint32_t)(keys[i - 1] >> 32) != id);
+    const uint32_t id = (uint32_t)(keys(i) >> 32);
+    return id < (uint32_t)enc && (i == 0 || (uint32_t)(keys(i - 1) >> 32) != id);
   };
   int cnt = 0;
   for (int i = b0; i < b1; i++) cnt += starts(i) ? 1 : 0;
@@ -3509,10 +3533,10 @@ __global__ __launch_bounds__(BLOCK) void control_kernel(Args a) {
   int p = block_excl_scan(cnt, s4, &total);
   for (int i = b0; i < b1; i++) {
     if (!starts(i)) continue;
-    const uint32_t id = (uint32_t)(keys[i] >> 32);
+    const uint32_t id = (uint32_t)(keys(i) >> 32);
     float x = allowed((int)id) ? rowp[id] : -INFINITY;
-    for (int j = i; j < n && (uint32_t)(keys[j] >> 32) == id; j++) {
-      const int o = (int)(uint32_t)keys[j];
+    for (int j = i; j < n && (uint32_t)(keys(j) >> 32) == id; j++) {
+      const int o = (int)(uint32_t)keys(j);
       if (o < c.n_ban) x = -INFINITY;
       else x = x + a.ctl_delta[c.bias_off + (o - c.n_ban)];
     }
@@ -3532,7 +3556,8 @@ __global__ __launch_bounds__(BLOCK) void control_kernel(Args a) {
     const int q = lower((uint32_t)id);
     return q < total && (uint32_t)(pl[q] >> 32) == (uint32_t)id;
   };
-  for (int i = tid; i < total; i += BLOCK) patch[i] = pl[i];
+  if (lds)
+    for (int i = tid; i < total; i += BLOCK) patch[i] = pl[i];
   for (int i = tid; i <= nc; i += BLOCK) cb[i] = (i == nc) ? total : lower((uint32_t)(i * SPC * SLOT));
 
   // pull: the max M over the row after the bans and biases (f32::max folds
@@ -3662,7 +3687,9 @@ struct xs_context {
   int32_t max_chunks;
   uint64_t* rec;
   int32_t* row_status;  // [max_rows] statuses of calls whose caller takes none (xs_argmax_probs)
-  uint64_t* ctl_patch;  // [max_rows, CTL_MAX] patch lists of controlled calls
+  uint64_t* ctl_patch;  // [max_rows, ctl_cap] patch lists of controlled calls
+  uint64_t* ctl_keys;   // [max_rows, 2, ctl_cap] sort buffers for lists past CTL_MAX (ctl_cap > CTL_MAX), or null
+  int32_t ctl_cap;      // the largest control list (bans plus biases) of one row
   xs::CtlRow* ctl_row;  // [max_rows]
   int32_t* ctl_chunk;   // [max_rows, max_chunks + 1]
   int32_t* row_ticket;  // [max_rows * TSTRIDE] arrival tickets, zero between calls
@@ -3708,6 +3735,8 @@ int launch(xs_context* ctx, xs::Args& a, int64_t rows, int span, bool mask, bool
   if (grid > 0x7FFFFFFF || span < 1) return XS_ERR_CAPACITY;
   if ((mask || ctl) && lse) return XS_ERR_ARG;
   a.patch = ctx->ctl_patch;
+  a.ctl_keys = ctx->ctl_keys;
+  a.ctl_cap = ctx->ctl_cap;
   a.ctl_row = ctx->ctl_row;
   a.ctl_chunk = ctx->ctl_chunk;
   a.row_ticket = ctx->row_ticket;
@@ -3735,7 +3764,12 @@ extern "C" {
 const char* xs_version(void) { return "xsamp 0.1 gfx950"; }
 
 int xs_create(int device, int64_t max_rows, int64_t vocab, int32_t k_max, xs_context** out) {
-  if (!out || max_rows < 1 || vocab < 1 || k_max < 0) return XS_ERR_ARG;
+  return xs_create_ex(device, max_rows, vocab, k_max, XS_CTL_MAX, out);
+}
+
+int xs_create_ex(int device, int64_t max_rows, int64_t vocab, int32_t k_max, int32_t ctl_max,
+                 xs_context** out) {
+  if (!out || max_rows < 1 || vocab < 1 || k_max < 0 || ctl_max < 0) return XS_ERR_ARG;
   *out = nullptr;
   if (hipSetDevice(device) != hipSuccess) return XS_ERR_HIP;
   const int32_t mc = chunks_for(vocab);
@@ -3748,12 +3782,15 @@ int xs_create(int device, int64_t max_rows, int64_t vocab, int32_t k_max, xs_con
   c->vocab = vocab;
   c->k_max = k_max;
   c->max_chunks = mc;
+  c->ctl_cap = ctl_max > xs::CTL_MAX ? ctl_max : xs::CTL_MAX;
   const int64_t nsp = ((int64_t)mc * xs::NWAVE + 63) / 64 * 64;  // sub-records per row, padded
   const int64_t units = max_rows * nsp;
   bool ok = hipMalloc((void**)&c->rec, units * xs::SRECW * sizeof(uint64_t)) == hipSuccess;
   ok = ok && hipMemset(c->rec, 0, units * xs::SRECW * sizeof(uint64_t)) == hipSuccess;
   ok = ok && hipMalloc((void**)&c->row_status, max_rows * sizeof(int32_t)) == hipSuccess;
-  ok = ok && hipMalloc((void**)&c->ctl_patch, max_rows * xs::CTL_MAX * sizeof(uint64_t)) == hipSuccess;
+  ok = ok && hipMalloc((void**)&c->ctl_patch, max_rows * c->ctl_cap * sizeof(uint64_t)) == hipSuccess;
+  if (c->ctl_cap > xs::CTL_MAX)  // lists past CTL_MAX: control_kernel sorts them in memory
+    ok = ok && hipMalloc((void**)&c->ctl_keys, (size_t)max_rows * 2 * c->ctl_cap * sizeof(uint64_t)) == hipSuccess;
   ok = ok && hipMalloc((void**)&c->ctl_row, max_rows * sizeof(xs::CtlRow)) == hipSuccess;
   ok = ok && hipMalloc((void**)&c->ctl_chunk, max_rows * (mc + 1) * sizeof(int32_t)) == hipSuccess;
   const size_t tbytes = (size_t)max_rows * xs::TSTRIDE * sizeof(int32_t);
@@ -3782,6 +3819,7 @@ int xs_destroy(xs_context* c) {
   (void)hipFree(c->rec);
   (void)hipFree(c->row_status);
   (void)hipFree(c->ctl_patch);
+  if (c->ctl_keys) (void)hipFree(c->ctl_keys);
   (void)hipFree(c->ctl_row);
   (void)hipFree(c->ctl_chunk);
   (void)hipFree(c->row_ticket);
@@ -3903,6 +3941,7 @@ int xs_sample_noalloc(const xs_sample_args* in, void* hip_stream) {
   c.max_chunks = (int32_t)xs::NA_CHUNKS;
   c.rec = base + xs::NA_OFF_REC;
   c.ctl_patch = base + xs::NA_OFF_PATCH;
+  c.ctl_cap = xs::CTL_MAX;
   c.ctl_row = reinterpret_cast<xs::CtlRow*>(base + xs::NA_OFF_CTLROW);
   c.ctl_chunk = reinterpret_cast<int32_t*>(base + xs::NA_OFF_CTLCHUNK);
   c.row_ticket = reinterpret_cast<int32_t*>(base + xs::NA_OFF_TICKET);

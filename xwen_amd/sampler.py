@@ -47,7 +47,8 @@ ROW_STATUS_NAMES = {
     _lib.ROW_ZERO_WEIGHT: "no candidate carries any probability mass after top-k/top-p filtering",
     _lib.ROW_NARROW: "logit row is narrower than the encodable ids the sampler draws over",
     _lib.ROW_BAD_PARAM: "top_k exceeds the sampler context's k_max (create the context with a "
-                        "larger k_max), or a control list holds more than XS_CTL_MAX entries",
+                        "larger k_max), or a control list holds more entries than the context's "
+                        "ctl_max (XS_CTL_MAX unless the context was created with a larger one)",
     _lib.ROW_INTERNAL: "internal error (reserved)",
 }
 
@@ -154,17 +155,20 @@ def _ptr(t):
 
 
 class Context:
-    """An xs_context: the device workspace for up to max_rows rows of `vocab` ids."""
+    """An xs_context: the device workspace for up to max_rows rows of `vocab` ids,
+    top_k up to k_max and control lists (bans plus biases of a row) up to ctl_max."""
 
-    def __init__(self, max_rows: int, vocab: int, k_max: int = _lib.K_MAX, device: int = 0):
+    def __init__(self, max_rows: int, vocab: int, k_max: int = _lib.K_MAX, device: int = 0,
+                 ctl_max: int = _lib.CTL_MAX):
         self.lib = _lib.load()
         torch = _torch()
         self.device = device
         torch.cuda.set_device(device)
         h = C.c_void_p()
-        _lib.check(self.lib.xs_create(device, max_rows, vocab, k_max, C.byref(h)), "xs_create")
+        _lib.check(self.lib.xs_create_ex(device, max_rows, vocab, k_max, ctl_max, C.byref(h)),
+                   "xs_create_ex")
         self.h = h
-        self.max_rows, self.vocab, self.k_max = max_rows, vocab, k_max
+        self.max_rows, self.vocab, self.k_max, self.ctl_max = max_rows, vocab, k_max, ctl_max
 
     def bind_current_stream(self):
         torch = _torch()

@@ -422,6 +422,9 @@ struct Args {
   // the serial denominator (serial_kernel): set on calls with a mask or
   // controls, whose rows at top_p >= 1 serial_kernel finalizes
   int32_t serial;
+  // split launch: sample_kernel's workgroups publish and exit; finalize_kernel
+  // (one workgroup per row) finalizes every row afterwards
+  int32_t split;
   uint64_t* ser_sum;  // [rows, ser_ld, 2]: segment summaries
   uint64_t* ser_e;    // [rows, SER_NB, SEG / 2]: kept segments' terms, two f32 per word
   int64_t ser_ld;     // segments per row of ser_sum
@@ -3070,7 +3073,10 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
 
   // Hand-off: every wave's stores acknowledged, the workgroup takes the row's
   // arrival ticket; the last of the row's workgroups resets it for the next
-  // call and its first wave finalizes the row.
+  // call and its first wave finalizes the row.  A split launch leaves all of
+  // that to finalize_kernel: the workgroup's slot goes to the next chunk at
+  // once, its stores completing on their own.
+  if (a.split) return;
   drain();
   __syncthreads();
   if (tid == 0) {
@@ -3089,6 +3095,37 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
   // holds is drawn by the whole workgroup (big_finalize); a verify block's
   // rows then walk accept_drafts (verify_walk).
   const bool big_row = cfg.big && !cfg.bad;  // uniform in the workgroup
+  if (wave != 0 && !big_row) return;
+  if (wave == 0) {
+    finalize_row<HAS_MASK, WANT_LSE, HAS_CTL>(a, cfg, row, rowrec, nsp, nc * NWAVE, rowp, mrow, Tl.fin);
+    if (held) held_fold<1>(a, row, rowp, rowrec, nsp, nc * NWAVE, Tl.fin);
+  }
+  if (big_row) big_finalize<HAS_MASK, HAS_CTL>(a, cfg, row, rowp, mrow, Tl);
+  if (wave == 0 && a.span > 0) verify_walk(a, row);
+}
+
+// ---------------------------------------------------------------------------
+// finalize_kernel: the rows of a split launch, one workgroup per row, after
+// sample_kernel published every chunk (the launch boundary orders the
+// sub-records before these loads).  The same finalization as sample_kernel's
+// last workgroup; it also clears held_row's running max key for the next
+// call.  Batches larger than the workgroups the GPU holds at once take this
+// path: their streaming workgroups then free their slots as soon as they
+// have published, instead of waiting for the hand-off or a finalizer.
+template <bool HAS_MASK, bool WANT_LSE, bool HAS_CTL>
+__global__ __launch_bounds__(BLOCK) void finalize_kernel(Args a) {
+  __shared__ TailLds Tl;
+  const int row = blockIdx.x, wave = wave_id();
+  const int nc = a.n_chunks;
+  const Cfg cfg = a.greedy_all ? greedy_cfg() : make_cfg(a.params[row], a.enc, a.n_top, a.k_max);
+  if (threadIdx.x == 0) st_agent(&a.row_ticket[row * TSTRIDE + 1], 0);  // held_row's running max key
+  if (a.serial && serial_row<HAS_MASK, HAS_CTL>(a, cfg, row)) return;  // serial_kernel finalizes it
+  const float* rowp = a.logits + (int64_t)row * a.ld;
+  const uint32_t* mrow = HAS_MASK ? a.allowed + (int64_t)row * a.allowed_ld : nullptr;
+  const int nsp = ((nc * NWAVE + 63) >> 6) << 6;
+  const uint64_t* const rowrec = a.rec + (int64_t)row * SRECW * nsp;
+  const bool held = WANT_LSE && (a.row_lse != nullptr || a.n_top > 0);
+  const bool big_row = cfg.big && !cfg.bad;
   if (wave != 0 && !big_row) return;
   if (wave == 0) {
     finalize_row<HAS_MASK, WANT_LSE, HAS_CTL>(a, cfg, row, rowrec, nsp, nc * NWAVE, rowp, mrow, Tl.fin);
@@ -3685,6 +3722,7 @@ struct xs_context {
   int64_t max_rows, vocab;
   int32_t k_max;
   int32_t max_chunks;
+  int32_t n_cu;         // compute units of the device
   uint64_t* rec;
   int32_t* row_status;  // [max_rows] statuses of calls whose caller takes none (xs_argmax_probs)
   uint64_t* ctl_patch;  // [max_rows, ctl_cap] patch lists of controlled calls
@@ -3708,10 +3746,16 @@ static_assert(xs_host::SLOT == xs::SLOT && xs_host::SPC == xs::SPC, "the host ch
 xs_host_limits limits_of(const xs_context* ctx) { return xs_host_limits{ctx->max_rows, ctx->vocab, ctx->max_chunks}; }
 
 // One sample_kernel launch over rows x n_chunks workgroups (it finalizes the
-// rows itself); a call with sparse controls runs control_kernel (one
-// workgroup per row) first.
+// rows itself), or, for a large batch, sample_kernel then finalize_kernel; a
+// call with sparse controls runs control_kernel (one workgroup per row) first,
+// and one that can observe the serial denominator serial_kernel last.
 template <bool M, bool S, bool C>
 void launch2(xs_context* ctx, xs::Args& a, int64_t rows, dim3 g1, const int32_t* order) {
+  // More workgroups than the GPU holds at once (4 per CU): the split launch,
+  // unless the rows carry held_row statistics or a cost order -- their long
+  // finalizers then overlap the later rows' streaming inside one launch (C5:
+  // 75 us in one launch, 91 us split; C4: 57.2 us in one, 55.4 us split).
+  a.split = (g1.x > (unsigned)(4 * ctx->n_cu) && !S && !order) ? 1 : 0;
   if (C) hipLaunchKernelGGL((xs::control_kernel<M>), dim3((unsigned)rows), dim3(xs::BLOCK), 0, ctx->stream, a);
   if (order) {
     xs::RowOrder<true> ro;
@@ -3721,6 +3765,7 @@ void launch2(xs_context* ctx, xs::Args& a, int64_t rows, dim3 g1, const int32_t*
     hipLaunchKernelGGL((xs::sample_kernel<M, S, C, false>), g1, dim3(xs::BLOCK), 0, ctx->stream, a,
                        xs::RowOrder<false>{});
   }
+  if (a.split) hipLaunchKernelGGL((xs::finalize_kernel<M, S, C>), dim3((unsigned)rows), dim3(xs::BLOCK), 0, ctx->stream, a);
   if ((M || C) && a.serial) hipLaunchKernelGGL((xs::serial_kernel<M, C>), g1, dim3(xs::BLOCK), 0, ctx->stream, a);
 }
 
@@ -3782,6 +3827,8 @@ int xs_create_ex(int device, int64_t max_rows, int64_t vocab, int32_t k_max, int
   c->vocab = vocab;
   c->k_max = k_max;
   c->max_chunks = mc;
+  if (hipDeviceGetAttribute(&c->n_cu, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || c->n_cu < 1)
+    c->n_cu = 256;
   c->ctl_cap = ctl_max > xs::CTL_MAX ? ctl_max : xs::CTL_MAX;
   const int64_t nsp = ((int64_t)mc * xs::NWAVE + 63) / 64 * 64;  // sub-records per row, padded
   const int64_t units = max_rows * nsp;
@@ -3912,6 +3959,16 @@ constexpr int NA_MAX_DEVICES = 64;
 std::mutex na_mu;
 uint64_t* na_ptr[NA_MAX_DEVICES];
 
+int na_cu[NA_MAX_DEVICES];
+
+int na_cus(int dev) {  // the device's compute units, asked once
+  std::lock_guard<std::mutex> g(na_mu);
+  if (na_cu[dev] < 1 && (hipDeviceGetAttribute(&na_cu[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+                         na_cu[dev] < 1))
+    na_cu[dev] = 256;
+  return na_cu[dev];
+}
+
 uint64_t* noalloc_scratch(int dev) {
   std::lock_guard<std::mutex> g(na_mu);
   if (!na_ptr[dev]) {
@@ -3939,6 +3996,7 @@ int xs_sample_noalloc(const xs_sample_args* in, void* hip_stream) {
   c.vocab = xs::NA_VOCAB;
   c.k_max = XS_K_MAX;
   c.max_chunks = (int32_t)xs::NA_CHUNKS;
+  c.n_cu = na_cus(dev);
   c.rec = base + xs::NA_OFF_REC;
   c.ctl_patch = base + xs::NA_OFF_PATCH;
   c.ctl_cap = xs::CTL_MAX;

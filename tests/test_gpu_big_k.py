@@ -114,3 +114,42 @@ def test_large_top_k_in_a_verify_block(bigctx, oracle):
                                      sum_mode=oracle.SUM_SEQ_F32, margins=True)
         if min(o.margin_order, o.margin_cut, o.margin_draw) > 1e-5:
             assert o.token == tok.reshape(-1)[r], r
+
+
+def test_head_selection_tie_groups(bigctx, oracle):
+    """top_k <= 1,024 takes a radix select on the values; the boundary's p can
+    be shared by several adjacent values (T = 0.7 and 1.3 map neighbouring
+    floats to one p), by a run of equal logits that fits the selection list or
+    overflows it (the group's lowest ids are taken in id order), or be 0 (a
+    mask leaves fewer ids than top_k: the rest of the row ties at p = 0).
+    top_k 129, 1,024 and 1,025 sit on the path's edges."""
+    x, rng = _rows(11128, 10)
+    T = np.array([0.7, 1.3, 1.0, 1.0, 1.0, 1.3, 1.0, 1.0, 1.0, 0.7])
+    K = np.array([1000, 1000, 1000, 1000, 500, 1000, 129, 1024, 1025, 1024])
+    P = np.array([0.95, 1.0, 1.0, 0.9, 1.0, 1.0, 0.95, 1.0, 0.95, 1.0])
+    # rows 2, 3: 600 ids above 6; a run of equal logits at 5 (500 ids: fits
+    # the list; 3,000 ids: overflows it)
+    for r, run in ((2, 500), (3, 3000)):
+        x[r] = np.minimum(x[r], 4.0)
+        ids = rng.permutation(V)
+        x[r, ids[:600]] = rng.uniform(6.0, 9.0, 600).astype(np.float32)
+        x[r, ids[600:600 + run]] = 5.0
+    # row 5: the boundary inside a block of consecutive floats below 5
+    base = np.float32(5.0)
+    x[5] = np.minimum(x[5], 4.0)
+    ids = rng.permutation(V)
+    x[5, ids[:900]] = rng.uniform(6.0, 9.0, 900).astype(np.float32)
+    steps = np.arange(1, 401, dtype=np.int64) // 4
+    x[5, ids[900:1300]] = (base.view(np.int32) - steps).astype(np.int32).view(np.float32)
+    # row 9: equal logits at the very top (the whole head one group)
+    x[9, :] = np.minimum(x[9], 4.0)
+    x[9, rng.integers(0, V, 1500)] = 7.5
+    allow = np.ones((10, V), bool)
+    allow[4] = False
+    allow[4, rng.integers(0, V, 100)] = True   # ~100 ids < top_k 500: p = 0 ties
+    mask = workloads.pack_mask(allow)
+    U = workloads.uniforms(rng, 10)
+    d = run_sample(bigctx, x, T, K, P, U, mask=mask, cand_k=1100)
+    assert (d["status"] == 0).all(), d["status"]
+    assert list(d["n_cand"]) == list(K)
+    check_rows(oracle, x, T, K, P, U, d, mask=mask, label="head ties")

@@ -672,10 +672,24 @@ struct BigLds {
 // The chunk pass stages each wave's entries here before it publishes them;
 // after the hand-off only the row's last workgroup uses the memory again, as
 // its finalizer's.
+// The whole-row path's selection of the top BIG_HEAD_K candidates: digit
+// counts per wave, the gathered entries, and the draw's prefix sums.
+constexpr int BIG_HEAD_K = 1024;
+constexpr uint32_t KEY_NINF = 0x007FFFFFu;  // fkey(-inf)
+constexpr uint32_t KEY_PINF = 0xFF800000u;  // fkey(+inf)
+struct BigHeadLds {
+  uint32_t hist[NWAVE][256];
+  uint64_t list[2 * BIG_HEAD_K];
+  float cum[BIG_HEAD_K];
+  double expt[64];
+  uint32_t sel[4];
+  int32_t s4[NWAVE];
+};
 union TailLds {
   uint64_t stage[NWAVE][CAPW];
   FinLds fin;
   BigLds big;
+  BigHeadLds bh;
 };
 // p = rn(e / S) of one controlled logit v (the reference's softmax_in_place:
 // v *= inv unless T == 1, then exp(v - max), then / sum; sampler.rs:289-310).
@@ -2196,87 +2210,16 @@ XS_DEV void radix_sort_desc(uint64_t* src, uint64_t* dst, int n, BigLds& B) {
   }
 }
 
-template <bool HAS_MASK, bool HAS_CTL>
-XS_DEV void big_finalize(const Args& a, const Cfg& cfg, int row, const float* rowp, const uint32_t* mrow,
-                         TailLds& Tl) {
-  __syncthreads();                 // the first wave has finalized the row and left its stash
-  const BigStash bs = Tl.fin.big;  // read before the workgroup reuses the memory
-  __syncthreads();
-  if (!bs.defer) return;
-  BigLds& B = Tl.big;
-  const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
-  const int enc = (int)a.enc;
-  uint64_t* const A = a.big + (int64_t)row * 2 * a.big_ld;
-  uint64_t* const A2 = A + a.big_ld;
-  if (tid < 64) B.expt[tid] = (&kExpT[0][0])[tid];
-  CtlRow cr{};
-  const uint64_t* pl = nullptr;
-  if (HAS_CTL) {
-    cr = a.ctl_row[row];
-    pl = a.patch + (int64_t)row * a.ctl_cap;
-  }
-  const bool ctl_on = HAS_CTL && cr.active;
-  __syncthreads();
-
-  // 1. p of every id, in id order; one slot (BLOCK float4s) per round, the
-  // controls applied as the streaming pass applies them
-  int pc = 0;
-#pragma unroll 1
-  for (int f0 = 0; 4 * f0 < enc; f0 += BLOCK) {
-    const int f = f0 + tid;
-    const int sb = 4 * f0;
-    float4 q = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
-    if (4 * f < enc) q = reinterpret_cast<const float4*>(rowp)[f];
-    float x[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-      const int id = 4 * f + e;
-      if (HAS_MASK && id < enc && !((mrow[id >> 5] >> (id & 31)) & 1u)) x[e] = -INFINITY;
-    }
-    if (ctl_on) {
-      if (cr.force_id >= 0) {
-#pragma unroll
-        for (int e = 0; e < 4; e++) x[e] = (4 * f + e == cr.force_id) ? cr.force_val : -INFINITY;
-      } else {
-        while (pc < cr.n_patch) {
-          const uint64_t pe = pl[pc];
-          const int off = (int)(uint32_t)(pe >> 32) - sb;
-          if (off >= SLOT) break;
-          if ((off >> 2) == tid) {
-            const float pv = __uint_as_float((uint32_t)pe);
-#pragma unroll
-            for (int e = 0; e < 4; e++) x[e] = ((off & 3) == e) ? pv : x[e];
-          }
-          pc++;
-        }
-        const int pt = cr.pull_id - sb;
-        if (pt >= 0 && pt < SLOT && (pt >> 2) == tid) {
-#pragma unroll
-          for (int e = 0; e < 4; e++) x[e] = ((pt & 3) == e) ? cr.pull_val : x[e];
-        }
-      }
-    }
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-      const int id = 4 * f + e;
-      if (id < enc) {
-        const float pe = exact_p(x[e], cfg, bs.m_s, bs.S, B.expt);
-        A[id] = ((uint64_t)__float_as_uint(pe + 0.0f) << 32) | (uint32_t)id;
-      }
-    }
-  }
-  __syncthreads();
-
-  // 2. (p desc, id asc)
-  radix_sort_desc(A, A2, enc, B);
-  if (wave != 0) return;
-
-  // 3. the candidates A[0..kk): truncate_top_p and the draw, serial f32
-  const int kk = min(cfg.k, enc);
+// The draw over the candidates srt[0..kk), (p bits << 32 | id) in (p desc,
+// id asc) order: truncate_top_p (sampler.rs:401-429) and WeightedIndex
+// (:235-243, rand 0.9) as the reference's serial f32 chains, every lane
+// adding the same weights in order; cum holds the serial prefixes (kk floats).
+// One wave.
+XS_DEV void big_draw(const Args& a, const Cfg& cfg, int row, const uint64_t* srt, float* cum, int kk) {
+  const int lane = lane_id();
   const bool renorm = !(cfg.top_p >= 1.0f);
-  float* const cum = reinterpret_cast<float*>(A2);  // serial prefixes, the sort's spare buffer
   auto wt = [&](int i) __attribute__((always_inline)) -> float {
-    const float w = __uint_as_float((uint32_t)(A[min(i, kk - 1)] >> 32));  // (clamped: never past the row)
+    const float w = __uint_as_float((uint32_t)(srt[min(i, kk - 1)] >> 32));  // (clamped: never past the row)
     return i < kk ? w : 0.0f;
   };
   int st = XS_ROW_OK;
@@ -2341,7 +2284,7 @@ XS_DEV void big_finalize(const Args& a, const Cfg& cfg, int row, const float* ro
           break;
         }
       }
-      const int tok = (int)(uint32_t)A[idx];
+      const int tok = (int)(uint32_t)srt[idx];
       if (lane == 0) st_agent(&a.token[row], tok);
     }
   }
@@ -2354,7 +2297,7 @@ XS_DEV void big_finalize(const Args& a, const Cfg& cfg, int row, const float* ro
     const int kw = (int)min((int64_t)kk, a.cand_ld);
 #pragma unroll 1
     for (int i = lane; i < kw; i += 64) {
-      const uint64_t e = A[i];
+      const uint64_t e = srt[i];
       float w = __uint_as_float((uint32_t)(e >> 32));
       if (renorm) w = i < keep ? __fdiv_rn(w, sum) : 0.0f;
       if (a.cand_id) a.cand_id[(int64_t)row * a.cand_ld + i] = (int32_t)(uint32_t)e;
@@ -2614,6 +2557,321 @@ XS_DEV uint32_t ser_walk(const Args& a, const Cfg& cfg, int row, uint32_t sb, co
     }
   }
   return sb;
+}
+
+
+// The head of a whole row for top_k <= BIG_HEAD_K: the candidates are the
+// top kk = min(top_k, enc) by (p desc, id asc), and p is non-decreasing in the
+// value, so they are found on the values without computing every p:
+//   1. every id's value key (fkey of the masked, controlled value) into K, and
+//      the count of each top byte;
+//   2. a radix select, byte by byte from the top, of tau, the kk-th largest key;
+//   3. the keys [lo, hi] whose p equals P_tau = p(tau), by a search over the
+//      key range (different values can round to one p);
+//   4. when the ids with a key >= lo fit the list, all of them with exact p
+//      (the top kk lie among them); else the ids above hi (fewer than kk) and
+//      the lowest `need` ids of [lo, hi] in id order, where need is kk less
+//      the first group's size;
+//   5. the gathered entries sorted by (p desc, id asc) in LDS (bitonic); the
+//      first kk are the candidates, as (p bits << 32 | id).
+template <bool HAS_MASK, typename VALS>
+XS_DEV void big_head(const Args& a, const Cfg& cfg, int row, const float* rowp, const uint32_t* mrow,
+                     const BigStash& bs, int kk, BigHeadLds& H, uint32_t* K, VALS& vals) {
+  const int tid = threadIdx.x, wave = wave_id();
+  const int enc = (int)a.enc;
+  const int fmax = (enc - 1) >> 2;
+  const int n4 = (enc + 3) >> 2;  // key quads
+  const uint4* const K4 = reinterpret_cast<const uint4*>(K);
+  // every key of the row, 16 quads per thread in flight: f(key, id)
+  auto sweep = [&](auto&& f) __attribute__((always_inline)) {
+    constexpr int U = 16;
+#pragma unroll 1
+    for (int base = 0; base < n4; base += U * BLOCK) {
+      uint4 v[U];
+#pragma unroll
+      for (int u = 0; u < U; u++) {
+        const int i = base + u * BLOCK + tid;
+        v[u] = i < n4 ? K4[i] : make_uint4(0u, 0u, 0u, 0u);
+      }
+#pragma unroll
+      for (int u = 0; u < U; u++) {
+        const int id0 = 4 * (base + u * BLOCK + tid);
+        const uint32_t k4[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+          if (id0 + e < enc) f(k4[e], id0 + e);
+      }
+    }
+  };
+  if (tid < 64) H.expt[tid] = (&kExpT[0][0])[tid];
+  for (int i = tid; i < NWAVE * 256; i += BLOCK) (&H.hist[0][0])[i] = 0u;
+  __syncthreads();
+  // 1. keys, eight slots per round with their loads issued first
+  int pc = 0;
+  const int nslot = (enc + SLOT - 1) / SLOT;
+#pragma unroll 1
+  for (int s0 = 0; s0 < nslot; s0 += 8) {
+    float4 q[8];
+    uint32_t mw[8];
+#pragma unroll
+    for (int g = 0; g < 8; g++) {
+      const int f = min((s0 + g) * BLOCK + tid, fmax);
+      q[g] = reinterpret_cast<const float4*>(rowp)[f];
+      mw[g] = HAS_MASK ? mrow[f >> 3] : 0xFFFFFFFFu;
+    }
+#pragma unroll
+    for (int g = 0; g < 8; g++) {
+      if (s0 + g < nslot) {
+        float x[4];
+        vals((s0 + g) * SLOT, q[g], mw[g], pc, x);
+        const int id0 = (s0 + g) * SLOT + 4 * tid;
+        uint32_t k[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          k[e] = fkey(x[e]);
+          if (id0 + e < enc) atomicAdd(&H.hist[wave][k[e] >> 24], 1u);
+        }
+        if (id0 + 3 < enc) {
+          reinterpret_cast<uint4*>(K)[id0 >> 2] = make_uint4(k[0], k[1], k[2], k[3]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; e++)
+            if (id0 + e < enc) K[id0 + e] = k[e];
+        }
+      }
+    }
+  }
+  __syncthreads();
+  // 2. tau, byte by byte: `above` keys lie above the current prefix's bucket
+  uint32_t prefix = 0;
+  int above = 0, c_eq = 0;
+#pragma unroll 1
+  for (int d = 0; d < 4; d++) {
+    if (d > 0) {
+      for (int i = tid; i < NWAVE * 256; i += BLOCK) (&H.hist[0][0])[i] = 0u;
+      __syncthreads();
+      const int sh = 32 - 8 * d;  // the matched high bits
+      sweep([&](uint32_t k, int) __attribute__((always_inline)) {
+        if ((k >> sh) == prefix) atomicAdd(&H.hist[wave][(k >> (sh - 8)) & 255u], 1u);
+      });
+      __syncthreads();
+    }
+    // bins from the top: thread t holds bin 255 - t
+    const int b = 255 - tid;
+    const int c = (int)(H.hist[0][b] + H.hist[1][b] + H.hist[2][b] + H.hist[3][b]);
+    int total;
+    const int ex = block_excl_scan(c, H.s4, &total);
+    if (above + ex < kk && above + ex + c >= kk) {
+      H.sel[0] = (prefix << 8) | (uint32_t)b;
+      H.sel[1] = (uint32_t)(above + ex);
+      H.sel[3] = (uint32_t)c;
+    }
+    __syncthreads();
+    prefix = H.sel[0];
+    above = (int)H.sel[1];
+    c_eq = (int)H.sel[3];
+    __syncthreads();
+  }
+  const uint32_t tau = prefix;
+  // 3. the tie group of tau in p: p is non-decreasing in the key (the scaled
+  // value, its exponential and the division all round monotonically; no key
+  // of a row drawn here is NaN), so the ids with p == P_tau are those whose
+  // keys lie in one interval [lo, hi] around tau, found by a 64-ary search
+  const float P_tau = exact_p(keyf(tau), cfg, bs.m_s, bs.S, H.expt);
+  if (wave == 0) {
+    const int lane = lane_id();
+    auto pk = [&](uint32_t k) __attribute__((always_inline)) { return exact_p(keyf(k), cfg, bs.m_s, bs.S, H.expt); };
+    // hi: the largest key with p <= P_tau; the key of +inf (p = inf) has more
+    uint64_t L = tau, R = KEY_PINF;  // p(L) <= P_tau < p(R)
+#pragma unroll 1
+    while (R - L > 1) {
+      const uint64_t st = (R - L + 63) / 64;
+      const uint64_t q = L + (uint64_t)(lane + 1) * st;
+      const bool in = q < R && pk((uint32_t)q) <= P_tau;
+      const uint64_t bm = __ballot(in);
+      const int j = bm ? 63 - __builtin_clzll(bm) : -1;  // last lane still at P_tau
+      const uint64_t nl = L + (uint64_t)(j + 1) * st;
+      R = min(R, nl + st);
+      L = nl;
+    }
+    const uint32_t hi = (uint32_t)L;
+    // lo: the smallest key with p >= P_tau (the key of -inf when P_tau is 0)
+    uint32_t lo = KEY_NINF;
+    if (pk(KEY_NINF) < P_tau) {
+      L = KEY_NINF;
+      R = tau;  // p(L) < P_tau <= p(R)
+#pragma unroll 1
+      while (R - L > 1) {
+        const uint64_t st = (R - L + 63) / 64;
+        const uint64_t q = L + (uint64_t)(lane + 1) * st;
+        const bool below = q < R && pk((uint32_t)q) < P_tau;
+        const uint64_t bm = __ballot(below);
+        const int j = bm ? 63 - __builtin_clzll(bm) : -1;  // last lane still below
+        const uint64_t nl = L + (uint64_t)(j + 1) * st;
+        R = min(R, nl + st);
+        L = nl;
+      }
+      lo = (uint32_t)R;
+    }
+    if (lane == 0) {
+      H.sel[0] = lo;
+      H.sel[1] = hi;
+      H.sel[2] = 0u;
+    }
+  }
+  __syncthreads();
+  const uint32_t lo = H.sel[0], hi = H.sel[1];
+  __syncthreads();
+  // 4. every id with p >= P_tau when they fit the list (then the top kk lie
+  // among them); else the ids above the group (fewer than kk: p > P_tau) and
+  // the group's lowest ids, in id order
+  const int cap = 2 * BIG_HEAD_K;
+  const bool one = P_tau > 0.0f && c_eq <= cap;  // (P_tau == 0: the group is the rest of the row)
+  if (one) {
+    sweep([&](uint32_t k, int id) __attribute__((always_inline)) {
+      if (k >= lo) {
+        const uint32_t pos = atomicAdd(&H.sel[2], 1u);
+        if (pos < (uint32_t)cap) H.list[pos] = (uint64_t)(uint32_t)id;
+      }
+    });
+    __syncthreads();
+  }
+  const bool fit = one && H.sel[2] <= (uint32_t)cap;  // (uniform)
+  if (!fit) {
+    __syncthreads();
+    if (tid == 0) H.sel[2] = 0u;
+    __syncthreads();
+    sweep([&](uint32_t k, int id) __attribute__((always_inline)) {
+      if (k > hi) {
+        const uint32_t pos = atomicAdd(&H.sel[2], 1u);
+        H.list[pos] = (uint64_t)(uint32_t)id;
+      }
+    });
+    __syncthreads();
+  }
+  const int ng = (int)H.sel[2];
+  for (int i = tid; i < ng; i += BLOCK) {
+    const uint32_t id = (uint32_t)H.list[i];
+    const float p = exact_p(keyf(K[id]), cfg, bs.m_s, bs.S, H.expt);
+    H.list[i] = ((uint64_t)__float_as_uint(p + 0.0f) << 32) | (uint64_t)(0xFFFFFFFFu - id);
+  }
+  int n = ng;
+  if (!fit) {
+    // the scan ends once `need` ids of the group are found: within the first
+    // slots for the p = 0 group, which holds most of the row
+    const int need = kk - ng;
+    const uint64_t tie_e = ((uint64_t)__float_as_uint(P_tau + 0.0f) << 32);
+    int found = 0;
+#pragma unroll 1
+    for (int base = 0; base < enc && found < need; base += BLOCK) {
+      const int i = base + tid;
+      const uint32_t k = i < enc ? K[i] : 0u;
+      const bool t = i < enc && k >= lo && k <= hi;
+      int got;
+      const int pos = found + block_excl_scan(t ? 1 : 0, H.s4, &got);
+      if (t && pos < need) H.list[ng + pos] = tie_e | (uint64_t)(0xFFFFFFFFu - (uint32_t)i);
+      found += got;  // (uniform)
+    }
+    n = ng + min(found, need);
+  }
+  // 5. (p desc, id asc): bitonic over the next power of two, padding at 0
+  int n2 = 1;
+  while (n2 < n) n2 <<= 1;
+  for (int i = n + tid; i < n2; i += BLOCK) H.list[i] = 0ull;
+  __syncthreads();
+  for (int size = 2; size <= n2; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = tid; i < n2 / 2; i += BLOCK) {
+        const int lo = 2 * i - (i & (stride - 1)), hi = lo + stride;
+        const bool desc = (lo & size) == 0;
+        const uint64_t x = H.list[lo], y = H.list[hi];
+        if ((x < y) == desc) {
+          H.list[lo] = y;
+          H.list[hi] = x;
+        }
+      }
+      __syncthreads();
+    }
+  }
+  for (int i = tid; i < kk; i += BLOCK) {
+    const uint64_t e = H.list[i];
+    H.list[i] = (e & 0xFFFFFFFF00000000ull) | (uint64_t)(0xFFFFFFFFu - (uint32_t)e);
+  }
+  __syncthreads();
+}
+
+template <bool HAS_MASK, bool HAS_CTL>
+XS_DEV void big_finalize(const Args& a, const Cfg& cfg, int row, const float* rowp, const uint32_t* mrow,
+                         TailLds& Tl) {
+  __syncthreads();                 // the first wave has finalized the row and left its stash
+  const BigStash bs = Tl.fin.big;  // read before the workgroup reuses the memory
+  __syncthreads();
+  if (!bs.defer) return;
+  const int tid = threadIdx.x, wave = wave_id();
+  const int enc = (int)a.enc;
+  const int kk = min(cfg.k, enc);
+  uint64_t* const A = a.big + (int64_t)row * 2 * a.big_ld;
+  uint64_t* const A2 = A + a.big_ld;
+  CtlRow cr{};
+  const uint64_t* pl = nullptr;
+  if (HAS_CTL) {
+    cr = a.ctl_row[row];
+    pl = a.patch + (int64_t)row * a.ctl_cap;
+  }
+  const bool ctl_on = HAS_CTL && cr.active;
+  // this thread's four masked and controlled values of the slot at sb (the
+  // slots in order: pc walks the sorted patch list as the streaming pass does)
+  auto vals = [&](int sb, float4 q, uint32_t mw, int& pc, float (&x)[4]) __attribute__((always_inline)) {
+    const int id0 = sb + 4 * tid;
+    x[0] = q.x;
+    x[1] = q.y;
+    x[2] = q.z;
+    x[3] = q.w;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      if (id0 + e >= enc) x[e] = -INFINITY;
+      else if (HAS_MASK && !((mw >> ((id0 + e) & 31)) & 1u)) x[e] = -INFINITY;
+    }
+    if (ctl_on) ctl_slot(x, sb, tid, pl, pc, cr.n_patch, cr.pull_id, cr.pull_val, cr.force_id, cr.force_val);
+  };
+
+  // The head: top_k <= BIG_HEAD_K selected by a radix select on the values,
+  // exact p only for those (big_head); else every id's p and a full sort.
+  if (kk <= BIG_HEAD_K) {
+    BigHeadLds& H = Tl.bh;
+    big_head<HAS_MASK>(a, cfg, row, rowp, mrow, bs, kk, H, reinterpret_cast<uint32_t*>(A), vals);
+    if (wave == 0) big_draw(a, cfg, row, H.list, H.cum, kk);
+    return;
+  }
+
+  BigLds& B = Tl.big;
+  if (tid < 64) B.expt[tid] = (&kExpT[0][0])[tid];
+  __syncthreads();
+  // 1. p of every id, in id order; one slot (BLOCK float4s) per round
+  int pc = 0;
+#pragma unroll 1
+  for (int f0 = 0; 4 * f0 < enc; f0 += BLOCK) {
+    const int f = f0 + tid;
+    float4 q = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+    if (4 * f < enc) q = reinterpret_cast<const float4*>(rowp)[f];
+    const uint32_t mw = (HAS_MASK && 4 * f < enc) ? mrow[f >> 3] : 0xFFFFFFFFu;
+    float x[4];
+    vals(4 * f0, q, mw, pc, x);
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const int id = 4 * f + e;
+      if (id < enc) {
+        const float pe = exact_p(x[e], cfg, bs.m_s, bs.S, B.expt);
+        A[id] = ((uint64_t)__float_as_uint(pe + 0.0f) << 32) | (uint32_t)id;
+      }
+    }
+  }
+  __syncthreads();
+
+  // 2. (p desc, id asc)
+  radix_sort_desc(A, A2, enc, B);
+  if (wave != 0) return;
+  big_draw(a, cfg, row, A, reinterpret_cast<float*>(A2), kk);
 }
 
 // ---------------------------------------------------------------------------

@@ -292,6 +292,13 @@ XS_DEV int block_excl_scan(int v, int* s4, int* total) {
 // one entry past it (K' = k + 1) to prove the boundary, or the whole row when
 // top_k >= enc (candidate_set's sort-everything branch, sampler.rs:323-332).
 
+// A whole-row row as its finalizer leaves it for the whole-row kernels.
+struct BigRow {
+  int32_t state;  // 1: the whole-row kernels draw the row in this call; 0: not
+  float m_s, S;   // scaled max and softmax denominator
+  int32_t kk;     // candidates: min(top_k, enc)
+};
+
 struct Cfg {
   float inv;     // (float)(1/T)  (softmax_in_place, sampler.rs:291)
   float top_p;
@@ -299,7 +306,7 @@ struct Cfg {
   int kp;        // selection size K' the streaming pass keeps per chunk
   bool greedy, scale, full, bad;
   bool big;      // more candidates than the streaming selection holds: the
-                 // whole-row path (big_finalize) draws the row
+                 // whole-row kernels draw the row
 };
 
 XS_DEV Cfg make_cfg(const xs_row_params& p, int64_t enc, int n_top, int k_max) {
@@ -322,7 +329,7 @@ XS_DEV Cfg make_cfg(const xs_row_params& p, int64_t enc, int n_top, int k_max) {
     c.full = false;
   }
   // K' past KSEL (top_k >= 128, or a whole row wider than KSEL): the streaming
-  // pass keeps only what the argmax and held_row need, and big_finalize sorts
+  // pass keeps only what the argmax and held_row need, and the whole-row kernels sort
   // the whole row
   c.big = !c.greedy && (c.kp > KSEL || (c.full && enc > KSEL));
   if (c.big) c.kp = 1;
@@ -417,8 +424,13 @@ struct Args {
   int32_t* seq_ticket;  // [seqs * TSTRIDE] rows of the sequence that are finalized (0 between calls)
   int32_t n_chunks, nslots;
   int32_t k_max;     // the context's largest top_k (of min(top_k, enc)); larger is XS_ROW_BAD_PARAM
-  uint64_t* big;     // [rows, 2, big_ld]: big_finalize's sort buffers (contexts with k_max > XS_K_MAX)
+  uint64_t* big;     // [rows, 2, big_ld]: the whole-row sort's buffers (contexts with k_max > XS_K_MAX)
   int64_t big_ld;
+  struct BigRow* big_state;  // [rows]: what the finalizer leaves for the whole-row kernels
+  uint32_t* big_hist;        // [rows, big_hld]: per-tile digit counts (then first positions) of a sort pass
+  int64_t big_hld;
+  int32_t* big_ticket;       // [rows * TSTRIDE]: the sort passes' arrival tickets, zero between kernels
+  int32_t big_tiles;         // tiles of BTILE ids per row
   // the serial denominator (serial_kernel): set on calls with a mask or
   // controls, whose rows at top_p >= 1 serial_kernel finalizes
   int32_t serial;
@@ -647,10 +659,10 @@ struct HeldLds {
   int32_t n_have;                   // top-n entries below
   float vals[XS_TOP_MAX];           // top-n logits, (logit desc, id asc)
 };
-// What the finalizing wave leaves for big_finalize.
+// What the finalizing wave leaves for the whole-row kernels.
 struct BigStash {
   float m_s, S;                     // scaled max and softmax denominator of the row
-  int32_t defer;                    // the row is drawn by big_finalize
+  int32_t defer;                    // the row is drawn by the whole-row kernels
   int32_t pad;
 };
 struct FinLds {
@@ -663,33 +675,12 @@ struct FinLds {
   HeldLds held;
   BigStash big;
 };
-// big_finalize's workspace: the exp table and the radix sort's counters.
-struct BigLds {
-  double expt[64];
-  uint32_t cnt[16][BLOCK];          // per digit, per thread: count, then write position
-  int32_t s4[NWAVE];
-};
 // The chunk pass stages each wave's entries here before it publishes them;
 // after the hand-off only the row's last workgroup uses the memory again, as
 // its finalizer's.
-// The whole-row path's selection of the top BIG_HEAD_K candidates: digit
-// counts per wave, the gathered entries, and the draw's prefix sums.
-constexpr int BIG_HEAD_K = 1024;
-constexpr uint32_t KEY_NINF = 0x007FFFFFu;  // fkey(-inf)
-constexpr uint32_t KEY_PINF = 0xFF800000u;  // fkey(+inf)
-struct BigHeadLds {
-  uint32_t hist[NWAVE][256];
-  uint64_t list[2 * BIG_HEAD_K];
-  float cum[BIG_HEAD_K];
-  double expt[64];
-  uint32_t sel[4];
-  int32_t s4[NWAVE];
-};
 union TailLds {
   uint64_t stage[NWAVE][CAPW];
   FinLds fin;
-  BigLds big;
-  BigHeadLds bh;
 };
 // p = rn(e / S) of one controlled logit v (the reference's softmax_in_place:
 // v *= inv unless T == 1, then exp(v - max), then / sum; sampler.rs:289-310).
@@ -1874,7 +1865,7 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
   w[1] = __uint_as_float((uint32_t)(pk[1] >> 32));
   int tok = -1;
   // a row with more candidates than the selection holds is drawn by the
-  // whole workgroup afterwards (big_finalize); here only its statistics
+  // whole-row kernels afterwards; here only its statistics
   const bool defer = cfg.big && stoch && st == XS_ROW_OK;
   if (st == XS_ROW_OK && !defer) {
     if (!stoch) {
@@ -2019,6 +2010,7 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
     F.big.defer = defer ? 1 : 0;
     F.big.m_s = m_s;
     F.big.S = S;
+    if (cfg.big && a.big_state) a.big_state[row] = BigRow{defer ? 1 : 0, m_s, S, k};
   }
   if (want_cands && stoch && st == XS_ROW_OK && !defer) {
     const int kw = (int)min((int64_t)k, a.cand_ld);  // a short cand_ld truncates the list
@@ -2149,27 +2141,15 @@ XS_DEV void verify_walk(const Args& a, int row) {
   }
 }
 
-// ---------------------------------------------------------------------------
-// The whole-row path: rows whose candidate set is larger than the streaming
-// selection holds -- top_k of 128 or more, and top_k >= enc, the reference's
-// candidate_set branch that sorts the whole row (sampler.rs:322-338), which is
-// xwen's only top-p-only mode because top_k <= 1 means greedy.  The row's last
-// workgroup, all four waves, after its first wave found the row's max and
-// softmax denominator:
-//   1. p = rn(exp(s - max) / S) of every id, the same correctly rounded f32
-//      arithmetic as the selection path, into the row's sort buffer as
-//      (p bits << 32 | id), in id order;
-//   2. a stable LSD radix sort by p descending (4-bit digits, eight passes,
-//      per-thread contiguous segments), so equal p keep ascending ids: the
-//      (p desc, id asc) order of top_k_desc and of the stable whole-row sort;
-//   3. the first min(top_k, enc) entries are the candidates; truncate_top_p
-//      (sampler.rs:401-429) and WeightedIndex (:235-243, rand 0.9) run as the
-//      reference's serial f32 chains, by one wave, every lane adding the same
-//      weights in order.
+// radix_sort_desc's counters.
+struct SortLds {
+  uint32_t cnt[16][BLOCK];          // per digit, per thread: count, then write position
+  int32_t s4[NWAVE];
+};
 
 // Stable LSD radix sort of n u64 entries by their high 32 bits, descending;
 // src holds the result afterwards (an even number of passes).  All waves.
-XS_DEV void radix_sort_desc(uint64_t* src, uint64_t* dst, int n, BigLds& B) {
+XS_DEV void radix_sort_desc(uint64_t* src, uint64_t* dst, int n, SortLds& B) {
   const int t = threadIdx.x;
   const int L = (n + BLOCK - 1) / BLOCK;
   const int i0 = min(n, t * L), i1 = min(n, i0 + L);
@@ -2210,100 +2190,11 @@ XS_DEV void radix_sort_desc(uint64_t* src, uint64_t* dst, int n, BigLds& B) {
   }
 }
 
-// The draw over the candidates srt[0..kk), (p bits << 32 | id) in (p desc,
-// id asc) order: truncate_top_p (sampler.rs:401-429) and WeightedIndex
-// (:235-243, rand 0.9) as the reference's serial f32 chains, every lane
-// adding the same weights in order; cum holds the serial prefixes (kk floats).
-// One wave.
-XS_DEV void big_draw(const Args& a, const Cfg& cfg, int row, const uint64_t* srt, float* cum, int kk) {
-  const int lane = lane_id();
-  const bool renorm = !(cfg.top_p >= 1.0f);
-  auto wt = [&](int i) __attribute__((always_inline)) -> float {
-    const float w = __uint_as_float((uint32_t)(srt[min(i, kk - 1)] >> 32));  // (clamped: never past the row)
-    return i < kk ? w : 0.0f;
-  };
-  int st = XS_ROW_OK;
-  float sum = 1.0f;
-  int keep = kk;
-  if (renorm) {
-    // sum of every candidate weight, folded from -0.0 as Rust's f32 Sum does
-    float acc = -0.0f;
-#pragma unroll 1
-    for (int b0 = 0; b0 < kk; b0 += 64) {
-      const float w = wt(b0 + lane);
-#pragma unroll 16
-      for (int u = 0; u < 64; u++) acc = acc + rdlf(w, u);
-    }
-    sum = acc;
-    if (!(sum > 0.0f)) st = XS_ROW_ZERO_WEIGHT;  // weights left unchanged: no mass to draw
-  }
-  if (st == XS_ROW_OK) {
-    // renormalised weights (or the raw ones at top_p >= 1), their serial
-    // prefix from 0 (truncate_top_p's cumsum, the same sums as WeightedIndex's
-    // cumulative weights) until the cut
-    float acc = 0.0f;
-    bool cut = false;
-#pragma unroll 1
-    for (int b0 = 0; b0 < kk && !cut; b0 += 64) {
-      const int i = b0 + lane;
-      float w = wt(i);
-      if (renorm) w = __fdiv_rn(w, sum);
-      float mine = 0.0f;
-#pragma unroll 16
-      for (int u = 0; u < 64; u++) {
-        acc = acc + rdlf(w, u);
-        mine = (lane == u) ? acc : mine;
-      }
-      if (i < kk) cum[i] = mine;
-      if (renorm) {
-        const uint64_t bm = __ballot(i < kk && mine >= cfg.top_p);
-        if (bm) {
-          keep = b0 + (int)__builtin_ctzll(bm) + 1;
-          cut = true;
-        }
-      }
-    }
-    wave_lds_sync();  // (cum is read back by other lanes below)
-    __builtin_amdgcn_s_waitcnt(0);
-    const float tot = cum[keep - 1];
-    if (!(tot > 0.0f)) {
-      st = XS_ROW_ZERO_WEIGHT;
-    } else {
-      const float u_row = a.uniforms[row];
-      const float x_draw = u_row * tot + 0.0f;
-      // the index: the cumulative weights (prefix through i, i < kk - 1; the
-      // total from keep - 1 on) at or below x
-      int idx = keep - 1;
-#pragma unroll 1
-      for (int b0 = 0; b0 < keep - 1; b0 += 64) {
-        const int i = b0 + lane;
-        const float c = cum[min(i, keep - 1)];
-        const uint64_t bm = __ballot(i < keep - 1 && c > x_draw);
-        if (bm) {
-          idx = b0 + (int)__builtin_ctzll(bm);
-          break;
-        }
-      }
-      const int tok = (int)(uint32_t)srt[idx];
-      if (lane == 0) st_agent(&a.token[row], tok);
-    }
-  }
-  if (lane == 0) {
-    if (st != XS_ROW_OK) st_agent(&a.token[row], -1);
-    st_agent(&a.status[row], st);
-    if (a.n_cand) a.n_cand[row] = st == XS_ROW_OK ? kk : 0;
-  }
-  if (st == XS_ROW_OK && (a.cand_id || a.cand_w)) {
-    const int kw = (int)min((int64_t)kk, a.cand_ld);
-#pragma unroll 1
-    for (int i = lane; i < kw; i += 64) {
-      const uint64_t e = srt[i];
-      float w = __uint_as_float((uint32_t)(e >> 32));
-      if (renorm) w = i < keep ? __fdiv_rn(w, sum) : 0.0f;
-      if (a.cand_id) a.cand_id[(int64_t)row * a.cand_ld + i] = (int32_t)(uint32_t)e;
-      if (a.cand_w) a.cand_w[(int64_t)row * a.cand_ld + i] = w;
-    }
-  }
+// The finalizing wave left the row to the whole-row kernels (which then walk
+// its verify block once they have drawn it).
+XS_DEV bool deferred(const Cfg& cfg, const FinLds& F) {
+  wave_lds_sync();  // lane 0 wrote the stash
+  return cfg.big && !cfg.bad && F.big.defer != 0;
 }
 
 // ---------------------------------------------------------------------------
@@ -2559,320 +2450,6 @@ XS_DEV uint32_t ser_walk(const Args& a, const Cfg& cfg, int row, uint32_t sb, co
   return sb;
 }
 
-
-// The head of a whole row for top_k <= BIG_HEAD_K: the candidates are the
-// top kk = min(top_k, enc) by (p desc, id asc), and p is non-decreasing in the
-// value, so they are found on the values without computing every p:
-//   1. every id's value key (fkey of the masked, controlled value) into K, and
-//      the count of each top byte;
-//   2. a radix select, byte by byte from the top, of tau, the kk-th largest key;
-//   3. the keys [lo, hi] whose p equals P_tau = p(tau), by a search over the
-//      key range (different values can round to one p);
-//   4. when the ids with a key >= lo fit the list, all of them with exact p
-//      (the top kk lie among them); else the ids above hi (fewer than kk) and
-//      the lowest `need` ids of [lo, hi] in id order, where need is kk less
-//      the first group's size;
-//   5. the gathered entries sorted by (p desc, id asc) in LDS (bitonic); the
-//      first kk are the candidates, as (p bits << 32 | id).
-template <bool HAS_MASK, typename VALS>
-XS_DEV void big_head(const Args& a, const Cfg& cfg, int row, const float* rowp, const uint32_t* mrow,
-                     const BigStash& bs, int kk, BigHeadLds& H, uint32_t* K, VALS& vals) {
-  const int tid = threadIdx.x, wave = wave_id();
-  const int enc = (int)a.enc;
-  const int fmax = (enc - 1) >> 2;
-  const int n4 = (enc + 3) >> 2;  // key quads
-  const uint4* const K4 = reinterpret_cast<const uint4*>(K);
-  // every key of the row, 16 quads per thread in flight: f(key, id)
-  auto sweep = [&](auto&& f) __attribute__((always_inline)) {
-    constexpr int U = 16;
-#pragma unroll 1
-    for (int base = 0; base < n4; base += U * BLOCK) {
-      uint4 v[U];
-#pragma unroll
-      for (int u = 0; u < U; u++) {
-        const int i = base + u * BLOCK + tid;
-        v[u] = i < n4 ? K4[i] : make_uint4(0u, 0u, 0u, 0u);
-      }
-#pragma unroll
-      for (int u = 0; u < U; u++) {
-        const int id0 = 4 * (base + u * BLOCK + tid);
-        const uint32_t k4[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
-#pragma unroll
-        for (int e = 0; e < 4; e++)
-          if (id0 + e < enc) f(k4[e], id0 + e);
-      }
-    }
-  };
-  if (tid < 64) H.expt[tid] = (&kExpT[0][0])[tid];
-  for (int i = tid; i < NWAVE * 256; i += BLOCK) (&H.hist[0][0])[i] = 0u;
-  __syncthreads();
-  // 1. keys, eight slots per round with their loads issued first
-  int pc = 0;
-  const int nslot = (enc + SLOT - 1) / SLOT;
-#pragma unroll 1
-  for (int s0 = 0; s0 < nslot; s0 += 8) {
-    float4 q[8];
-    uint32_t mw[8];
-#pragma unroll
-    for (int g = 0; g < 8; g++) {
-      const int f = min((s0 + g) * BLOCK + tid, fmax);
-      q[g] = reinterpret_cast<const float4*>(rowp)[f];
-      mw[g] = HAS_MASK ? mrow[f >> 3] : 0xFFFFFFFFu;
-    }
-#pragma unroll
-    for (int g = 0; g < 8; g++) {
-      if (s0 + g < nslot) {
-        float x[4];
-        vals((s0 + g) * SLOT, q[g], mw[g], pc, x);
-        const int id0 = (s0 + g) * SLOT + 4 * tid;
-        uint32_t k[4];
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          k[e] = fkey(x[e]);
-          if (id0 + e < enc) atomicAdd(&H.hist[wave][k[e] >> 24], 1u);
-        }
-        if (id0 + 3 < enc) {
-          reinterpret_cast<uint4*>(K)[id0 >> 2] = make_uint4(k[0], k[1], k[2], k[3]);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; e++)
-            if (id0 + e < enc) K[id0 + e] = k[e];
-        }
-      }
-    }
-  }
-  __syncthreads();
-  // 2. tau, byte by byte: `above` keys lie above the current prefix's bucket
-  uint32_t prefix = 0;
-  int above = 0, c_eq = 0;
-#pragma unroll 1
-  for (int d = 0; d < 4; d++) {
-    if (d > 0) {
-      for (int i = tid; i < NWAVE * 256; i += BLOCK) (&H.hist[0][0])[i] = 0u;
-      __syncthreads();
-      const int sh = 32 - 8 * d;  // the matched high bits
-      sweep([&](uint32_t k, int) __attribute__((always_inline)) {
-        if ((k >> sh) == prefix) atomicAdd(&H.hist[wave][(k >> (sh - 8)) & 255u], 1u);
-      });
-      __syncthreads();
-    }
-    // bins from the top: thread t holds bin 255 - t
-    const int b = 255 - tid;
-    const int c = (int)(H.hist[0][b] + H.hist[1][b] + H.hist[2][b] + H.hist[3][b]);
-    int total;
-    const int ex = block_excl_scan(c, H.s4, &total);
-    if (above + ex < kk && above + ex + c >= kk) {
-      H.sel[0] = (prefix << 8) | (uint32_t)b;
-      H.sel[1] = (uint32_t)(above + ex);
-      H.sel[3] = (uint32_t)c;
-    }
-    __syncthreads();
-    prefix = H.sel[0];
-    above = (int)H.sel[1];
-    c_eq = (int)H.sel[3];
-    __syncthreads();
-  }
-  const uint32_t tau = prefix;
-  // 3. the tie group of tau in p: p is non-decreasing in the key (the scaled
-  // value, its exponential and the division all round monotonically; no key
-  // of a row drawn here is NaN), so the ids with p == P_tau are those whose
-  // keys lie in one interval [lo, hi] around tau, found by a 64-ary search
-  const float P_tau = exact_p(keyf(tau), cfg, bs.m_s, bs.S, H.expt);
-  if (wave == 0) {
-    const int lane = lane_id();
-    auto pk = [&](uint32_t k) __attribute__((always_inline)) { return exact_p(keyf(k), cfg, bs.m_s, bs.S, H.expt); };
-    // hi: the largest key with p <= P_tau; the key of +inf (p = inf) has more
-    uint64_t L = tau, R = KEY_PINF;  // p(L) <= P_tau < p(R)
-#pragma unroll 1
-    while (R - L > 1) {
-      const uint64_t st = (R - L + 63) / 64;
-      const uint64_t q = L + (uint64_t)(lane + 1) * st;
-      const bool in = q < R && pk((uint32_t)q) <= P_tau;
-      const uint64_t bm = __ballot(in);
-      const int j = bm ? 63 - __builtin_clzll(bm) : -1;  // last lane still at P_tau
-      const uint64_t nl = L + (uint64_t)(j + 1) * st;
-      R = min(R, nl + st);
-      L = nl;
-    }
-    const uint32_t hi = (uint32_t)L;
-    // lo: the smallest key with p >= P_tau (the key of -inf when P_tau is 0)
-    uint32_t lo = KEY_NINF;
-    if (pk(KEY_NINF) < P_tau) {
-      L = KEY_NINF;
-      R = tau;  // p(L) < P_tau <= p(R)
-#pragma unroll 1
-      while (R - L > 1) {
-        const uint64_t st = (R - L + 63) / 64;
-        const uint64_t q = L + (uint64_t)(lane + 1) * st;
-        const bool below = q < R && pk((uint32_t)q) < P_tau;
-        const uint64_t bm = __ballot(below);
-        const int j = bm ? 63 - __builtin_clzll(bm) : -1;  // last lane still below
-        const uint64_t nl = L + (uint64_t)(j + 1) * st;
-        R = min(R, nl + st);
-        L = nl;
-      }
-      lo = (uint32_t)R;
-    }
-    if (lane == 0) {
-      H.sel[0] = lo;
-      H.sel[1] = hi;
-      H.sel[2] = 0u;
-    }
-  }
-  __syncthreads();
-  const uint32_t lo = H.sel[0], hi = H.sel[1];
-  __syncthreads();
-  // 4. every id with p >= P_tau when they fit the list (then the top kk lie
-  // among them); else the ids above the group (fewer than kk: p > P_tau) and
-  // the group's lowest ids, in id order
-  const int cap = 2 * BIG_HEAD_K;
-  const bool one = P_tau > 0.0f && c_eq <= cap;  // (P_tau == 0: the group is the rest of the row)
-  if (one) {
-    sweep([&](uint32_t k, int id) __attribute__((always_inline)) {
-      if (k >= lo) {
-        const uint32_t pos = atomicAdd(&H.sel[2], 1u);
-        if (pos < (uint32_t)cap) H.list[pos] = (uint64_t)(uint32_t)id;
-      }
-    });
-    __syncthreads();
-  }
-  const bool fit = one && H.sel[2] <= (uint32_t)cap;  // (uniform)
-  if (!fit) {
-    __syncthreads();
-    if (tid == 0) H.sel[2] = 0u;
-    __syncthreads();
-    sweep([&](uint32_t k, int id) __attribute__((always_inline)) {
-      if (k > hi) {
-        const uint32_t pos = atomicAdd(&H.sel[2], 1u);
-        H.list[pos] = (uint64_t)(uint32_t)id;
-      }
-    });
-    __syncthreads();
-  }
-  const int ng = (int)H.sel[2];
-  for (int i = tid; i < ng; i += BLOCK) {
-    const uint32_t id = (uint32_t)H.list[i];
-    const float p = exact_p(keyf(K[id]), cfg, bs.m_s, bs.S, H.expt);
-    H.list[i] = ((uint64_t)__float_as_uint(p + 0.0f) << 32) | (uint64_t)(0xFFFFFFFFu - id);
-  }
-  int n = ng;
-  if (!fit) {
-    // the scan ends once `need` ids of the group are found: within the first
-    // slots for the p = 0 group, which holds most of the row
-    const int need = kk - ng;
-    const uint64_t tie_e = ((uint64_t)__float_as_uint(P_tau + 0.0f) << 32);
-    int found = 0;
-#pragma unroll 1
-    for (int base = 0; base < enc && found < need; base += BLOCK) {
-      const int i = base + tid;
-      const uint32_t k = i < enc ? K[i] : 0u;
-      const bool t = i < enc && k >= lo && k <= hi;
-      int got;
-      const int pos = found + block_excl_scan(t ? 1 : 0, H.s4, &got);
-      if (t && pos < need) H.list[ng + pos] = tie_e | (uint64_t)(0xFFFFFFFFu - (uint32_t)i);
-      found += got;  // (uniform)
-    }
-    n = ng + min(found, need);
-  }
-  // 5. (p desc, id asc): bitonic over the next power of two, padding at 0
-  int n2 = 1;
-  while (n2 < n) n2 <<= 1;
-  for (int i = n + tid; i < n2; i += BLOCK) H.list[i] = 0ull;
-  __syncthreads();
-  for (int size = 2; size <= n2; size <<= 1) {
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      for (int i = tid; i < n2 / 2; i += BLOCK) {
-        const int lo = 2 * i - (i & (stride - 1)), hi = lo + stride;
-        const bool desc = (lo & size) == 0;
-        const uint64_t x = H.list[lo], y = H.list[hi];
-        if ((x < y) == desc) {
-          H.list[lo] = y;
-          H.list[hi] = x;
-        }
-      }
-      __syncthreads();
-    }
-  }
-  for (int i = tid; i < kk; i += BLOCK) {
-    const uint64_t e = H.list[i];
-    H.list[i] = (e & 0xFFFFFFFF00000000ull) | (uint64_t)(0xFFFFFFFFu - (uint32_t)e);
-  }
-  __syncthreads();
-}
-
-template <bool HAS_MASK, bool HAS_CTL>
-XS_DEV void big_finalize(const Args& a, const Cfg& cfg, int row, const float* rowp, const uint32_t* mrow,
-                         TailLds& Tl) {
-  __syncthreads();                 // the first wave has finalized the row and left its stash
-  const BigStash bs = Tl.fin.big;  // read before the workgroup reuses the memory
-  __syncthreads();
-  if (!bs.defer) return;
-  const int tid = threadIdx.x, wave = wave_id();
-  const int enc = (int)a.enc;
-  const int kk = min(cfg.k, enc);
-  uint64_t* const A = a.big + (int64_t)row * 2 * a.big_ld;
-  uint64_t* const A2 = A + a.big_ld;
-  CtlRow cr{};
-  const uint64_t* pl = nullptr;
-  if (HAS_CTL) {
-    cr = a.ctl_row[row];
-    pl = a.patch + (int64_t)row * a.ctl_cap;
-  }
-  const bool ctl_on = HAS_CTL && cr.active;
-  // this thread's four masked and controlled values of the slot at sb (the
-  // slots in order: pc walks the sorted patch list as the streaming pass does)
-  auto vals = [&](int sb, float4 q, uint32_t mw, int& pc, float (&x)[4]) __attribute__((always_inline)) {
-    const int id0 = sb + 4 * tid;
-    x[0] = q.x;
-    x[1] = q.y;
-    x[2] = q.z;
-    x[3] = q.w;
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-      if (id0 + e >= enc) x[e] = -INFINITY;
-      else if (HAS_MASK && !((mw >> ((id0 + e) & 31)) & 1u)) x[e] = -INFINITY;
-    }
-    if (ctl_on) ctl_slot(x, sb, tid, pl, pc, cr.n_patch, cr.pull_id, cr.pull_val, cr.force_id, cr.force_val);
-  };
-
-  // The head: top_k <= BIG_HEAD_K selected by a radix select on the values,
-  // exact p only for those (big_head); else every id's p and a full sort.
-  if (kk <= BIG_HEAD_K) {
-    BigHeadLds& H = Tl.bh;
-    big_head<HAS_MASK>(a, cfg, row, rowp, mrow, bs, kk, H, reinterpret_cast<uint32_t*>(A), vals);
-    if (wave == 0) big_draw(a, cfg, row, H.list, H.cum, kk);
-    return;
-  }
-
-  BigLds& B = Tl.big;
-  if (tid < 64) B.expt[tid] = (&kExpT[0][0])[tid];
-  __syncthreads();
-  // 1. p of every id, in id order; one slot (BLOCK float4s) per round
-  int pc = 0;
-#pragma unroll 1
-  for (int f0 = 0; 4 * f0 < enc; f0 += BLOCK) {
-    const int f = f0 + tid;
-    float4 q = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
-    if (4 * f < enc) q = reinterpret_cast<const float4*>(rowp)[f];
-    const uint32_t mw = (HAS_MASK && 4 * f < enc) ? mrow[f >> 3] : 0xFFFFFFFFu;
-    float x[4];
-    vals(4 * f0, q, mw, pc, x);
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-      const int id = 4 * f + e;
-      if (id < enc) {
-        const float pe = exact_p(x[e], cfg, bs.m_s, bs.S, B.expt);
-        A[id] = ((uint64_t)__float_as_uint(pe + 0.0f) << 32) | (uint32_t)id;
-      }
-    }
-  }
-  __syncthreads();
-
-  // 2. (p desc, id asc)
-  radix_sort_desc(A, A2, enc, B);
-  if (wave != 0) return;
-  big_draw(a, cfg, row, A, reinterpret_cast<float*>(A2), kk);
-}
 
 // ---------------------------------------------------------------------------
 // The kernel.  Grid: rows x n_chunks workgroups of BLOCK lanes; chunk c of a
@@ -3349,17 +2926,13 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
   if (!Lc.last) return;
   if (a.serial && serial_row<HAS_MASK, HAS_CTL>(a, cfg, row)) return;  // serial_kernel finalizes it
   // The first wave finalizes the row; held_row outputs then get the reference's
-  // serial fold (held_fold); a row with more candidates than the selection
-  // holds is drawn by the whole workgroup (big_finalize); a verify block's
-  // rows then walk accept_drafts (verify_walk).
-  const bool big_row = cfg.big && !cfg.bad;  // uniform in the workgroup
-  if (wave != 0 && !big_row) return;
-  if (wave == 0) {
-    finalize_row<HAS_MASK, WANT_LSE, HAS_CTL>(a, cfg, row, rowrec, nsp, nc * NWAVE, rowp, mrow, Tl.fin);
-    if (held) held_fold<1>(a, row, rowp, rowrec, nsp, nc * NWAVE, Tl.fin);
-  }
-  if (big_row) big_finalize<HAS_MASK, HAS_CTL>(a, cfg, row, rowp, mrow, Tl);
-  if (wave == 0 && a.span > 0) verify_walk(a, row);
+  // serial fold (held_fold); a verify block's rows then walk accept_drafts
+  // (verify_walk), except a row with more candidates than the selection
+  // holds: the whole-row kernels draw it and walk its block.
+  if (wave != 0) return;
+  finalize_row<HAS_MASK, WANT_LSE, HAS_CTL>(a, cfg, row, rowrec, nsp, nc * NWAVE, rowp, mrow, Tl.fin);
+  if (held) held_fold<1>(a, row, rowp, rowrec, nsp, nc * NWAVE, Tl.fin);
+  if (a.span > 0 && !deferred(cfg, Tl.fin)) verify_walk(a, row);
 }
 
 // ---------------------------------------------------------------------------
@@ -3383,14 +2956,10 @@ __global__ __launch_bounds__(BLOCK) void finalize_kernel(Args a) {
   const int nsp = ((nc * NWAVE + 63) >> 6) << 6;
   const uint64_t* const rowrec = a.rec + (int64_t)row * SRECW * nsp;
   const bool held = WANT_LSE && (a.row_lse != nullptr || a.n_top > 0);
-  const bool big_row = cfg.big && !cfg.bad;
-  if (wave != 0 && !big_row) return;
-  if (wave == 0) {
-    finalize_row<HAS_MASK, WANT_LSE, HAS_CTL>(a, cfg, row, rowrec, nsp, nc * NWAVE, rowp, mrow, Tl.fin);
-    if (held) held_fold<1>(a, row, rowp, rowrec, nsp, nc * NWAVE, Tl.fin);
-  }
-  if (big_row) big_finalize<HAS_MASK, HAS_CTL>(a, cfg, row, rowp, mrow, Tl);
-  if (wave == 0 && a.span > 0) verify_walk(a, row);
+  if (wave != 0) return;
+  finalize_row<HAS_MASK, WANT_LSE, HAS_CTL>(a, cfg, row, rowrec, nsp, nc * NWAVE, rowp, mrow, Tl.fin);
+  if (held) held_fold<1>(a, row, rowp, rowrec, nsp, nc * NWAVE, Tl.fin);
+  if (a.span > 0 && !deferred(cfg, Tl.fin)) verify_walk(a, row);
 }
 
 // ---------------------------------------------------------------------------
@@ -3720,11 +3289,9 @@ __global__ __launch_bounds__(BLOCK) void serial_kernel(Args a) {
     }
     S_ser = __uint_as_float(sb);
   }
-  const bool big_row = cfg.big && !cfg.bad;
-  if (wave != 0 && !big_row) return;
-  if (wave == 0) finalize_row<HAS_MASK, false, HAS_CTL>(a, cfg, row, rowrec, nsp, nsub, rowp, mrow, St.tl.fin, S_ser);
-  if (big_row) big_finalize<HAS_MASK, HAS_CTL>(a, cfg, row, rowp, mrow, St.tl);
-  if (wave == 0 && a.span > 0) verify_walk(a, row);
+  if (wave != 0) return;
+  finalize_row<HAS_MASK, false, HAS_CTL>(a, cfg, row, rowrec, nsp, nsub, rowp, mrow, St.tl.fin, S_ser);
+  if (a.span > 0 && !deferred(cfg, St.tl.fin)) verify_walk(a, row);
 }
 
 // ---------------------------------------------------------------------------
@@ -3740,7 +3307,7 @@ template <bool HAS_MASK>
 __global__ __launch_bounds__(BLOCK) void control_kernel(Args a) {
   __shared__ uint64_t lkeys[CTL_MAX];  // (id << 32 | list position), sorted (lists of CTL_MAX or fewer)
   __shared__ uint64_t lpl[CTL_MAX];    // the patch list (idem)
-  __shared__ BigLds B;                 // the radix sort's counters (longer lists)
+  __shared__ SortLds B;                // the radix sort's counters (longer lists)
   __shared__ int s4[NWAVE];
   __shared__ float wmax[NWAVE];
   const int row = blockIdx.x, tid = threadIdx.x, lane = lane_id(), wave = wave_id();
@@ -3964,6 +3531,543 @@ constexpr int64_t NA_WORDS = na_up(NA_OFF_SERE + NA_ROWS * SER_NB * (SEG / 2));
 static_assert(sizeof(CtlRow) % 8 == 0, "CtlRow packs into u64 words");
 static_assert(NA_WORDS * 8 == XS_NOALLOC_BYTES, "XS_NOALLOC_BYTES states the array's size");
 
+// ---------------------------------------------------------------------------
+// The whole-row path: rows whose candidate set is larger than the streaming
+// selection holds -- top_k of 128 or more, and top_k >= enc, the reference's
+// candidate_set branch that sorts the whole row (sampler.rs:322-338), which is
+// xwen's only top-p-only mode because top_k <= 1 means greedy.  The row's
+// finalizer leaves its max and softmax denominator in big_state; then, on the
+// row's tiles of BTILE ids (one workgroup each):
+//   big_key_kernel      p = rn(exp(s - max) / S) of every id (the selection
+//                       path's correctly rounded f32 arithmetic) as a sort key
+//                       that ascends as p descends, with the id, in id order;
+//                       the tile's counts of the first digit, which the row's
+//                       last tile turns into every tile's first positions;
+//   big_scatter_kernel  one pass of a stable LSD radix sort (RB-bit digits,
+//                       RPASS passes): each tile places its entries at those
+//                       positions, in order within the tile, so equal p keep
+//                       ascending ids -- the (p desc, id asc) order of
+//                       top_k_desc and of the stable whole-row sort;
+//   big_hist_kernel     the next pass's counts of the reordered tiles, and
+//                       their positions;
+//   big_draw_kernel     one workgroup per row: the first min(top_k, enc)
+//                       entries are the candidates; truncate_top_p
+//                       (sampler.rs:401-429) and WeightedIndex (:235-243,
+//                       rand 0.9) as the reference's serial f32 chains, each
+//                       evaluated by big_chain below.
+
+constexpr int RB = 8;               // radix bits per pass
+constexpr int RBINS = 1 << RB;      // digits per pass: one per thread
+constexpr int RPASS = 4;            // the sort keys have 31 bits
+constexpr int SPT = 4;              // slots per tile
+constexpr int BTILE = SPT * SLOT;   // ids per tile
+constexpr int EPL = BTILE / BLOCK;  // a lane's entries of a tile
+constexpr int QW = BTILE / NWAVE;   // a wave's quarter of a tile
+constexpr int CPT = 16;             // chain terms per thread and block
+constexpr int CBLK = CPT * BLOCK;   // chain terms per block
+constexpr int CHEAD = 128;          // chain terms added one at a time first
+static_assert(RBINS == BLOCK && EPL * 64 == QW, "one digit per thread; a wave's quarter in EPL steps");
+static_assert(SPC % SPT == 0, "tiles inside chunks");
+
+// The sort key of p >= +0: ascending as p descends.
+XS_DEV uint32_t pkey(float p) { return 0x7FFFFFFFu - __float_as_uint(p + 0.0f); }
+XS_DEV float pkey_p(uint32_t k) { return __uint_as_float(0x7FFFFFFFu - k); }
+XS_DEV uint32_t rdigit(uint32_t k, int pass) { return (k >> (RB * pass)) & (uint32_t)(RBINS - 1); }
+
+// The lanes whose digit d equals this lane's, among the lanes with `valid`
+// (meaningless on the others).  Wave-uniform control flow only.
+XS_DEV uint64_t digit_peers(uint32_t d, bool valid) {
+  uint64_t m = __ballot(valid);
+#pragma unroll
+  for (int b = 0; b < RB; b++) {
+    const bool bit = (d >> b) & 1u;
+    const uint64_t bb = __ballot(valid && bit);
+    m &= bit ? bb : ~bb;
+  }
+  return m;
+}
+XS_DEV uint64_t lanes_below() { return (1ull << lane_id()) - 1ull; }
+// Count this lane's digit once per group of equal digits (the group's lowest lane).
+XS_DEV void count_digit(uint32_t* cnt, uint32_t d, bool valid) {
+  const uint64_t pe = digit_peers(d, valid);
+  if (valid && (pe & lanes_below()) == 0) atomicAdd(&cnt[d], (uint32_t)__popcll(pe));
+}
+
+// The row's whole-row state for the kernels below: null when the call does not
+// draw the row on this path.
+XS_DEV const BigRow* big_live(const Args& a, int row, Cfg& cfg) {
+  cfg = a.greedy_all ? greedy_cfg() : make_cfg(a.params[row], a.enc, a.n_top, a.k_max);
+  if (!cfg.big || cfg.bad) return nullptr;  // (then big_state[row] is not this call's)
+  const BigRow* br = a.big_state + row;
+  return br->state ? br : nullptr;
+}
+
+// A tile's digit counts `c` (thread t: digit t) go out; the row's last tile to
+// arrive (an arrival ticket, as in sample_kernel's hand-off) turns every
+// tile's counts into the tile's first position of each digit, in place:
+// digits ascending, and within a digit the tiles in order.
+XS_DEV void big_counts(const Args& a, int row, int tile, uint32_t c, int32_t* s4, int32_t& last) {
+  int32_t* const H = reinterpret_cast<int32_t*>(a.big_hist) + (int64_t)row * a.big_hld;
+  const int tid = threadIdx.x, nt = a.big_tiles;
+  st_agent(&H[(int64_t)tile * RBINS + tid], (int32_t)c);
+  drain();
+  __syncthreads();
+  if (tid == 0) {
+    const int t = __hip_atomic_fetch_add(&a.big_ticket[row * TSTRIDE], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last = (t == nt - 1) ? 1 : 0;
+    if (t == nt - 1) st_agent(&a.big_ticket[row * TSTRIDE], 0);
+  }
+  __syncthreads();
+  if (!last) return;
+  constexpr int U = 16;
+  uint32_t tot = 0;
+#pragma unroll 1
+  for (int t0 = 0; t0 < nt; t0 += U) {
+    int32_t v[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) v[u] = t0 + u < nt ? ld_agent(&H[(int64_t)(t0 + u) * RBINS + tid]) : 0;
+#pragma unroll
+    for (int u = 0; u < U; u++) tot += (uint32_t)v[u];
+  }
+  int total;
+  uint32_t pos = (uint32_t)block_excl_scan((int)tot, s4, &total);
+#pragma unroll 1
+  for (int t0 = 0; t0 < nt; t0 += U) {
+    int32_t v[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) v[u] = t0 + u < nt ? ld_agent(&H[(int64_t)(t0 + u) * RBINS + tid]) : 0;
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      if (t0 + u < nt) H[(int64_t)(t0 + u) * RBINS + tid] = (int32_t)pos;
+      pos += (uint32_t)v[u];
+    }
+  }
+}
+
+// Grid: rows x big_tiles.  The sort keys of the tile's ids and the first
+// pass's digit counts.
+template <bool HAS_MASK, bool HAS_CTL>
+__global__ __launch_bounds__(BLOCK) void big_key_kernel(Args a) {
+  __shared__ double expt[64];
+  __shared__ uint32_t hist[RBINS];
+  __shared__ int32_t s4[NWAVE];
+  __shared__ int32_t last;
+  const int row = blockIdx.x / a.big_tiles, tile = blockIdx.x % a.big_tiles;
+  Cfg cfg;
+  const BigRow* br = big_live(a, row, cfg);
+  if (!br) return;
+  const float m_s = br->m_s, S = br->S;
+  const int tid = threadIdx.x;
+  const int enc = (int)a.enc;
+  const float* rowp = a.logits + (int64_t)row * a.ld;
+  const uint32_t* mrow = HAS_MASK ? a.allowed + (int64_t)row * a.allowed_ld : nullptr;
+  const int fmax = (enc - 1) >> 2;
+  const int s0 = tile * SPT;
+  const int ns = min(SPT, a.nslots - s0);
+  float4 q[SPT];
+  uint32_t mw[SPT];
+#pragma unroll
+  for (int j = 0; j < SPT; j++) {
+    const int f = min((s0 + j) * BLOCK + tid, fmax);
+    q[j] = reinterpret_cast<const float4*>(rowp)[f];
+    mw[j] = HAS_MASK ? mrow[f >> 3] : 0xFFFFFFFFu;
+  }
+  CtlRow cr{};
+  const uint64_t* pl = nullptr;
+  int pc = 0, phi = 0;
+  if (HAS_CTL) {
+    // the chunk's patches from its first (ctl_slot passes over earlier slots')
+    const int chunk = s0 / SPC;
+    cr = a.ctl_row[row];
+    pl = a.patch + (int64_t)row * a.ctl_cap;
+    pc = a.ctl_chunk[(int64_t)row * (a.n_chunks + 1) + chunk];
+    phi = a.ctl_chunk[(int64_t)row * (a.n_chunks + 1) + chunk + 1];
+  }
+  const bool ctl_on = HAS_CTL && cr.active;
+  if (tid < 64) expt[tid] = (&kExpT[0][0])[tid];
+  hist[tid] = 0u;
+  __syncthreads();
+  uint64_t* const A = a.big + (int64_t)row * 2 * a.big_ld;
+#pragma unroll
+  for (int j = 0; j < SPT; j++) {
+    if (j >= ns) break;  // (uniform)
+    const int sb = (s0 + j) * SLOT;
+    const int id0 = sb + 4 * tid;
+    float x[4] = {q[j].x, q[j].y, q[j].z, q[j].w};
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      if (id0 + e >= enc) x[e] = -INFINITY;
+      else if (HAS_MASK && !((mw[j] >> ((id0 + e) & 31)) & 1u)) x[e] = -INFINITY;
+    }
+    if (ctl_on) ctl_slot(x, sb, tid, pl, pc, phi, cr.pull_id, cr.pull_val, cr.force_id, cr.force_val);
+    uint32_t k[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      k[e] = pkey(exact_p(x[e], cfg, m_s, S, expt));
+      count_digit(hist, rdigit(k[e], 0), id0 + e < enc);
+    }
+    if (id0 + 3 < enc) {
+#pragma unroll
+      for (int e = 0; e < 4; e++) A[id0 + e] = ((uint64_t)k[e] << 32) | (uint32_t)(id0 + e);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; e++)
+        if (id0 + e < enc) A[id0 + e] = ((uint64_t)k[e] << 32) | (uint32_t)(id0 + e);
+    }
+  }
+  __syncthreads();
+  big_counts(a, row, tile, hist[tid], s4, last);
+}
+
+// Grid: rows x big_tiles.  Pass `pass`'s digit counts of the reordered tiles.
+__global__ __launch_bounds__(BLOCK) void big_hist_kernel(Args a, int pass) {
+  __shared__ uint32_t hist[RBINS];
+  __shared__ int32_t s4[NWAVE];
+  __shared__ int32_t last;
+  const int row = blockIdx.x / a.big_tiles, tile = blockIdx.x % a.big_tiles;
+  Cfg cfg;
+  if (!big_live(a, row, cfg)) return;
+  const int tid = threadIdx.x;
+  const int t0 = tile * BTILE, nt = min(BTILE, (int)a.enc - t0);
+  // the keys: the high words of the entries
+  const uint32_t* src = reinterpret_cast<const uint32_t*>(a.big + (int64_t)row * 2 * a.big_ld +
+                                                         ((pass & 1) ? a.big_ld : 0) + t0);
+  uint32_t k[EPL];
+#pragma unroll
+  for (int s = 0; s < EPL; s++) {
+    const int i = s * BLOCK + tid;
+    k[s] = i < nt ? src[2 * i + 1] : 0u;
+  }
+  hist[tid] = 0u;
+  __syncthreads();
+#pragma unroll
+  for (int s = 0; s < EPL; s++) count_digit(hist, rdigit(k[s], pass), s * BLOCK + tid < nt);
+  __syncthreads();
+  big_counts(a, row, tile, hist[tid], s4, last);
+}
+
+// One stable pass: the tile's entries go to their digit's place among all
+// tiles' (big_counts' first positions).  Each wave places a quarter of the
+// tile, in order, after the earlier quarters' entries of the same digit.
+// Grid: rows x big_tiles.
+__global__ __launch_bounds__(BLOCK) void big_scatter_kernel(Args a, int pass) {
+  __shared__ uint32_t cnt[NWAVE][RBINS];  // per wave: count, then next position
+  __shared__ uint64_t ent[NWAVE][QW];     // per wave: its quarter of the tile
+  const int row = blockIdx.x / a.big_tiles, tile = blockIdx.x % a.big_tiles;
+  Cfg cfg;
+  if (!big_live(a, row, cfg)) return;
+  const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
+  const int t0 = tile * BTILE, nt = min(BTILE, (int)a.enc - t0);
+  uint64_t* const A = a.big + (int64_t)row * 2 * a.big_ld;
+  const uint64_t* src = A + ((pass & 1) ? a.big_ld : 0) + t0;
+  uint64_t* dst = A + ((pass & 1) ? 0 : a.big_ld);
+  const uint32_t first = a.big_hist[(int64_t)row * a.big_hld + (int64_t)tile * RBINS + tid];
+  const int q0 = wave * QW;
+  {
+    uint64_t e[EPL];  // all of the quarter's loads in flight at once
+#pragma unroll
+    for (int s = 0; s < EPL; s++) {
+      const int i = q0 + s * 64 + lane;
+      e[s] = i < nt ? src[i] : 0ull;
+    }
+#pragma unroll
+    for (int s = 0; s < EPL; s++) ent[wave][s * 64 + lane] = e[s];
+  }
+  // each wave's count of every digit in its quarter
+#pragma unroll
+  for (int i = lane; i < RBINS; i += 64) cnt[wave][i] = 0u;
+  wave_lds_sync();
+#pragma unroll 1
+  for (int s = 0; s < EPL; s++) {
+    count_digit(cnt[wave], rdigit((uint32_t)(ent[wave][s * 64 + lane] >> 32), pass), q0 + s * 64 + lane < nt);
+    wave_lds_sync();
+  }
+  __syncthreads();
+  // each wave's first position of every digit (thread t: digit t)
+  uint32_t pos = first;
+#pragma unroll
+  for (int w = 0; w < NWAVE; w++) {
+    const uint32_t c = cnt[w][tid];
+    cnt[w][tid] = pos;
+    pos += c;
+  }
+  __syncthreads();
+  // the entries, in order
+#pragma unroll 1
+  for (int s = 0; s < EPL; s++) {
+    const bool valid = q0 + s * 64 + lane < nt;
+    const uint64_t e = ent[wave][s * 64 + lane];
+    const uint32_t d = rdigit((uint32_t)(e >> 32), pass);
+    const uint64_t pe = digit_peers(d, valid);
+    const uint32_t at = valid ? cnt[wave][d] : 0u;
+    const uint32_t p = at + (uint32_t)__popcll(pe & lanes_below());
+    if (valid && p < (uint32_t)a.enc) dst[p] = e;  // (always below enc when the counts are the tiles')
+    wave_lds_sync();
+    if (valid && (pe & lanes_below()) == 0) cnt[wave][d] = at + (uint32_t)__popcll(pe);
+    wave_lds_sync();
+  }
+}
+
+// 64-bit prefix sums over the block (in thread order); *total gets the sum.
+XS_DEV uint64_t wave_incl_scan64(uint64_t v) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint64_t t = __shfl_up(v, (unsigned)o, 64);
+    if (lane >= o) v += t;
+  }
+  return v;
+}
+XS_DEV uint64_t block_excl_scan64(uint64_t v, uint64_t* s4, uint64_t* total) {
+  const int lane = lane_id(), wave = wave_id();
+  const uint64_t inc = wave_incl_scan64(v);
+  if (lane == 63) s4[wave] = inc;
+  __syncthreads();
+  uint64_t pre = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < NWAVE; w++) {
+    const uint64_t t = s4[w];
+    pre += (w < wave) ? t : 0ull;
+    tot += t;
+  }
+  __syncthreads();
+  *total = tot;
+  return pre + inc - v;
+}
+
+struct ChainLds {
+  uint64_t s4[NWAVE];
+  int32_t stop;    // the block's first index that ends grid stepping
+  int32_t absorb;  // the block's last term rounds away at the block's grid
+  int32_t hit;
+  float acc;
+  float w1;
+};
+struct ChainOut {
+  float acc;  // the prefix sum through idx, or the whole sum when idx == n
+  int idx;    // the first index whose prefix sum reaches the target, or n
+};
+
+// The serial f32 sum acc_{i+1} = fl(acc_i + w_i) from acc_0 = acc0 over
+// terms w_0 >= w_1 >= ... >= 0 (term(i), i < n), as the reference's f32 loops
+// add them one at a time, and (mode 1) the first i whose prefix is >= thr, or
+// (mode 2) > thr.  The first CHEAD terms (the largest: the sum climbs through
+// most of its binades there) go one at a time, by one wave.  After them, while
+// the sum stays in one binade every addition lands on that binade's grid, so
+// it adds rn(w_i / grid) grid units (grid_units), independent of the others:
+// a block of CBLK terms then advances by an exact integer prefix sum.  Term
+// by term (the hardware f32 addition) go only a term that carries the sum
+// into the next binade and a term exactly half-way between grid points
+// (rounded to even, which depends on the sum before it).  The terms are
+// non-increasing, so once one rounds to no units, every later one does: the
+// sum is final.  Every thread of the block, uniform arguments.
+template <typename TERM>
+XS_DEV ChainOut big_chain(int n, float acc, int mode, float thr, TERM term, ChainLds& L) {
+  const int tid = threadIdx.x, lane = lane_id();
+  auto reached = [&](double c) __attribute__((always_inline)) { return mode == 1 ? c >= (double)thr : c > (double)thr; };
+  // 1. the head
+  const int nh = min(n, CHEAD);
+  if (wave_id() == 0) {
+    float s = acc;
+    int found = -1;
+#pragma unroll 1
+    for (int b = 0; b < nh && found < 0; b += 64) {
+      const float wl = b + lane < nh ? term(b + lane) : 0.0f;
+      const int m = min(64, nh - b);
+#pragma unroll 1
+      for (int u = 0; u < m; u++) {
+        s = s + rdlf(wl, u);
+        if (mode && reached((double)s)) {
+          found = b + u;
+          break;
+        }
+      }
+    }
+    if (lane == 0) {
+      L.acc = s;
+      L.hit = found;
+    }
+  }
+  __syncthreads();
+  acc = L.acc;
+  const int f = L.hit;
+  __syncthreads();
+  if (f >= 0) return ChainOut{acc, f};
+  // 2. blocks of CBLK terms, the next block's loaded ahead
+  float w[CPT], wn[CPT];
+  auto load = [&](float (&v)[CPT], int b0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int g = 0; g < CPT; g++) {
+      const int j = b0 + CPT * tid + g;
+      v[g] = j < n ? term(j) : 0.0f;
+    }
+  };
+  if (nh < n) load(wn, nh);
+#pragma unroll 1
+  for (int b0 = nh; b0 < n; b0 += CBLK) {
+    const int j0 = b0 + CPT * tid;
+    const int bend = min(n, b0 + CBLK);
+#pragma unroll
+    for (int g = 0; g < CPT; g++) w[g] = wn[g];
+    if (bend < n) load(wn, bend);
+    int start = b0;
+#pragma unroll 1
+    while (start < bend) {  // (uniform)
+      if (!(acc > 0.0f)) {
+        // a zero sum (from -0 or +0): the next term alone
+        if (j0 <= start && start < j0 + CPT) {
+#pragma unroll
+          for (int g = 0; g < CPT; g++)
+            if (j0 + g == start) L.w1 = w[g];
+        }
+        __syncthreads();
+        acc = acc + L.w1;
+        __syncthreads();
+        if (mode && reached((double)acc)) return ChainOut{acc, start};
+        if (!(acc > 0.0f)) return ChainOut{acc, n};  // every later term is 0 too
+        start++;
+        continue;
+      }
+      const int fa = f32_field(acc), F = max(fa, 1);
+      const uint64_t Ma = (__float_as_uint(acc) & 0x7FFFFFu) | (fa ? 0x800000u : 0u);
+      const double grid = __builtin_ldexp(1.0, F - 150);
+      uint32_t u[CPT];
+      uint32_t ties = 0;
+      uint64_t mysum = 0;
+#pragma unroll
+      for (int g = 0; g < CPT; g++) {
+        bool t;
+        const uint32_t v = grid_units(__float_as_uint(w[g]), F, t);
+        const bool live = j0 + g >= start && j0 + g < n;
+        u[g] = live ? v : 0u;
+        ties |= (live && t) ? (1u << g) : 0u;
+        mysum += u[g];
+      }
+      if (tid == 0) L.stop = 0x7FFFFFFF;
+      if (j0 <= bend - 1 && bend - 1 < j0 + CPT) {
+#pragma unroll
+        for (int g = 0; g < CPT; g++)
+          if (j0 + g == bend - 1) L.absorb = (u[g] == 0u && !((ties >> g) & 1u)) ? 1 : 0;
+      }
+      uint64_t tot;
+      const uint64_t ex = block_excl_scan64(mysum, L.s4, &tot);  // (its barriers order the stores above)
+      // this thread's first stop: a tie, a carry into the next binade, or the target
+      uint64_t run = Ma + ex;
+      int stop = 0x7FFFFFFF, sg = 0;
+      bool hit = false;
+#pragma unroll
+      for (int g = 0; g < CPT; g++) {
+        if (stop == 0x7FFFFFFF && j0 + g >= start && j0 + g < n) {
+          if (((ties >> g) & 1u) || run + u[g] >= (1ull << 24)) {
+            stop = j0 + g;
+            sg = g;
+          } else {
+            run += u[g];
+            if (mode && reached((double)run * grid)) {
+              stop = j0 + g;
+              sg = g;
+              hit = true;
+            }
+          }
+        }
+      }
+      if (stop != 0x7FFFFFFF) atomicMin(&L.stop, stop);
+      __syncthreads();
+      const int first = L.stop;
+      if (first == 0x7FFFFFFF) {
+        acc = (float)((double)(Ma + tot) * grid);  // exact: below the binade's end
+        const bool absorbed = L.absorb != 0;
+        __syncthreads();
+        if (absorbed) return ChainOut{acc, n};
+        break;
+      }
+      if (stop == first) {
+        // run: the units through the term before `first` (or through it, on a hit)
+        float nv;
+        bool h = hit;
+        if (hit) {
+          nv = (float)((double)run * grid);
+        } else {
+          float wv = 0.0f;
+#pragma unroll
+          for (int g = 0; g < CPT; g++) wv = g == sg ? w[g] : wv;
+          nv = (float)((double)run * grid) + wv;  // the reference's own addition
+          h = mode && reached((double)nv);
+        }
+        L.acc = nv;
+        L.hit = h ? 1 : 0;
+      }
+      __syncthreads();
+      acc = L.acc;
+      const bool h = L.hit != 0;
+      __syncthreads();
+      if (h) return ChainOut{acc, first};
+      start = first + 1;
+    }
+  }
+  return ChainOut{acc, n};
+}
+
+// Grid: rows.  The draw over the sorted row (big_chain for every serial sum).
+__global__ __launch_bounds__(BLOCK) void big_draw_kernel(Args a) {
+  __shared__ ChainLds L;
+  const int row = blockIdx.x;
+  Cfg cfg;
+  const BigRow* br = big_live(a, row, cfg);
+  if (!br) return;
+  const int tid = threadIdx.x;
+  const int kk = br->kk;
+  // (RPASS odd: the sorted row is in the second buffer)
+  const uint64_t* srt = a.big + (int64_t)row * 2 * a.big_ld + ((RPASS & 1) ? a.big_ld : 0);
+  auto pw = [&](int i) __attribute__((always_inline)) { return pkey_p((uint32_t)(srt[i] >> 32)); };
+  const bool renorm = !(cfg.top_p >= 1.0f);
+  int st = XS_ROW_OK;
+  float sum = 1.0f;
+  int keep = kk, tok = -1;
+  if (renorm) {
+    // sum of every candidate weight, folded from -0.0 as Rust's f32 Sum does
+    sum = big_chain(kk, -0.0f, 0, 0.0f, pw, L).acc;
+    if (!(sum > 0.0f)) st = XS_ROW_ZERO_WEIGHT;  // weights left unchanged: no mass to draw
+  }
+  if (st == XS_ROW_OK) {
+    // renormalised weights (or the raw ones at top_p >= 1), their serial prefix
+    // from 0 (truncate_top_p's cumsum, the same sums as WeightedIndex's
+    // cumulative weights) until the cut
+    auto ww = [&](int i) __attribute__((always_inline)) {
+      const float v = pw(i);
+      return renorm ? __fdiv_rn(v, sum) : v;
+    };
+    const ChainOut c = big_chain(kk, 0.0f, renorm ? 1 : 0, cfg.top_p, ww, L);
+    if (c.idx < kk) keep = c.idx + 1;
+    const float tot = c.acc;  // the prefix through keep - 1
+    if (!(tot > 0.0f)) {
+      st = XS_ROW_ZERO_WEIGHT;
+    } else {
+      // the index: the cumulative weights (prefix through i, i < keep - 1; the
+      // total from keep - 1 on) at or below x
+      const float x = a.uniforms[row] * tot + 0.0f;
+      const ChainOut d = big_chain(keep - 1, 0.0f, 2, x, ww, L);
+      tok = (int)(uint32_t)srt[d.idx < keep - 1 ? d.idx : keep - 1];
+    }
+  }
+  if (tid == 0) {
+    st_agent(&a.token[row], st == XS_ROW_OK ? tok : -1);
+    st_agent(&a.status[row], st);
+    if (a.n_cand) a.n_cand[row] = st == XS_ROW_OK ? kk : 0;
+  }
+  if (st == XS_ROW_OK && (a.cand_id || a.cand_w)) {
+    const int kw = (int)min((int64_t)kk, a.cand_ld);
+    for (int i = tid; i < kw; i += BLOCK) {
+      const uint64_t e = srt[i];
+      float v = pkey_p((uint32_t)(e >> 32));
+      if (renorm) v = i < keep ? __fdiv_rn(v, sum) : 0.0f;
+      if (a.cand_id) a.cand_id[(int64_t)row * a.cand_ld + i] = (int32_t)(uint32_t)e;
+      if (a.cand_w) a.cand_w[(int64_t)row * a.cand_ld + i] = v;
+    }
+  }
+  if (a.span > 0 && wave_id() == 0) verify_walk(a, row);
+}
+
 }  // namespace xs
 
 // The no-allocation entry point's workspace.  Each GPU holds its own copy at
@@ -3991,6 +4095,10 @@ struct xs_context {
   int32_t* row_ticket;  // [max_rows * TSTRIDE] arrival tickets, zero between calls
   int32_t* seq_ticket;  // [max_rows * TSTRIDE]
   uint64_t* big;        // [max_rows, 2, vocab] whole-row sort buffers (k_max > XS_K_MAX), or null
+  xs::BigRow* big_state;  // [max_rows] (with big)
+  uint32_t* big_hist;   // [max_rows, big_tiles_max, RBINS] (with big)
+  int32_t* big_ticket;  // [max_rows * TSTRIDE] (with big)
+  int32_t big_tiles_max;
   uint64_t* ser_sum;    // [max_rows, max_chunks * SPC * NWAVE, 2] serial_kernel's segment summaries
   uint64_t* ser_e;      // [max_rows, SER_NB, SEG / 2] its kept terms
 };
@@ -4006,7 +4114,8 @@ xs_host_limits limits_of(const xs_context* ctx) { return xs_host_limits{ctx->max
 // One sample_kernel launch over rows x n_chunks workgroups (it finalizes the
 // rows itself), or, for a large batch, sample_kernel then finalize_kernel; a
 // call with sparse controls runs control_kernel (one workgroup per row) first,
-// and one that can observe the serial denominator serial_kernel last.
+// one that can observe the serial denominator serial_kernel after them, and a
+// context sized for top_k >= 128 the whole-row kernels last.
 template <bool M, bool S, bool C>
 void launch2(xs_context* ctx, xs::Args& a, int64_t rows, dim3 g1, const int32_t* order) {
   // More workgroups than the GPU holds at once (4 per CU): the split launch,
@@ -4025,6 +4134,15 @@ void launch2(xs_context* ctx, xs::Args& a, int64_t rows, dim3 g1, const int32_t*
   }
   if (a.split) hipLaunchKernelGGL((xs::finalize_kernel<M, S, C>), dim3((unsigned)rows), dim3(xs::BLOCK), 0, ctx->stream, a);
   if ((M || C) && a.serial) hipLaunchKernelGGL((xs::serial_kernel<M, C>), g1, dim3(xs::BLOCK), 0, ctx->stream, a);
+  if (a.big && !a.greedy_all) {  // a context that serves top_k >= 128: the whole-row kernels (rows not drawn there return at once)
+    const dim3 gt((unsigned)(rows * a.big_tiles));
+    hipLaunchKernelGGL((xs::big_key_kernel<M, C>), gt, dim3(xs::BLOCK), 0, ctx->stream, a);
+    for (int pass = 0; pass < xs::RPASS; pass++) {
+      if (pass > 0) hipLaunchKernelGGL(xs::big_hist_kernel, gt, dim3(xs::BLOCK), 0, ctx->stream, a, pass);
+      hipLaunchKernelGGL(xs::big_scatter_kernel, gt, dim3(xs::BLOCK), 0, ctx->stream, a, pass);
+    }
+    hipLaunchKernelGGL(xs::big_draw_kernel, dim3((unsigned)rows), dim3(xs::BLOCK), 0, ctx->stream, a);
+  }
 }
 
 // order: null, or a host permutation of the rows (checked by the caller,
@@ -4047,6 +4165,11 @@ int launch(xs_context* ctx, xs::Args& a, int64_t rows, int span, bool mask, bool
   a.k_max = ctx->k_max;
   a.big = ctx->big;
   a.big_ld = ctx->vocab;
+  a.big_state = ctx->big_state;
+  a.big_hist = ctx->big_hist;
+  a.big_hld = (int64_t)ctx->big_tiles_max * xs::RBINS;
+  a.big_ticket = ctx->big_ticket;
+  a.big_tiles = (int32_t)((a.enc + xs::BTILE - 1) / xs::BTILE);
   a.serial = (serial && (mask || ctl)) ? 1 : 0;
   a.ser_sum = ctx->ser_sum;
   a.ser_e = ctx->ser_e;
@@ -4106,8 +4229,14 @@ int xs_create_ex(int device, int64_t max_rows, int64_t vocab, int32_t k_max, int
   const int64_t nseg = (int64_t)mc * xs::SPC * xs::NWAVE;
   ok = ok && hipMalloc((void**)&c->ser_sum, max_rows * nseg * 2 * sizeof(uint64_t)) == hipSuccess;
   ok = ok && hipMalloc((void**)&c->ser_e, max_rows * xs::SER_NB * (xs::SEG / 2) * sizeof(uint64_t)) == hipSuccess;
-  if (k_max > XS_K_MAX)  // top_k past the streaming selection: the whole-row path's buffers
+  if (k_max > XS_K_MAX) {  // top_k past the streaming selection: the whole-row path's buffers
     ok = ok && hipMalloc((void**)&c->big, (size_t)max_rows * 2 * vocab * sizeof(uint64_t)) == hipSuccess;
+    ok = ok && hipMalloc((void**)&c->big_state, (size_t)max_rows * sizeof(xs::BigRow)) == hipSuccess;
+    c->big_tiles_max = (int32_t)((vocab + xs::BTILE - 1) / xs::BTILE);
+    ok = ok && hipMalloc((void**)&c->big_hist, (size_t)max_rows * c->big_tiles_max * xs::RBINS * sizeof(uint32_t)) == hipSuccess;
+    ok = ok && hipMalloc((void**)&c->big_ticket, tbytes) == hipSuccess;
+    ok = ok && hipMemset(c->big_ticket, 0, tbytes) == hipSuccess;
+  }
   ok = ok && hipDeviceSynchronize() == hipSuccess;
   if (!ok) {
     xs_destroy(c);
@@ -4130,6 +4259,9 @@ int xs_destroy(xs_context* c) {
   (void)hipFree(c->row_ticket);
   (void)hipFree(c->seq_ticket);
   if (c->big) (void)hipFree(c->big);
+  if (c->big_state) (void)hipFree(c->big_state);
+  if (c->big_hist) (void)hipFree(c->big_hist);
+  if (c->big_ticket) (void)hipFree(c->big_ticket);
   (void)hipFree(c->ser_sum);
   (void)hipFree(c->ser_e);
   free(c);

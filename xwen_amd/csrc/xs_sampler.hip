@@ -3619,7 +3619,7 @@ XS_DEV void big_counts(const Args& a, int row, int tile, uint32_t c, int32_t* s4
   }
   __syncthreads();
   if (!last) return;
-  constexpr int U = 16;
+  constexpr int U = 64;  // (one round for rows of up to 262,144 ids)
   uint32_t tot = 0;
 #pragma unroll 1
   for (int t0 = 0; t0 < nt; t0 += U) {
@@ -3808,6 +3808,17 @@ __global__ __launch_bounds__(BLOCK) void big_scatter_kernel(Args a, int pass) {
   }
 }
 
+// A workgroup barrier for LDS traffic only: this wave's LDS operations done,
+// then s_barrier.  Unlike __syncthreads (a workgroup release fence, which on
+// this target waits for every outstanding vector memory operation) it leaves
+// global loads in flight, so a block's prefetched terms keep coming.
+XS_DEV void lds_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 // 64-bit prefix sums over the block (in thread order); *total gets the sum.
 XS_DEV uint64_t wave_incl_scan64(uint64_t v) {
   const int lane = lane_id();
@@ -3822,7 +3833,7 @@ XS_DEV uint64_t block_excl_scan64(uint64_t v, uint64_t* s4, uint64_t* total) {
   const int lane = lane_id(), wave = wave_id();
   const uint64_t inc = wave_incl_scan64(v);
   if (lane == 63) s4[wave] = inc;
-  __syncthreads();
+  lds_barrier();
   uint64_t pre = 0, tot = 0;
 #pragma unroll
   for (int w = 0; w < NWAVE; w++) {
@@ -3830,7 +3841,7 @@ XS_DEV uint64_t block_excl_scan64(uint64_t v, uint64_t* s4, uint64_t* total) {
     pre += (w < wave) ? t : 0ull;
     tot += t;
   }
-  __syncthreads();
+  lds_barrier();
   *total = tot;
   return pre + inc - v;
 }
@@ -3861,8 +3872,9 @@ struct ChainOut {
 // (rounded to even, which depends on the sum before it).  The terms are
 // non-increasing, so once one rounds to no units, every later one does: the
 // sum is final.  Every thread of the block, uniform arguments.
-template <typename TERM>
-XS_DEV ChainOut big_chain(int n, float acc, int mode, float thr, TERM term, ChainLds& L) {
+// The terms: conv(srt[i]), from the sorted entries.
+template <typename CONV>
+XS_DEV ChainOut big_chain(const uint64_t* srt, int n, float acc, int mode, float thr, CONV conv, ChainLds& L) {
   const int tid = threadIdx.x, lane = lane_id();
   auto reached = [&](double c) __attribute__((always_inline)) { return mode == 1 ? c >= (double)thr : c > (double)thr; };
   // 1. the head
@@ -3872,7 +3884,7 @@ XS_DEV ChainOut big_chain(int n, float acc, int mode, float thr, TERM term, Chai
     int found = -1;
 #pragma unroll 1
     for (int b = 0; b < nh && found < 0; b += 64) {
-      const float wl = b + lane < nh ? term(b + lane) : 0.0f;
+      const float wl = b + lane < nh ? conv(srt[b + lane]) : 0.0f;
       const int m = min(64, nh - b);
 #pragma unroll 1
       for (int u = 0; u < m; u++) {
@@ -3888,28 +3900,30 @@ XS_DEV ChainOut big_chain(int n, float acc, int mode, float thr, TERM term, Chai
       L.hit = found;
     }
   }
-  __syncthreads();
+  lds_barrier();
   acc = L.acc;
   const int f = L.hit;
-  __syncthreads();
+  lds_barrier();
   if (f >= 0) return ChainOut{acc, f};
-  // 2. blocks of CBLK terms, the next block's loaded ahead
-  float w[CPT], wn[CPT];
-  auto load = [&](float (&v)[CPT], int b0) __attribute__((always_inline)) {
+  // 2. blocks of CBLK terms, the next block's entries loaded ahead (converted
+  // only when their block starts, so that the loads stay in flight)
+  float w[CPT];
+  uint64_t rn[CPT];
+  auto load = [&](int b0) __attribute__((always_inline)) {
 #pragma unroll
     for (int g = 0; g < CPT; g++) {
       const int j = b0 + CPT * tid + g;
-      v[g] = j < n ? term(j) : 0.0f;
+      rn[g] = j < n ? srt[j] : 0ull;
     }
   };
-  if (nh < n) load(wn, nh);
+  if (nh < n) load(nh);
 #pragma unroll 1
   for (int b0 = nh; b0 < n; b0 += CBLK) {
     const int j0 = b0 + CPT * tid;
     const int bend = min(n, b0 + CBLK);
 #pragma unroll
-    for (int g = 0; g < CPT; g++) w[g] = wn[g];
-    if (bend < n) load(wn, bend);
+    for (int g = 0; g < CPT; g++) w[g] = j0 + g < n ? conv(rn[g]) : 0.0f;
+    if (bend < n) load(bend);
     int start = b0;
 #pragma unroll 1
     while (start < bend) {  // (uniform)
@@ -3920,9 +3934,9 @@ XS_DEV ChainOut big_chain(int n, float acc, int mode, float thr, TERM term, Chai
           for (int g = 0; g < CPT; g++)
             if (j0 + g == start) L.w1 = w[g];
         }
-        __syncthreads();
+        lds_barrier();
         acc = acc + L.w1;
-        __syncthreads();
+        lds_barrier();
         if (mode && reached((double)acc)) return ChainOut{acc, start};
         if (!(acc > 0.0f)) return ChainOut{acc, n};  // every later term is 0 too
         start++;
@@ -3951,13 +3965,17 @@ XS_DEV ChainOut big_chain(int n, float acc, int mode, float thr, TERM term, Chai
       }
       uint64_t tot;
       const uint64_t ex = block_excl_scan64(mysum, L.s4, &tot);  // (its barriers order the stores above)
-      // this thread's first stop: a tie, a carry into the next binade, or the target
+      // this thread's first stop: a tie, a carry into the next binade, or the
+      // target (none when its terms hold no tie and its end stays below both:
+      // the prefix only grows)
       uint64_t run = Ma + ex;
       int stop = 0x7FFFFFFF, sg = 0;
       bool hit = false;
+      const bool calm = ties == 0u && run + mysum < (1ull << 24) &&
+                        !(mode && reached((double)(run + mysum) * grid));
 #pragma unroll
       for (int g = 0; g < CPT; g++) {
-        if (stop == 0x7FFFFFFF && j0 + g >= start && j0 + g < n) {
+        if (!calm && stop == 0x7FFFFFFF && j0 + g >= start && j0 + g < n) {
           if (((ties >> g) & 1u) || run + u[g] >= (1ull << 24)) {
             stop = j0 + g;
             sg = g;
@@ -3972,12 +3990,12 @@ XS_DEV ChainOut big_chain(int n, float acc, int mode, float thr, TERM term, Chai
         }
       }
       if (stop != 0x7FFFFFFF) atomicMin(&L.stop, stop);
-      __syncthreads();
+      lds_barrier();
       const int first = L.stop;
       if (first == 0x7FFFFFFF) {
         acc = (float)((double)(Ma + tot) * grid);  // exact: below the binade's end
         const bool absorbed = L.absorb != 0;
-        __syncthreads();
+        lds_barrier();
         if (absorbed) return ChainOut{acc, n};
         break;
       }
@@ -3997,10 +4015,10 @@ XS_DEV ChainOut big_chain(int n, float acc, int mode, float thr, TERM term, Chai
         L.acc = nv;
         L.hit = h ? 1 : 0;
       }
-      __syncthreads();
+      lds_barrier();
       acc = L.acc;
       const bool h = L.hit != 0;
-      __syncthreads();
+      lds_barrier();
       if (h) return ChainOut{acc, first};
       start = first + 1;
     }
@@ -4019,25 +4037,25 @@ __global__ __launch_bounds__(BLOCK) void big_draw_kernel(Args a) {
   const int kk = br->kk;
   // (RPASS odd: the sorted row is in the second buffer)
   const uint64_t* srt = a.big + (int64_t)row * 2 * a.big_ld + ((RPASS & 1) ? a.big_ld : 0);
-  auto pw = [&](int i) __attribute__((always_inline)) { return pkey_p((uint32_t)(srt[i] >> 32)); };
+  auto pw = [&](uint64_t e) __attribute__((always_inline)) { return pkey_p((uint32_t)(e >> 32)); };
   const bool renorm = !(cfg.top_p >= 1.0f);
   int st = XS_ROW_OK;
   float sum = 1.0f;
   int keep = kk, tok = -1;
   if (renorm) {
     // sum of every candidate weight, folded from -0.0 as Rust's f32 Sum does
-    sum = big_chain(kk, -0.0f, 0, 0.0f, pw, L).acc;
+    sum = big_chain(srt, kk, -0.0f, 0, 0.0f, pw, L).acc;
     if (!(sum > 0.0f)) st = XS_ROW_ZERO_WEIGHT;  // weights left unchanged: no mass to draw
   }
   if (st == XS_ROW_OK) {
     // renormalised weights (or the raw ones at top_p >= 1), their serial prefix
     // from 0 (truncate_top_p's cumsum, the same sums as WeightedIndex's
     // cumulative weights) until the cut
-    auto ww = [&](int i) __attribute__((always_inline)) {
-      const float v = pw(i);
+    auto ww = [&](uint64_t e) __attribute__((always_inline)) {
+      const float v = pw(e);
       return renorm ? __fdiv_rn(v, sum) : v;
     };
-    const ChainOut c = big_chain(kk, 0.0f, renorm ? 1 : 0, cfg.top_p, ww, L);
+    const ChainOut c = big_chain(srt, kk, 0.0f, renorm ? 1 : 0, cfg.top_p, ww, L);
     if (c.idx < kk) keep = c.idx + 1;
     const float tot = c.acc;  // the prefix through keep - 1
     if (!(tot > 0.0f)) {
@@ -4046,7 +4064,7 @@ __global__ __launch_bounds__(BLOCK) void big_draw_kernel(Args a) {
       // the index: the cumulative weights (prefix through i, i < keep - 1; the
       // total from keep - 1 on) at or below x
       const float x = a.uniforms[row] * tot + 0.0f;
-      const ChainOut d = big_chain(keep - 1, 0.0f, 2, x, ww, L);
+      const ChainOut d = big_chain(srt, keep - 1, 0.0f, 2, x, ww, L);
       tok = (int)(uint32_t)srt[d.idx < keep - 1 ? d.idx : keep - 1];
     }
   }

@@ -130,7 +130,7 @@ def calibrate_copy(nbytes: int, reps: int) -> None:
                       "launches": reps}), flush=True)
 
 
-def setup(name, nbuf, dev, torch, workloads, xsm, _lib, lib) -> dict:
+def setup(name, nbuf, dev, torch, workloads, xsm, _lib, lib, k_max=None) -> dict:
     """Build one workload's inputs (resident in HBM, `nbuf` rotating copies)
     and its launch.  c2 is the headline configuration; c3-c5 are the other
     measured configurations of the path."""
@@ -139,14 +139,19 @@ def setup(name, nbuf, dev, torch, workloads, xsm, _lib, lib) -> dict:
 
     log(f"generating the {name} workload")
     wl = {"c1": workloads.c1_single, "c1g": lambda: workloads.c1_single(greedy=True),
-          "c2": workloads.c2_batch, "c3": workloads.c3_masked, "c3p1": workloads.c3_masked,
+          "c2": workloads.c2_batch, "c2w": workloads.c2_batch, "c3": workloads.c3_masked,
+          "c3p1": workloads.c3_masked,
           "c4": workloads.c4_verify, "c5": workloads.c5_heterogeneous}[name]()
     if name == "c3p1":  # C3 at top_p = 1: the serial denominator reaches the weights
         wl.top_p = np.ones_like(wl.top_p)
+    if name == "c2w":  # C2 with top_k >= V: the whole-row (top-p-only) path
+        wl.top_k = np.full_like(wl.top_k, 2**31 - 1)
     if name in ("c1", "c1g"):  # one 1 MB row: rotate enough copies to leave the Infinity Cache
         nbuf = max(nbuf, 300)
     rows, V = wl.logits.shape
-    ctx = xsm.Context(max_rows=rows, vocab=V)
+    if k_max is None and name == "c2w":
+        k_max = 2**31 - 1
+    ctx = xsm.Context(max_rows=rows, vocab=V, **({} if k_max is None else {"k_max": k_max}))
     base = torch.as_tensor(wl.logits).to(dev)
     bufs = [base if i == 0 else base.clone() for i in range(nbuf)]
     params = xsm.params_tensor(wl.temperature, wl.top_k, wl.top_p, rows, dev)
@@ -244,6 +249,8 @@ WORKLOAD_TEXT = {
            "300 rotating copies)",
     "c2": "C2 batched sampling: 64 rows x V=248,320 fp32, T 0.7 / top_k 20 / top_p 0.80, "
           "one uniform per row",
+    "c2w": "C2 rows with top_k >= V, the whole-row (top-p-only) path: 64 rows x V=248,320 fp32, "
+           "T 0.7 / top_p 0.80, the candidate set the whole row sorted by (p desc, id asc)",
     "c3": "C3 grammar-constrained sampling: 32 rows x V=248,320 fp32 + packed u32 allow-masks "
           "(1% / 10% / 50% dense, one one-hot), T 1.0 / top_k 20 / top_p 0.95",
     "c3p1": "C3 at top_p 1.0 with the top-20 candidate list and the softmax denominator: the "
@@ -268,8 +275,11 @@ def main() -> int:
                     help="rows the CPU baseline samples at once (one per thread); 0 = the "
                          "host cores of this process's share (at most 16)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="BYTES")
-    ap.add_argument("--workload", choices=["c1", "c1g", "c2", "c3", "c3p1", "c4", "c5"], default="c2",
+    ap.add_argument("--workload", choices=["c1", "c1g", "c2", "c2w", "c3", "c3p1", "c4", "c5"], default="c2",
                     help="c2 (default) is the headline configuration; c1/c1g one row (latency)")
+    ap.add_argument("--k-max", type=int, default=None,
+                    help="the context's k_max (default: 127, or INT32_MAX for c2w); above 127 every "
+                         "call also launches the whole-row kernels")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path "
@@ -290,7 +300,7 @@ def main() -> int:
 
     dev = torch.device("cuda:0")
     lib = _lib.load()
-    S = setup(args.workload, args.nbuf, dev, torch, workloads, xsm, _lib, lib)
+    S = setup(args.workload, args.nbuf, dev, torch, workloads, xsm, _lib, lib, args.k_max)
     wl, rows, ctx, step, outs, alg_bytes = S["wl"], S["rows"], S["ctx"], S["step"], S["outs"], S["alg_bytes"]
     V = wl.logits.shape[1]
 
@@ -362,6 +372,8 @@ def main() -> int:
 
     headline = args.workload == "c2"
     config = {"workload": WORKLOAD_TEXT[args.workload], "rows": rows, "vocab": V}
+    if args.k_max is not None:
+        config["k_max"] = args.k_max
     if headline:
         config.update({"temperature": 0.7, "top_k": 20, "top_p": 0.8})
     config.update({"launch": "hipGraph" if graph is not None else "eager",

@@ -73,7 +73,8 @@ extern "C" {
  * A context created with k_max above it serves every top_k up to k_max --
  * top_k >= enc included, the reference's whole-row candidate set
  * (sampler.rs:322-338) -- through the whole-row path: every probability,
- * a (p desc, id asc) sort of the row and the serial f32 top-p and draw. */
+ * a (p desc, id asc) sort of the row and the serial f32 top-p and draw, in
+ * kernels of their own after the row's finalizer. */
 #define XS_K_MAX 127
 /* Largest number of held_row log-probs per row. */
 #define XS_TOP_MAX 128
@@ -94,7 +95,11 @@ typedef struct {
  * rows of up to `vocab` encodable ids (<= 1,048,576) and min(top_k, enc) <=
  * k_max (any k_max >= 0; the reference's top_k is an unbounded usize, and
  * INT32_MAX serves every top_k).  k_max above XS_K_MAX adds the whole-row
- * path's buffers, 16 bytes per row and id (32 MB for 8 rows of 248,320).
+ * path's buffers, 16 bytes per row and id plus 1 KiB per row and 4,096 ids
+ * (33 MB for 8 rows of 248,320), and every sampling call on such a context
+ * then launches the whole-row kernels too (rows that do not take that path
+ * return at once: about 25 us more per call when no row does; create a
+ * context with k_max <= XS_K_MAX for traffic that never asks for more).
  * Allocates the device workspace once; calls allocate nothing afterwards. */
 int xs_create(int device, int64_t max_rows, int64_t vocab, int32_t k_max, xs_context** out);
 

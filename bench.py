@@ -130,7 +130,7 @@ def calibrate_copy(nbytes: int, reps: int) -> None:
                       "launches": reps}), flush=True)
 
 
-def setup(name, nbuf, dev, torch, workloads, xsm, _lib, lib, k_max=None) -> dict:
+def setup(name, nbuf, dev, torch, workloads, xsm, _lib, lib, k_max=None, call_k_max=0) -> dict:
     """Build one workload's inputs (resident in HBM, `nbuf` rotating copies)
     and its launch.  c2 is the headline configuration; c3-c5 are the other
     measured configurations of the path."""
@@ -170,6 +170,7 @@ def setup(name, nbuf, dev, torch, workloads, xsm, _lib, lib, k_max=None) -> dict
             a = _lib.VerifyArgs()
             a.logits = bufs[i].data_ptr()
             a.seqs, a.span, a.ld, a.width, a.enc = wl.seqs, wl.span, V, V, V
+            a.k_max = call_k_max
             a.params, a.uniforms, a.drafts = params.data_ptr(), u.data_ptr(), drafts.data_ptr()
             a.row_token, a.row_status = outs[i].row_token.data_ptr(), outs[i].row_status.data_ptr()
             a.accepted, a.committed = outs[i].accepted.data_ptr(), outs[i].committed.data_ptr()
@@ -204,6 +205,7 @@ def setup(name, nbuf, dev, torch, workloads, xsm, _lib, lib, k_max=None) -> dict
             a = _lib.SampleArgs()
             a.logits = bufs[i].data_ptr()
             a.rows, a.ld, a.width, a.enc = rows, V, V, V
+            a.k_max = call_k_max
             a.params, a.uniforms = params.data_ptr(), u.data_ptr()
             a.token, a.status = outs[i].token.data_ptr(), outs[i].status.data_ptr()
             if "mask" in extra:
@@ -280,6 +282,9 @@ def main() -> int:
     ap.add_argument("--k-max", type=int, default=None,
                     help="the context's k_max (default: 127, or INT32_MAX for c2w); above 127 every "
                          "call also launches the whole-row kernels")
+    ap.add_argument("--call-k-max", type=int, default=0,
+                    help="the calls' own bound on min(top_k, enc) (xs_sample_args.k_max; 0 = the "
+                         "context's): 127 or less leaves the whole-row kernels out")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path "
@@ -300,7 +305,7 @@ def main() -> int:
 
     dev = torch.device("cuda:0")
     lib = _lib.load()
-    S = setup(args.workload, args.nbuf, dev, torch, workloads, xsm, _lib, lib, args.k_max)
+    S = setup(args.workload, args.nbuf, dev, torch, workloads, xsm, _lib, lib, args.k_max, args.call_k_max)
     wl, rows, ctx, step, outs, alg_bytes = S["wl"], S["rows"], S["ctx"], S["step"], S["outs"], S["alg_bytes"]
     V = wl.logits.shape[1]
 
@@ -374,6 +379,8 @@ def main() -> int:
     config = {"workload": WORKLOAD_TEXT[args.workload], "rows": rows, "vocab": V}
     if args.k_max is not None:
         config["k_max"] = args.k_max
+    if args.call_k_max:
+        config["call_k_max"] = args.call_k_max
     if headline:
         config.update({"temperature": 0.7, "top_k": 20, "top_p": 0.8})
     config.update({"launch": "hipGraph" if graph is not None else "eager",

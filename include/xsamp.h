@@ -98,8 +98,8 @@ typedef struct {
  * path's buffers, 16 bytes per row and id plus 1 KiB per row and 4,096 ids
  * (33 MB for 8 rows of 248,320), and every sampling call on such a context
  * then launches the whole-row kernels too (rows that do not take that path
- * return at once: about 25 us more per call when no row does; create a
- * context with k_max <= XS_K_MAX for traffic that never asks for more).
+ * return at once: about 25 us more per call when no row does), unless the
+ * call bounds its own top_k at XS_K_MAX or less (xs_sample_args.k_max).
  * Allocates the device workspace once; calls allocate nothing afterwards. */
 int xs_create(int device, int64_t max_rows, int64_t vocab, int32_t k_max, xs_context** out);
 
@@ -208,6 +208,13 @@ typedef struct {
    * XS_ERR_ARG.  No counterpart in the reference, which samples one row at a
    * time. */
   const int32_t* row_order;
+  /* A bound on min(top_k, enc) for this call, or 0 for the context's k_max:
+   * rows above it report XS_ROW_BAD_PARAM, and a bound of XS_K_MAX or less
+   * leaves out the whole-row kernels on a context sized for more, which
+   * otherwise run on every call.  No counterpart in the reference, whose
+   * options are per row: a caller batching rows of several top_k passes the
+   * largest min(top_k, enc) among them. */
+  int32_t k_max;
 } xs_sample_args;
 #define XS_ORDER_MAX 1024
 
@@ -269,6 +276,8 @@ typedef struct {
    * accepted, so the caller computes these, with the per-position masks,
    * by stepping a copy of its grammar state along the drafts. */
   const uint8_t* done_after;
+  /* as xs_sample_args.k_max */
+  int32_t k_max;
 } xs_verify_args;
 
 int xs_verify(xs_context* ctx, const xs_verify_args* args);

@@ -51,6 +51,7 @@ int main(void) {
   F(xs_row_control, n_bias); F(xs_row_control, pull_alpha); F(xs_row_control, force_id);
   F(xs_sample_args, controls); F(xs_sample_args, ctl_delta);
   F(xs_verify_args, controls); F(xs_verify_args, ctl_delta); F(xs_verify_args, done_after);
+  F(xs_sample_args, row_order); F(xs_sample_args, k_max); F(xs_verify_args, k_max);
   return 0;
 }
 ''')

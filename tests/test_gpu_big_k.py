@@ -153,3 +153,28 @@ def test_head_selection_tie_groups(bigctx, oracle):
     assert (d["status"] == 0).all(), d["status"]
     assert list(d["n_cand"]) == list(K)
     check_rows(oracle, x, T, K, P, U, d, mask=mask, label="head ties")
+
+
+def test_a_call_bounds_its_own_top_k(bigctx, oracle):
+    """xs_sample_args.k_max (no counterpart in the reference) bounds one call
+    below the context's k_max: rows above it report XS_ROW_BAD_PARAM, rows
+    within it draw exactly as without the bound, and a bound of 127 or less
+    leaves the whole-row kernels out of the call."""
+    x, rng = _rows(12128, 6)
+    K = np.array([20, 100, 127, 2, 500, 128])
+    T, P = 1.0, 0.9
+    U = workloads.uniforms(rng, 6)
+    full = run_sample(bigctx, x, T, K, P, U, cand_k=600)
+    assert (full["status"] == 0).all(), full["status"]
+    check_rows(oracle, x, T, K, P, U, full, label="unbounded call")
+    for bound, ok in ((127, [True, True, True, True, False, False]), (600, [True] * 6), (500, [True] * 6)):
+        d = run_sample(bigctx, x, T, K, P, U, cand_k=600, k_max=bound)
+        for r in range(6):
+            if ok[r]:
+                assert d["status"][r] == 0 and d["token"][r] == full["token"][r], (bound, r)
+                n = int(d["n_cand"][r])
+                assert n == full["n_cand"][r], (bound, r)
+                assert (d["cand_id"][r, :n] == full["cand_id"][r, :n]).all(), (bound, r)
+                assert (d["cand_w"][r, :n] == full["cand_w"][r, :n]).all(), (bound, r)
+            else:
+                assert d["status"][r] == 7 and d["token"][r] == -1, (bound, r)  # XS_ROW_BAD_PARAM

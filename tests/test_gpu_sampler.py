@@ -61,7 +61,7 @@ def dev(x):
 
 
 def run_sample(ctx, logits, T, K, P, U, *, enc=None, width=None, mask=None, mask_words=None,
-               cand_k=128, n_top=0, ctls=None):
+               cand_k=128, n_top=0, ctls=None, k_max=0):
     """One xs_sample call; `ctls` is one SampleControl (sparse part) or None per row."""
     from xwen_amd import sampler as xsm
     rows = logits.shape[0]
@@ -72,7 +72,7 @@ def run_sample(ctx, logits, T, K, P, U, *, enc=None, width=None, mask=None, mask
     controls = None if ctls is None else xsm.controls_tensor(ctls, "cuda")
     out = xsm.sample_batch(ctx, lg, p, u, enc=enc, width=width, allowed=m,
                            allowed_words=mask_words, cand_k=cand_k, stats=True, n_top=n_top,
-                           controls=controls)
+                           controls=controls, k_max=k_max)
     torch.cuda.synchronize()
     return {k: (None if v is None else v.cpu().numpy()) for k, v in vars(out).items()}
 

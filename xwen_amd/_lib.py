@@ -55,6 +55,7 @@ class SampleArgs(C.Structure):
         ("top_logprob", _vp), ("top_ld", _i64),
         ("controls", _vp), ("ctl_ids", _vp), ("ctl_delta", _vp),
         ("row_order", _vp),  # host array [rows] (int32), or NULL
+        ("k_max", _i32),     # this call's bound on min(top_k, enc), 0 = the context's
     ]
 
 
@@ -67,6 +68,7 @@ class VerifyArgs(C.Structure):
         ("row_token", _vp), ("row_status", _vp), ("accepted", _vp), ("committed", _vp),
         ("n_committed", _vp), ("seq_status", _vp),
         ("controls", _vp), ("ctl_ids", _vp), ("ctl_delta", _vp), ("done_after", _vp),
+        ("k_max", _i32),
     ]
 
 

@@ -41,6 +41,7 @@ int xs_host_check_sample(const xs_host_limits* lim, const xs_sample_args* in) {
                               in->uniforms, in->allowed, in->allowed_words, in->allowed_ld);
   if (rc) return rc;
   if ((in->cand_id || in->cand_w) && in->cand_ld < 1) return XS_ERR_ARG;
+  if (in->k_max < 0) return XS_ERR_ARG;
   if (in->n_top < 0 || in->n_top > XS_TOP_MAX) return XS_ERR_ARG;
   if ((in->top_id || in->top_logprob) && in->top_ld < in->n_top) return XS_ERR_ARG;
   const bool lse = in->row_max || in->row_lse || in->top_id || in->top_logprob;
@@ -61,7 +62,7 @@ int xs_host_check_verify(const xs_host_limits* lim, const xs_verify_args* in) {
   if (!lim || !in || !in->row_token || !in->row_status || !in->accepted || !in->committed ||
       !in->n_committed || !in->seq_status)
     return XS_ERR_ARG;
-  if (in->seqs < 0 || in->span < 1 || in->n_eog < 0 || in->n_eog > 8) return XS_ERR_ARG;
+  if (in->seqs < 0 || in->span < 1 || in->n_eog < 0 || in->n_eog > 8 || in->k_max < 0) return XS_ERR_ARG;
   if (in->span > 1 && !in->drafts) return XS_ERR_ARG;
   if (in->seqs > INT64_MAX / in->span) return XS_ERR_CAPACITY;
   return check_common(lim, in->logits, in->seqs * in->span, in->ld, in->width, in->enc, in->params,

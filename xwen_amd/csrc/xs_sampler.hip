@@ -4152,7 +4152,9 @@ void launch2(xs_context* ctx, xs::Args& a, int64_t rows, dim3 g1, const int32_t*
   }
   if (a.split) hipLaunchKernelGGL((xs::finalize_kernel<M, S, C>), dim3((unsigned)rows), dim3(xs::BLOCK), 0, ctx->stream, a);
   if ((M || C) && a.serial) hipLaunchKernelGGL((xs::serial_kernel<M, C>), g1, dim3(xs::BLOCK), 0, ctx->stream, a);
-  if (a.big && !a.greedy_all) {  // a context that serves top_k >= 128: the whole-row kernels (rows not drawn there return at once)
+  // a call that may hold top_k >= 128 on a context sized for it: the
+  // whole-row kernels (rows not drawn there return at once)
+  if (a.big && !a.greedy_all && a.k_max > XS_K_MAX) {
     const dim3 gt((unsigned)(rows * a.big_tiles));
     hipLaunchKernelGGL((xs::big_key_kernel<M, C>), gt, dim3(xs::BLOCK), 0, ctx->stream, a);
     for (int pass = 0; pass < xs::RPASS; pass++) {
@@ -4180,7 +4182,7 @@ int launch(xs_context* ctx, xs::Args& a, int64_t rows, int span, bool mask, bool
   a.ctl_chunk = ctx->ctl_chunk;
   a.row_ticket = ctx->row_ticket;
   a.seq_ticket = ctx->seq_ticket;
-  a.k_max = ctx->k_max;
+  a.k_max = (a.k_max > 0 && a.k_max < ctx->k_max) ? a.k_max : ctx->k_max;  // the call's bound, if tighter
   a.big = ctx->big;
   a.big_ld = ctx->vocab;
   a.big_state = ctx->big_state;
@@ -4342,6 +4344,7 @@ int sample_impl(xs_context* ctx, const xs_sample_args* in, bool clear_tickets) {
   a.controls = in->controls;
   a.ctl_ids = in->ctl_ids;
   a.ctl_delta = in->ctl_delta;
+  a.k_max = in->k_max;  // (0: the context's)
   a.span = 0;
   a.n_chunks = chunks_for(in->enc);
   a.nslots = (int32_t)slots_for(in->enc);
@@ -4458,6 +4461,7 @@ int xs_verify(xs_context* ctx, const xs_verify_args* in) {
   a.controls = in->controls;
   a.ctl_ids = in->ctl_ids;
   a.ctl_delta = in->ctl_delta;
+  a.k_max = in->k_max;  // (0: the context's)
   a.n_chunks = chunks_for(in->enc);
   a.nslots = (int32_t)slots_for(in->enc);
   a.rec = ctx->rec;

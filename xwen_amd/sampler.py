@@ -223,14 +223,17 @@ class Draws:
 def sample_batch(ctx: Context, logits, params, uniforms, *, enc: int | None = None,
                  width: int | None = None, allowed=None, allowed_words: int | None = None,
                  cand_k: int = 0, stats: bool = False, n_top: int = 0, out: Draws | None = None,
-                 controls: Controls | None = None, order=None, check: bool = True) -> Draws:
+                 controls: Controls | None = None, order=None, k_max: int = 0,
+                 check: bool = True) -> Draws:
     """One xs_sample call.  logits: float32 [rows, ld] CUDA tensor (ld % 4 == 0);
     params: the uint8 tensor from params_tensor; uniforms: float32 [rows];
     order: an optional host permutation of the rows (see cost_order), the
-    order in which the launch starts them."""
+    order in which the launch starts them; k_max: this call's bound on
+    min(top_k, enc), 0 for the context's (127 or less skips the whole-row
+    kernels of a context sized for more)."""
     a, out, keep = _sample_args(logits, params, uniforms, enc=enc, width=width, allowed=allowed,
                                 allowed_words=allowed_words, cand_k=cand_k, stats=stats,
-                                n_top=n_top, out=out, controls=controls, order=order)
+                                n_top=n_top, out=out, controls=controls, order=order, k_max=k_max)
     rc = ctx.lib.xs_sample(ctx.h, C.byref(a))
     del keep
     if check:
@@ -259,7 +262,7 @@ def sample_batch_noalloc(logits, params, uniforms, *, stream=None, check: bool =
 def _sample_args(logits, params, uniforms, *, enc: int | None = None, width: int | None = None,
                  allowed=None, allowed_words: int | None = None, cand_k: int = 0,
                  stats: bool = False, n_top: int = 0, out: Draws | None = None,
-                 controls: Controls | None = None, order=None):
+                 controls: Controls | None = None, order=None, k_max: int = 0):
     """xs_sample_args for one call, the output tensors, and the host arrays the
     call reads (kept alive by the caller through the call)."""
     torch = _torch()
@@ -285,6 +288,7 @@ def _sample_args(logits, params, uniforms, *, enc: int | None = None, width: int
     a = _lib.SampleArgs()
     a.logits = logits.data_ptr()
     a.rows, a.ld, a.width, a.enc = rows, ld, width, enc
+    a.k_max = int(k_max)
     a.params = params.data_ptr()
     a.uniforms = uniforms.data_ptr()
     if allowed is not None:
@@ -351,9 +355,10 @@ class Verdict:
 def verify_batch(ctx: Context, logits, seqs: int, span: int, params, uniforms, drafts, *,
                  budget=None, eog=(), enc: int | None = None, allowed=None,
                  controls: Controls | None = None, done_after=None,
-                 out: Verdict | None = None) -> Verdict:
+                 out: Verdict | None = None, k_max: int = 0) -> Verdict:
     """One xs_verify call over logits [seqs*span, ld]; drafts int32 [seqs, span-1].
-    `allowed` / `done_after` per position come from masks_along_drafts."""
+    `allowed` / `done_after` per position come from masks_along_drafts; k_max
+    as in sample_batch."""
     torch = _torch()
     rows, ld = logits.shape
     assert rows == seqs * span
@@ -369,6 +374,7 @@ def verify_batch(ctx: Context, logits, seqs: int, span: int, params, uniforms, d
     a = _lib.VerifyArgs()
     a.logits = logits.data_ptr()
     a.seqs, a.span, a.ld, a.width, a.enc = seqs, span, ld, ld, enc
+    a.k_max = int(k_max)
     a.params = params.data_ptr()
     a.uniforms = uniforms.data_ptr()
     if allowed is not None:

@@ -297,6 +297,7 @@ struct BigRow {
   int32_t state;  // 1: the whole-row kernels draw the row in this call; 0: not
   float m_s, S;   // scaled max and softmax denominator
   int32_t kk;     // candidates: min(top_k, enc)
+  float sum;      // the candidate weights' serial sum (big_sum_kernel; top_p < 1)
 };
 
 struct Cfg {
@@ -431,6 +432,7 @@ struct Args {
   int64_t big_hld;
   int32_t* big_ticket;       // [rows * TSTRIDE]: the sort passes' arrival tickets, zero between kernels
   int32_t big_tiles;         // tiles of BTILE ids per row
+  int32_t big_nblk;          // chain blocks per row past the first CHEAD terms
   // the serial denominator (serial_kernel): set on calls with a mask or
   // controls, whose rows at top_p >= 1 serial_kernel finalizes
   int32_t serial;
@@ -2010,7 +2012,7 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
     F.big.defer = defer ? 1 : 0;
     F.big.m_s = m_s;
     F.big.S = S;
-    if (cfg.big && a.big_state) a.big_state[row] = BigRow{defer ? 1 : 0, m_s, S, k};
+    if (cfg.big && a.big_state) a.big_state[row] = BigRow{defer ? 1 : 0, m_s, S, k, 1.0f};
   }
   if (want_cands && stoch && st == XS_ROW_OK && !defer) {
     const int kw = (int)min((int64_t)k, a.cand_ld);  // a short cand_ld truncates the list
@@ -2262,6 +2264,18 @@ XS_DEV uint32_t grid_units(uint32_t eb, int F, bool& tie) {
 }
 
 XS_DEV int f32_field(float f) { return (int)(__float_as_uint(f) >> 23); }
+
+// grid_units of a term w >= 0 in float operations, the same value and tie
+// flag: w scaled onto the grid (by 2^(150 - F), exact: a multiple of the grid
+// below 2^24 stays normal), its floor and fraction, both exact.  A term the
+// scaling makes subnormal rounds to 0 units either way.
+XS_DEV uint32_t grid_units_f(float w, int F, bool& tie) {
+  const float v = __builtin_ldexpf(w, 150 - max(F, 1));
+  const float fl = __builtin_floorf(v);
+  const float fr = v - fl;
+  tie = fr == 0.5f;
+  return min((uint32_t)fminf(fl, (float)GSAT) + (fr > 0.5f ? 1u : 0u), GSAT);
+}
 
 // exp(d), d <= 0: within 2^-21 of the correctly rounded f32 value for
 // d >= -87 (d * log2e split in two, v_exp_f32 on the high part, a first-order
@@ -3566,6 +3580,10 @@ constexpr int QW = BTILE / NWAVE;   // a wave's quarter of a tile
 constexpr int CPT = 16;             // chain terms per thread and block
 constexpr int CBLK = CPT * BLOCK;   // chain terms per block
 constexpr int CHEAD = 128;          // chain terms added one at a time first
+constexpr int NG = 4;               // binades whose grid units big_units_kernel sums per block
+constexpr int FTOP = 127;           // the highest of them: sums of probabilities stay below 2
+constexpr int NBU = 256;            // blocks whose units a chain holds in LDS
+constexpr int UW = NG + 1;          // words per block: NG sums, then the tie and absorb bits
 static_assert(RBINS == BLOCK && EPL * 64 == QW, "one digit per thread; a wave's quarter in EPL steps");
 static_assert(SPC % SPT == 0, "tiles inside chunks");
 
@@ -3847,6 +3865,7 @@ XS_DEV uint64_t block_excl_scan64(uint64_t v, uint64_t* s4, uint64_t* total) {
 }
 
 struct ChainLds {
+  uint64_t bu[NBU * UW];  // per block: its units at the NG binades, tie and absorb bits
   uint64_t s4[NWAVE];
   int32_t stop;    // the block's first index that ends grid stepping
   int32_t absorb;  // the block's last term rounds away at the block's grid
@@ -3872,9 +3891,14 @@ struct ChainOut {
 // (rounded to even, which depends on the sum before it).  The terms are
 // non-increasing, so once one rounds to no units, every later one does: the
 // sum is final.  Every thread of the block, uniform arguments.
-// The terms: conv(srt[i]), from the sorted entries.
+// The terms: conv(srt[i]), from the sorted entries.  With nbu > 0, L.bu holds
+// big_units_kernel's sums for the first nbu blocks of the nu-term chain these
+// terms begin (nu >= n): a block wholly inside both, whose units at the sum's
+// binade keep the sum in it with no half-way term and do not reach the
+// target, is crossed in one step.
 template <typename CONV>
-XS_DEV ChainOut big_chain(const uint64_t* srt, int n, float acc, int mode, float thr, CONV conv, ChainLds& L) {
+XS_DEV ChainOut big_chain(const uint64_t* srt, int n, float acc, int mode, float thr, CONV conv, ChainLds& L,
+                          int nbu, int nu) {
   const int tid = threadIdx.x, lane = lane_id();
   auto reached = [&](double c) __attribute__((always_inline)) { return mode == 1 ? c >= (double)thr : c > (double)thr; };
   // 1. the head
@@ -3884,7 +3908,8 @@ XS_DEV ChainOut big_chain(const uint64_t* srt, int n, float acc, int mode, float
     int found = -1;
 #pragma unroll 1
     for (int b = 0; b < nh && found < 0; b += 64) {
-      const float wl = b + lane < nh ? conv(srt[b + lane]) : 0.0f;
+      const uint64_t rl = srt[min(b + lane, nh - 1)];
+      const float wl = b + lane < nh ? conv(rl) : 0.0f;
       const int m = min(64, nh - b);
 #pragma unroll 1
       for (int u = 0; u < m; u++) {
@@ -3905,25 +3930,32 @@ XS_DEV ChainOut big_chain(const uint64_t* srt, int n, float acc, int mode, float
   const int f = L.hit;
   lds_barrier();
   if (f >= 0) return ChainOut{acc, f};
-  // 2. blocks of CBLK terms, the next block's entries loaded ahead (converted
-  // only when their block starts, so that the loads stay in flight)
+  // 2. blocks of CBLK terms: in one step where the block's units allow, else
+  // term by term as below
   float w[CPT];
-  uint64_t rn[CPT];
-  auto load = [&](int b0) __attribute__((always_inline)) {
-#pragma unroll
-    for (int g = 0; g < CPT; g++) {
-      const int j = b0 + CPT * tid + g;
-      rn[g] = j < n ? srt[j] : 0ull;
-    }
-  };
-  if (nh < n) load(nh);
 #pragma unroll 1
-  for (int b0 = nh; b0 < n; b0 += CBLK) {
+  for (int b0 = nh, bi = 0; b0 < n; b0 += CBLK, bi++) {
     const int j0 = b0 + CPT * tid;
     const int bend = min(n, b0 + CBLK);
+    if (bi < nbu && bend == min(nu, b0 + CBLK) && acc > 0.0f) {
+      const int fa = f32_field(acc), g = max(fa, 1) - (FTOP - NG + 1);
+      if (g >= 0 && g < NG) {
+        const uint64_t* B = &L.bu[bi * UW];
+        const uint64_t Ma = (__float_as_uint(acc) & 0x7FFFFFu) | (fa ? 0x800000u : 0u);
+        const uint64_t end = Ma + B[g];
+        const double gridv = __builtin_ldexp(1.0, max(fa, 1) - 150);
+        if (!((B[NG] >> g) & 1u) && end < (1ull << 24) && !(mode && reached((double)end * gridv))) {
+          acc = (float)((double)end * gridv);  // exact: below the binade's end
+          if ((B[NG] >> (NG + g)) & 1u) return ChainOut{acc, n};  // every later term rounds away
+          continue;
+        }
+      }
+    }
+    uint64_t r[CPT];  // clamped indices, not guarded loads: all of them in flight at once
 #pragma unroll
-    for (int g = 0; g < CPT; g++) w[g] = j0 + g < n ? conv(rn[g]) : 0.0f;
-    if (bend < n) load(bend);
+    for (int g = 0; g < CPT; g++) r[g] = srt[min(j0 + g, n - 1)];
+#pragma unroll
+    for (int g = 0; g < CPT; g++) w[g] = j0 + g < n ? conv(r[g]) : 0.0f;
     int start = b0;
 #pragma unroll 1
     while (start < bend) {  // (uniform)
@@ -3951,7 +3983,7 @@ XS_DEV ChainOut big_chain(const uint64_t* srt, int n, float acc, int mode, float
 #pragma unroll
       for (int g = 0; g < CPT; g++) {
         bool t;
-        const uint32_t v = grid_units(__float_as_uint(w[g]), F, t);
+        const uint32_t v = grid_units_f(w[g], F, t);
         const bool live = j0 + g >= start && j0 + g < n;
         u[g] = live ? v : 0u;
         ties |= (live && t) ? (1u << g) : 0u;
@@ -4026,7 +4058,98 @@ XS_DEV ChainOut big_chain(const uint64_t* srt, int n, float acc, int mode, float
   return ChainOut{acc, n};
 }
 
-// Grid: rows.  The draw over the sorted row (big_chain for every serial sum).
+// Grid: rows x big_nblk.  Per block of CBLK chain terms past the first CHEAD
+// (the sorted entries' weights: `which` 0 the probabilities, for the sum of
+// a row that top_p renormalises; 1 the weights its cut and draw add, p / sum
+// or p), the block's grid units at each of the NG binades below 2^(FTOP-126),
+// whether a term lies half-way between grid points there, and whether the
+// block's last term rounds to no units there.  Units saturate at 2^24: a
+// block with that many carries the sum out of any of these binades.
+__global__ __launch_bounds__(BLOCK) void big_units_kernel(Args a, int which) {
+  __shared__ uint32_t red[NWAVE][NG + 1];
+  const int nb = a.big_nblk;
+  const int row = blockIdx.x / nb, blk = blockIdx.x % nb;
+  Cfg cfg;
+  const BigRow* br = big_live(a, row, cfg);
+  if (!br) return;
+  const bool renorm = !(cfg.top_p >= 1.0f);
+  if (which == 0 && !renorm) return;
+  const float sum = br->sum;
+  if (which == 1 && renorm && !(sum > 0.0f)) return;  // no chain follows
+  const int kk = br->kk;
+  const int b0 = CHEAD + blk * CBLK;
+  if (b0 >= kk) return;
+  const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
+  const int bend = min(kk, b0 + CBLK);
+  const uint64_t* srt = a.big + (int64_t)row * 2 * a.big_ld + ((RPASS & 1) ? a.big_ld : 0);
+  // (the sums take the block's terms in any order: strided, so that each load
+  // is one contiguous run across the block)
+  uint64_t e[CPT];
+#pragma unroll
+  for (int g = 0; g < CPT; g++) e[g] = srt[min(b0 + g * BLOCK + tid, bend - 1)];  // (clamped, not guarded: all in flight)
+  float v[CPT];
+#pragma unroll
+  for (int g = 0; g < CPT; g++) {
+    v[g] = pkey_p((uint32_t)(e[g] >> 32));
+    if (which == 1 && renorm) v[g] = __fdiv_rn(v[g], sum);
+  }
+  uint32_t ties = 0u, absorb = 0u;
+#pragma unroll 1
+  for (int f = 0; f < NG; f++) {
+    uint32_t su = 0u;
+#pragma unroll
+    for (int g = 0; g < CPT; g++) {
+      bool t;
+      const int j = b0 + g * BLOCK + tid;
+      const bool live = j < bend;
+      const uint32_t u = grid_units_f(v[g], FTOP - NG + 1 + f, t);
+      su = min(su + (live ? u : 0u), 1u << 24);
+      ties |= (live && t) ? (1u << f) : 0u;
+      absorb |= (j == bend - 1 && u == 0u && !t) ? (1u << f) : 0u;
+    }
+    const uint32_t ws = (uint32_t)wave_sumi((int)su);  // (64 x 2^24 fits)
+    if (lane == 0) red[wave][f] = min(ws, 1u << 24);
+  }
+  const uint32_t fl = wave_or(ties | (absorb << NG));
+  if (lane == 0) red[wave][NG] = fl;
+  __syncthreads();
+  if (tid <= NG) {
+    uint64_t* U = a.big + (int64_t)row * 2 * a.big_ld + ((RPASS & 1) ? 0 : a.big_ld) +
+                  (int64_t)(which * nb + blk) * UW;
+    uint64_t v = 0;
+#pragma unroll
+    for (int w = 0; w < NWAVE; w++) v = tid < NG ? v + red[w][tid] : (v | red[w][tid]);
+    U[tid] = tid < NG ? min(v, (uint64_t)1 << 24) : v;
+  }
+}
+
+// A chain's block units into LDS (the first NBU blocks); returns how many.
+XS_DEV int load_units(const Args& a, int row, int which, ChainLds& L) {
+  const int nb = min(a.big_nblk, NBU);
+  const uint64_t* U = a.big + (int64_t)row * 2 * a.big_ld + ((RPASS & 1) ? 0 : a.big_ld) +
+                      (int64_t)which * a.big_nblk * UW;
+  for (int i = threadIdx.x; i < nb * UW; i += BLOCK) L.bu[i] = U[i];
+  __syncthreads();
+  return nb;
+}
+
+// Grid: rows.  A row that top_p renormalises: the serial sum of its candidate
+// weights (truncate_top_p's total, folded from -0.0 as Rust's f32 Sum does).
+__global__ __launch_bounds__(BLOCK) void big_sum_kernel(Args a) {
+  __shared__ ChainLds L;
+  const int row = blockIdx.x;
+  Cfg cfg;
+  const BigRow* br = big_live(a, row, cfg);
+  if (!br || cfg.top_p >= 1.0f) return;
+  const int kk = br->kk;
+  const uint64_t* srt = a.big + (int64_t)row * 2 * a.big_ld + ((RPASS & 1) ? a.big_ld : 0);
+  auto pw = [&](uint64_t e) __attribute__((always_inline)) { return pkey_p((uint32_t)(e >> 32)); };
+  const int nbu = load_units(a, row, 0, L);
+  const float sum = big_chain(srt, kk, -0.0f, 0, 0.0f, pw, L, nbu, kk).acc;
+  if (threadIdx.x == 0) a.big_state[row].sum = sum;
+}
+
+// Grid: rows.  The cut and the draw over the sorted row, the outputs.
 __global__ __launch_bounds__(BLOCK) void big_draw_kernel(Args a) {
   __shared__ ChainLds L;
   const int row = blockIdx.x;
@@ -4035,18 +4158,13 @@ __global__ __launch_bounds__(BLOCK) void big_draw_kernel(Args a) {
   if (!br) return;
   const int tid = threadIdx.x;
   const int kk = br->kk;
-  // (RPASS odd: the sorted row is in the second buffer)
   const uint64_t* srt = a.big + (int64_t)row * 2 * a.big_ld + ((RPASS & 1) ? a.big_ld : 0);
   auto pw = [&](uint64_t e) __attribute__((always_inline)) { return pkey_p((uint32_t)(e >> 32)); };
   const bool renorm = !(cfg.top_p >= 1.0f);
   int st = XS_ROW_OK;
-  float sum = 1.0f;
+  const float sum = renorm ? br->sum : 1.0f;
   int keep = kk, tok = -1;
-  if (renorm) {
-    // sum of every candidate weight, folded from -0.0 as Rust's f32 Sum does
-    sum = big_chain(srt, kk, -0.0f, 0, 0.0f, pw, L).acc;
-    if (!(sum > 0.0f)) st = XS_ROW_ZERO_WEIGHT;  // weights left unchanged: no mass to draw
-  }
+  if (renorm && !(sum > 0.0f)) st = XS_ROW_ZERO_WEIGHT;  // weights left unchanged: no mass to draw
   if (st == XS_ROW_OK) {
     // renormalised weights (or the raw ones at top_p >= 1), their serial prefix
     // from 0 (truncate_top_p's cumsum, the same sums as WeightedIndex's
@@ -4055,7 +4173,8 @@ __global__ __launch_bounds__(BLOCK) void big_draw_kernel(Args a) {
       const float v = pw(e);
       return renorm ? __fdiv_rn(v, sum) : v;
     };
-    const ChainOut c = big_chain(srt, kk, 0.0f, renorm ? 1 : 0, cfg.top_p, ww, L);
+    const int nbu = load_units(a, row, 1, L);
+    const ChainOut c = big_chain(srt, kk, 0.0f, renorm ? 1 : 0, cfg.top_p, ww, L, nbu, kk);
     if (c.idx < kk) keep = c.idx + 1;
     const float tot = c.acc;  // the prefix through keep - 1
     if (!(tot > 0.0f)) {
@@ -4064,7 +4183,7 @@ __global__ __launch_bounds__(BLOCK) void big_draw_kernel(Args a) {
       // the index: the cumulative weights (prefix through i, i < keep - 1; the
       // total from keep - 1 on) at or below x
       const float x = a.uniforms[row] * tot + 0.0f;
-      const ChainOut d = big_chain(srt, keep - 1, 0.0f, 2, x, ww, L);
+      const ChainOut d = big_chain(srt, keep - 1, 0.0f, 2, x, ww, L, nbu, kk);
       tok = (int)(uint32_t)srt[d.idx < keep - 1 ? d.idx : keep - 1];
     }
   }
@@ -4161,6 +4280,10 @@ void launch2(xs_context* ctx, xs::Args& a, int64_t rows, dim3 g1, const int32_t*
       if (pass > 0) hipLaunchKernelGGL(xs::big_hist_kernel, gt, dim3(xs::BLOCK), 0, ctx->stream, a, pass);
       hipLaunchKernelGGL(xs::big_scatter_kernel, gt, dim3(xs::BLOCK), 0, ctx->stream, a, pass);
     }
+    const dim3 gb((unsigned)(rows * a.big_nblk));
+    if (a.big_nblk > 0) hipLaunchKernelGGL(xs::big_units_kernel, gb, dim3(xs::BLOCK), 0, ctx->stream, a, 0);
+    hipLaunchKernelGGL(xs::big_sum_kernel, dim3((unsigned)rows), dim3(xs::BLOCK), 0, ctx->stream, a);
+    if (a.big_nblk > 0) hipLaunchKernelGGL(xs::big_units_kernel, gb, dim3(xs::BLOCK), 0, ctx->stream, a, 1);
     hipLaunchKernelGGL(xs::big_draw_kernel, dim3((unsigned)rows), dim3(xs::BLOCK), 0, ctx->stream, a);
   }
 }
@@ -4190,6 +4313,7 @@ int launch(xs_context* ctx, xs::Args& a, int64_t rows, int span, bool mask, bool
   a.big_hld = (int64_t)ctx->big_tiles_max * xs::RBINS;
   a.big_ticket = ctx->big_ticket;
   a.big_tiles = (int32_t)((a.enc + xs::BTILE - 1) / xs::BTILE);
+  a.big_nblk = (int32_t)(a.enc > xs::CHEAD ? (a.enc - xs::CHEAD + xs::CBLK - 1) / xs::CBLK : 0);
   a.serial = (serial && (mask || ctl)) ? 1 : 0;
   a.ser_sum = ctx->ser_sum;
   a.ser_e = ctx->ser_e;

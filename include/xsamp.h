@@ -98,7 +98,7 @@ typedef struct {
  * path's buffers, 16 bytes per row and id plus 1 KiB per row and 4,096 ids
  * (33 MB for 8 rows of 248,320), and every sampling call on such a context
  * then launches the whole-row kernels too (rows that do not take that path
- * return at once: about 25 us more per call when no row does), unless the
+ * return at once: about 33 us more per call when no row does), unless the
  * call bounds its own top_k at XS_K_MAX or less (xs_sample_args.k_max).
  * Allocates the device workspace once; calls allocate nothing afterwards. */
 int xs_create(int device, int64_t max_rows, int64_t vocab, int32_t k_max, xs_context** out);

@@ -3564,11 +3564,17 @@ static_assert(NA_WORDS * 8 == XS_NOALLOC_BYTES, "XS_NOALLOC_BYTES states the arr
 //                       top_k_desc and of the stable whole-row sort;
 //   big_hist_kernel     the next pass's counts of the reordered tiles, and
 //                       their positions;
-//   big_draw_kernel     one workgroup per row: the first min(top_k, enc)
-//                       entries are the candidates; truncate_top_p
-//                       (sampler.rs:401-429) and WeightedIndex (:235-243,
-//                       rand 0.9) as the reference's serial f32 chains, each
-//                       evaluated by big_chain below.
+// then the first min(top_k, enc) sorted entries are the candidates, and
+// truncate_top_p (sampler.rs:401-429) and WeightedIndex (:235-243, rand 0.9)
+// run as the reference's serial f32 chains, each evaluated by big_chain:
+//   big_units_kernel    per block of chain terms, their grid units at the
+//                       binades where sums of probabilities end (one
+//                       workgroup per block), for the chains to cross blocks
+//                       in one step;
+//   big_sum_kernel      one workgroup per row: the weights' sum (rows that
+//                       top_p renormalises);
+//   big_draw_kernel     one workgroup per row: the cut, the draw, the
+//                       candidate list.
 
 constexpr int RB = 8;               // radix bits per pass
 constexpr int RBINS = 1 << RB;      // digits per pass: one per thread

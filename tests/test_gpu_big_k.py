@@ -178,3 +178,53 @@ def test_a_call_bounds_its_own_top_k(bigctx, oracle):
                 assert (d["cand_w"][r, :n] == full["cand_w"][r, :n]).all(), (bound, r)
             else:
                 assert d["status"][r] == 7 and d["token"][r] == -1, (bound, r)  # XS_ROW_BAD_PARAM
+
+
+def test_flat_rows_walk_the_whole_chain(bigctx, oracle):
+    """Flat rows (N(0, 1) at T = 1, and equal logits) keep every weight above
+    the sum's half-ulp, so the serial chains walk the whole sorted row: blocks
+    crossed in one step from their grid units, carries into the next binade
+    inside blocks, half-way terms, and cuts and draws far down the row (top_p
+    0.5 and 0.95); quantised logits make many equal p (ties in id order)."""
+    rng = np.random.default_rng(13128)
+    rows = 8
+    x = rng.normal(0, 1.0, (rows, V)).astype(np.float32)
+    x[2] = np.round(x[2] * 4) / 4            # a few hundred distinct values
+    x[3] = 0.0                               # every p equal
+    x[4] = rng.uniform(-0.01, 0.01, V).astype(np.float32)
+    x[5] = np.round(rng.normal(0, 3.0, V)).astype(np.float32)
+    K = np.array([V, V, V, V, 10**6, V, 200_000, 50_000])
+    P = np.array([0.95, 0.5, 0.95, 0.3, 1.0, 0.99, 0.95, 1.0])
+    T = np.array([1.0, 1.0, 1.0, 1.0, 1.0, 0.8, 1.3, 1.0])
+    U = workloads.uniforms(rng, rows)
+    d = run_sample(bigctx, x, T, K, P, U, cand_k=4096)
+    assert (d["status"] == 0).all(), d["status"]
+    check_rows(oracle, x, T, K, P, U, d, label="flat whole rows")
+
+
+def test_small_vocabularies_on_the_whole_row_path(oracle):
+    """Whole rows of 129 to 9,000 ids (one partial block of chain terms, or
+    none past the first 128), with masks and controls, top_k from 128 up."""
+    from xwen_amd import sampler as xsm
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    rng = np.random.default_rng(14128)
+    for enc in (129, 300, 4224, 4225, 9000):
+        rows = 4
+        ld = (enc + 3) // 4 * 4
+        c = xsm.Context(max_rows=rows, vocab=ld, k_max=2**31 - 1)
+        c.bind_current_stream()
+        try:
+            x = rng.normal(0, 1.5, (rows, ld)).astype(np.float32)
+            allow = rng.random((rows, enc)) < np.array([[1.0], [0.7], [1.0], [0.9]])
+            allow[:, 0] = True
+            mask = workloads.pack_mask(allow)
+            ctls = [None, None, xsm.SampleControl(banned=[1, 2, 3], bias=[(5, 2.0)]), None]
+            K = [enc, 10**6, 128, max(128, enc - 1)]
+            P = [0.9, 1.0, 0.95, 0.8]
+            U = workloads.uniforms(rng, rows)
+            d = run_sample(c, x, 1.0, K, P, U, enc=enc, mask=mask, ctls=ctls, cand_k=enc)
+            assert (d["status"] == 0).all(), (enc, d["status"])
+            check_rows(oracle, x, 1.0, K, P, U, d, enc=enc, mask=mask, ctls=ctls, label=f"enc {enc}")
+        finally:
+            c.close()

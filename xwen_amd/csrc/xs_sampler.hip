@@ -2364,39 +2364,51 @@ XS_DEV void seg_terms(const Args& a, const Cfg& cfg, int row, int g, float m_s, 
 
 // One segment added to the running sum's bits sb, its SEG terms at evp (LDS,
 // in id order): grid units up to the first term that carries into the next
-// binade or lies half-way, and from there the terms one at a time by f32 adds
-// (the reference's own operation).  One wave.
+// binade or lies half-way, that term by the f32 add (the reference's own
+// operation), then grid units again at the sum's new binade; after a few
+// such terms, the rest one at a time by f32 adds.  One wave.
 XS_DEV uint32_t ser_segment(uint32_t sb, const float* evp) {
   const int lane = lane_id();
   const float4 e4 = reinterpret_cast<const float4*>(evp)[lane];
   const float ev[4] = {e4.x, e4.y, e4.z, e4.w};
-  const uint32_t F = sb >> 23, m = F ? (sb & 0x7FFFFFu) : sb;
-  uint32_t p[4], P = 0;
-  bool tie[4];
+  int from = 0;  // the first term not yet added (uniform)
+#pragma unroll 1
+  for (int round = 0; round < 4; round++) {
+    const uint32_t F = sb >> 23, m = F ? (sb & 0x7FFFFFu) : sb;
+    uint32_t p[4], P = 0;
+    bool tie[4];
 #pragma unroll
-  for (int k = 0; k < 4; k++) {
-    P += grid_units(__float_as_uint(ev[k]), (int)F, tie[k]);
-    p[k] = P;
+    for (int k = 0; k < 4; k++) {
+      bool t;
+      const uint32_t u = grid_units(__float_as_uint(ev[k]), (int)F, t);
+      const bool live = 4 * lane + k >= from;  // (terms before `from` are added)
+      P += live ? u : 0u;
+      p[k] = P;
+      tie[k] = live && t;
+    }
+    const uint32_t Pc = min(P, GSAT);
+    const uint32_t incl = (uint32_t)wave_incl_scan((int)Pc);
+    const uint32_t excl = incl - Pc;
+    int kf = 4;  // this lane's first term that carries or ties
+#pragma unroll
+    for (int k = 3; k >= 0; k--)
+      if (tie[k] || m + excl + p[k] >= GSAT) kf = k;
+    const uint64_t bm = __ballot(kf < 4);
+    if (!bm) return sb + rdl(incl, 63);
+    const int L = (int)__builtin_ctzll(bm);
+    uint32_t before = excl;  // units before that term
+#pragma unroll
+    for (int k = 1; k < 4; k++) before = (kf == k) ? excl + p[k - 1] : before;
+    sb += rdl(before, L);
+    const int t = 4 * L + (int)rdl((uint32_t)kf, L);
+    sb = __float_as_uint(__uint_as_float(sb) + evp[t]);
+    from = t + 1;
+    if (from >= SEG) return sb;
   }
-  const uint32_t Pc = min(P, GSAT);
-  const uint32_t incl = (uint32_t)wave_incl_scan((int)Pc);
-  const uint32_t excl = incl - Pc;
-  int kf = 4;  // this lane's first term that carries or ties
-#pragma unroll
-  for (int k = 3; k >= 0; k--)
-    if (tie[k] || m + excl + p[k] >= GSAT) kf = k;
-  const uint64_t bm = __ballot(kf < 4);
-  if (!bm) return sb + rdl(incl, 63);
-  const int L = (int)__builtin_ctzll(bm);
-  uint32_t before = excl;  // units before that term
-#pragma unroll
-  for (int k = 1; k < 4; k++) before = (kf == k) ? excl + p[k - 1] : before;
-  sb += rdl(before, L);
-  const int start = 4 * L + (int)rdl((uint32_t)kf, L);
   float s = __uint_as_float(sb);
   if (lane == 0) {
 #pragma unroll 8
-    for (int i = start; i < SEG; i++) s = s + evp[i];
+    for (int i = from; i < SEG; i++) s = s + evp[i];
   }
   return (uint32_t)__builtin_amdgcn_readfirstlane((int)__float_as_uint(s));
 }

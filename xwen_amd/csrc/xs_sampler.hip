@@ -3243,22 +3243,26 @@ __global__ __launch_bounds__(BLOCK) void serial_kernel(Args a) {
     }
   }
   __syncthreads();
-  if (ok && tid == 0) {
+  if (ok && wave == 0) {
     // segments that keep their terms: nonzero ones where the exact sum may
-    // pass a power of two, or with a half-way term; one reservation of
-    // side-buffer slots for the workgroup
-    uint64_t km = 0ull;
-    for (int t = 0; t < SPC * NWAVE; t++) {
-      if (t / NWAVE >= ns) continue;
+    // pass a power of two, or with a half-way term (lane t: segment t); one
+    // reservation of side-buffer slots for the workgroup
+    static_assert(SPC * NWAVE == 64, "one segment per lane");
+    const int t = lane;
+    bool keep = false;
+    if (t / NWAVE < ns) {
       const uint32_t mt = Ls.meta[t];
       const double X1 = Ls.segpre[t] + Ls.segsum[t];
       const bool pass2 = f32_field((float)(X1 * (1.0 + SER_DELTA))) != (int)(mt & 0xFFu);
-      if (!(mt & SM_ZERO) && (pass2 || (mt & (SM_TIE0 | SM_TIE1)))) km |= 1ull << t;
+      keep = !(mt & SM_ZERO) && (pass2 || (mt & (SM_TIE0 | SM_TIE1)));
     }
-    Ls.kmask = km;
-    Ls.kbase = km ? __hip_atomic_fetch_add(&a.row_ticket[row * TSTRIDE + 2], __popcll(km), __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT)
-                  : 0;
+    const uint64_t km = __ballot(keep);
+    if (lane == 0) {
+      Ls.kmask = km;
+      Ls.kbase = km ? __hip_atomic_fetch_add(&a.row_ticket[row * TSTRIDE + 2], __popcll(km), __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT)
+                    : 0;
+    }
   }
   __syncthreads();
   if (ok) {

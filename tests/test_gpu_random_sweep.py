@@ -162,3 +162,37 @@ def test_random_held_row_statistics(ctx, oracle, b):
     check_rows(oracle, x, T, K, P, U, d, label=label + " held_row")
     for r in range(x.shape[0]):
         check_held_row(oracle, x[r], d, r, n_top, label=label)
+
+
+@pytest.fixture(scope="module")
+def bigctx():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from xwen_amd import sampler as xsm
+    c = xsm.Context(max_rows=16, vocab=workloads.V, k_max=2**31 - 1)
+    c.bind_current_stream()
+    yield c
+    c.close()
+
+
+@pytest.mark.parametrize("b", range(8))
+def test_random_whole_row_batch(bigctx, oracle, b):
+    """The whole-row path (top_k of 128 up to past the vocabulary) over the
+    sweep's distributions, with masks and sparse controls on some batches."""
+    from xwen_amd import sampler as xsm
+    x, T, _, P, U, mask, label = _batch(200 + b)
+    rows = 12
+    x, T, P, U = x[:rows], T[:rows], P[:rows], U[:rows]
+    mask = None if mask is None else mask[:rows]
+    v = x.shape[1]
+    rng = np.random.default_rng(60_000 + b)
+    T = np.where(T == 0.0, 1.0, T)  # (greedy rows never reach the path)
+    K = rng.choice([128, 129, 500, 1000, 5000, 2**31 - 1], rows)
+    ctls = None
+    if b % 3 == 1:
+        ctls = [None if r % 3 == 0 else
+                xsm.SampleControl(banned=[int(i) for i in rng.choice(v, 20)],
+                                  bias=[(int(i), float(rng.normal(0, 3))) for i in rng.choice(v, 10)])
+                for r in range(rows)]
+    d = run_sample(bigctx, x, T, K, P, U, mask=mask, ctls=ctls, cand_k=5000)
+    check_rows(oracle, x, T, K, P, U, d, mask=mask, ctls=ctls, label="whole-row " + label)

@@ -4336,6 +4336,7 @@ int launch(xs_context* ctx, xs::Args& a, int64_t rows, int span, bool mask, bool
   a.big_ticket = ctx->big_ticket;
   a.big_tiles = (int32_t)((a.enc + xs::BTILE - 1) / xs::BTILE);
   a.big_nblk = (int32_t)(a.enc > xs::CHEAD ? (a.enc - xs::CHEAD + xs::CBLK - 1) / xs::CBLK : 0);
+  if (a.big && rows * (int64_t)a.big_tiles > 0x7FFFFFFF) return XS_ERR_CAPACITY;  // the whole-row grids
   a.serial = (serial && (mask || ctl)) ? 1 : 0;
   a.ser_sum = ctx->ser_sum;
   a.ser_e = ctx->ser_e;

@@ -2088,10 +2088,18 @@ XS_DEV void finalize_row(const Args& a, const Cfg& cfg, int row, const uint64_t*
   const int lane = lane_id();
   uint64_t h[NHW], E[EPRE];
   const bool live = lane < nsub;
+  // every lane loads (its word lies inside the row's record: nsp >= 64), and
+  // the lanes past nsub drop what they read: unguarded loads all go out at
+  // once, where guarded ones were waited for in turn
 #pragma unroll
-  for (int i = 0; i < NHW; i++) h[i] = live ? ld_agent(&rowrec[i * nsp + lane]) : 0ull;
+  for (int i = 0; i < NHW; i++)  // (word 2, the held_row partial, only when it is read)
+    h[i] = (i == 2 && !WANT_LSE) ? 0ull : ld_agent(&rowrec[(uint32_t)(i * nsp + lane)]);
 #pragma unroll
-  for (int j = 0; j < EPRE; j++) E[j] = live ? ld_agent(&rowrec[(SHDR + j) * nsp + lane]) : 0ull;
+  for (int j = 0; j < EPRE; j++) E[j] = ld_agent(&rowrec[(uint32_t)((SHDR + j) * nsp + lane)]);
+#pragma unroll
+  for (int i = 0; i < NHW; i++) h[i] = live ? h[i] : 0ull;
+#pragma unroll
+  for (int j = 0; j < EPRE; j++) E[j] = live ? E[j] : 0ull;
   CtlRow cr{};
   if (HAS_CTL) cr = a.ctl_row[row];
   const bool done = !(HAS_CTL && cr.active) && nsub <= 64 && cfg.kp <= 64 && !cfg.bad && !cfg.big &&

@@ -998,13 +998,12 @@ XS_DEV void held_fold(const Args& a, int row, const float* rowp, const uint64_t*
     for (int g = 0; g * 64 < nsub; g++) {
       const int s = g * 64 + lane;
       const bool has = s < nsub;
-      const uint64_t h1 = has ? ld_agent(&rowrec[1 * nsp + s]) : 0ull;
-      const uint64_t h2 = has ? ld_agent(&rowrec[2 * nsp + s]) : 0ull;
-      const uint64_t h3 = has ? ld_agent(&rowrec[3 * nsp + s]) : 0ull;
-      const uint64_t h4 = has ? ld_agent(&rowrec[4 * nsp + s]) : 0ull;
-      const uint64_t h7 = has ? ld_agent(&rowrec[7 * nsp + s]) : 0ull;
-      const uint64_t h8 = has ? ld_agent(&rowrec[8 * nsp + s]) : 0ull;
-      const uint64_t h9 = has ? ld_agent(&rowrec[9 * nsp + s]) : 0ull;
+      // (s < nsp: the words lie inside the row's record; loaded unguarded,
+      // so that all go out at once, and dropped where !has)
+      const uint64_t h1 = ld_agent(&rowrec[1 * nsp + s]), h2 = ld_agent(&rowrec[2 * nsp + s]);
+      const uint64_t h3 = ld_agent(&rowrec[3 * nsp + s]), h4 = ld_agent(&rowrec[4 * nsp + s]);
+      const uint64_t h7 = ld_agent(&rowrec[7 * nsp + s]), h8 = ld_agent(&rowrec[8 * nsp + s]);
+      const uint64_t h9 = ld_agent(&rowrec[9 * nsp + s]);
       const int c = s / NWAVE;
       const float mw = __uint_as_float((uint32_t)h3);
       const bool fold_data = ((h3 >> 32) & 8u) != 0;
@@ -1201,7 +1200,8 @@ XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, int nsub, const uin
   for (int j0 = EPRE; __ballot(j0 < lim); j0 += 4) {
     uint64_t e[4];
 #pragma unroll
-    for (int u = 0; u < 4; u++) e[u] = (j0 + u < lim) ? ld_agent(rowrec + (int64_t)(SHDR + j0 + u) * nsp + lane) : 0ull;
+    for (int u = 0; u < 4; u++)  // (clamped inside the sub-record, not guarded: all four in flight)
+      e[u] = ld_agent(rowrec + (int64_t)(SHDR + min(j0 + u, CAPW - 1)) * nsp + lane);
 #pragma unroll
     for (int u = 0; u < 4; u++) put(e[u], j0 + u < lim && e[u] >= floor_e);
     if (srt && j0 + 3 < lim && e[3] < floor_e) lim = j0;
@@ -1395,7 +1395,8 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
       for (int t = 1; t < NHW; t++) v = i == t ? h[t] : v;
       return has(0) ? v : 0ull;
     }
-    return has(g) ? ld_agent(&rr[i * nsp + g * 64 + lane]) : 0ull;
+    const uint64_t v = ld_agent(&rr[i * nsp + min(g * 64 + lane, nsp - 1)]);  // (clamped, not guarded)
+    return has(g) ? v : 0ull;
   };
 
   float mv = -INFINITY;
@@ -1503,7 +1504,8 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
     for (; __ballot(j < lim); j += 4) {
       uint64_t e[4];
 #pragma unroll
-      for (int u = 0; u < 4; u++) e[u] = (j + u < lim) ? ld_agent(rr + (int64_t)(SHDR + j + u) * nsp + s) : 0ull;
+      for (int u = 0; u < 4; u++)  // (clamped inside the sub-record, not guarded: all four in flight)
+        e[u] = ld_agent(rr + (int64_t)(SHDR + min(j + u, CAPW - 1)) * nsp + s);
 #pragma unroll
       for (int u = 0; u < 4; u++) put(e[u], j + u < lim && e[u] >= fl_e);
       if (srt && j + 3 < lim && e[3] < fl_e) lim = j;
@@ -1708,7 +1710,8 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
               for (int j = 0; __ballot(j < lim); j += 4) {
                 uint64_t e[4];
 #pragma unroll
-                for (int u = 0; u < 4; u++) e[u] = (j + u < lim) ? ld_agent(rr + (int64_t)(SHDR + j + u) * nsp + s) : 0ull;
+                for (int u = 0; u < 4; u++)  // (clamped inside the sub-record, not guarded)
+                  e[u] = ld_agent(rr + (int64_t)(SHDR + min(j + u, CAPW - 1)) * nsp + s);
                 uint32_t hb = 0;  // bit u: entry j + u ties
 #pragma unroll
                 for (int u = 0; u < 4; u++) {
@@ -3085,9 +3088,13 @@ __global__ __launch_bounds__(BLOCK) void serial_kernel(Args a) {
     for (int gi = 0; gi < GMAX; gi++) {
       const int sub = gi * 64 + lane;
       const bool before = sub < chunk * NWAVE;
-      h3[gi] = sub < nsub ? ld_agent(&rowrec[3 * nsp + sub]) : 0ull;
-      h0[gi] = before ? ld_agent(&rowrec[sub]) : 0ull;
-      h1[gi] = before ? ld_agent(&rowrec[nsp + sub]) : 0ull;
+      const int sc = min(sub, nsp - 1);  // (clamped, not guarded: all in flight)
+      h3[gi] = ld_agent(&rowrec[3 * nsp + sc]);
+      h0[gi] = ld_agent(&rowrec[sc]);
+      h1[gi] = ld_agent(&rowrec[nsp + sc]);
+      h3[gi] = sub < nsub ? h3[gi] : 0ull;
+      h0[gi] = before ? h0[gi] : 0ull;
+      h1[gi] = before ? h1[gi] : 0ull;
     }
   }
   v4f q[SPC];
@@ -3673,9 +3680,9 @@ XS_DEV void big_counts(const Args& a, int row, int tile, uint32_t c, int32_t* s4
   for (int t0 = 0; t0 < nt; t0 += U) {
     int32_t v[U];
 #pragma unroll
-    for (int u = 0; u < U; u++) v[u] = t0 + u < nt ? ld_agent(&H[(int64_t)(t0 + u) * RBINS + tid]) : 0;
+    for (int u = 0; u < U; u++) v[u] = ld_agent(&H[(int64_t)min(t0 + u, nt - 1) * RBINS + tid]);  // (clamped)
 #pragma unroll
-    for (int u = 0; u < U; u++) tot += (uint32_t)v[u];
+    for (int u = 0; u < U; u++) tot += t0 + u < nt ? (uint32_t)v[u] : 0u;
   }
   int total;
   uint32_t pos = (uint32_t)block_excl_scan((int)tot, s4, &total);
@@ -3683,11 +3690,11 @@ XS_DEV void big_counts(const Args& a, int row, int tile, uint32_t c, int32_t* s4
   for (int t0 = 0; t0 < nt; t0 += U) {
     int32_t v[U];
 #pragma unroll
-    for (int u = 0; u < U; u++) v[u] = t0 + u < nt ? ld_agent(&H[(int64_t)(t0 + u) * RBINS + tid]) : 0;
+    for (int u = 0; u < U; u++) v[u] = ld_agent(&H[(int64_t)min(t0 + u, nt - 1) * RBINS + tid]);  // (clamped)
 #pragma unroll
     for (int u = 0; u < U; u++) {
       if (t0 + u < nt) H[(int64_t)(t0 + u) * RBINS + tid] = (int32_t)pos;
-      pos += (uint32_t)v[u];
+      pos += t0 + u < nt ? (uint32_t)v[u] : 0u;
     }
   }
 }

@@ -1027,10 +1027,15 @@ XS_DEV void held_fold(const Args& a, int row, const float* rowp, const uint64_t*
       }
       if (wave == 0 && from_entries) {
         const int cnt = (int)min((uint32_t)h4, (uint32_t)CAPW);
-        for (int j = 0; j < cnt; j++) {
-          const float v = keyf(pk_key(ld_agent(&rowrec[(int64_t)(SHDR + j) * nsp + s])));
-          const float x = v - m_v;
-          if (x >= LN_HALF_ULP1) post += (long long)__builtin_rint(exp_f64((double)x, T) * 0x1p52);
+        for (int j0 = 0; j0 < cnt; j0 += 8) {
+          uint64_t e[8];  // (clamped inside the sub-record, not guarded: eight loads in flight)
+#pragma unroll
+          for (int u = 0; u < 8; u++) e[u] = ld_agent(&rowrec[(int64_t)(SHDR + min(j0 + u, CAPW - 1)) * nsp + s]);
+#pragma unroll
+          for (int u = 0; u < 8; u++) {
+            const float x = keyf(pk_key(e[u])) - m_v;
+            if (j0 + u < cnt && x >= LN_HALF_ULP1) post += (long long)__builtin_rint(exp_f64((double)x, T) * 0x1p52);
+          }
         }
       }
       uint64_t m = __ballot(reread);

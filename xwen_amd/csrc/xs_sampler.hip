@@ -49,6 +49,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <type_traits>
 #include <cmath>
 #include <mutex>
 #include <cstring>
@@ -2581,71 +2582,86 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
   double racc = 0.0;
   float rc = -__FLT_MAX__;
   uint32_t nanl = 0;
+  // The loop comes in three copies, so that the uniform tests leave the
+  // per-float4 path where they can: EDGE for a chunk with absent or partial
+  // slots (the row's last), and STOCH for a stochastic row of a chunk without
+  // them.  Masked and controlled rows keep one copy (a second one spills).
+  auto stream = [&](auto edge_c, auto stoch_c) __attribute__((always_inline)) {
+    constexpr bool EDGE = decltype(edge_c)::value, STOCH = decltype(stoch_c)::value;
 #pragma unroll
-  for (int j = 0; j < SPC; j++) {
-    float x[4] = {q[j].x, q[j].y, q[j].z, q[j].w};
-    if (HAS_MASK) {
-      const uint32_t bits = mw[j] >> ((((s0 + j) * BLOCK + tid) & 7) * 4);
+    for (int j = 0; j < SPC; j++) {
+      float x[4] = {q[j].x, q[j].y, q[j].z, q[j].w};
+      if (HAS_MASK) {
+        const uint32_t bits = mw[j] >> ((((s0 + j) * BLOCK + tid) & 7) * 4);
 #pragma unroll
-      for (int e = 0; e < 4; e++)
-        if (!((bits >> e) & 1u)) x[e] = -INFINITY;
-    }
-    if (j >= ns || (s0 + j + 1) * SLOT > enc) {  // absent or partial slot (uniform)
-      const int id0 = (s0 + j) * SLOT + 4 * tid;
+        for (int e = 0; e < 4; e++)
+          if (!((bits >> e) & 1u)) x[e] = -INFINITY;
+      }
+      if (EDGE && (j >= ns || (s0 + j + 1) * SLOT > enc)) {  // absent or partial slot
+        const int id0 = (s0 + j) * SLOT + 4 * tid;
 #pragma unroll
-      for (int e = 0; e < 4; e++)
-        if (j >= ns || id0 + e >= enc) x[e] = -INFINITY;
-    }
-    if (HAS_CTL) {
-      const int sb = (s0 + j) * SLOT;
-      if (ctl_force >= 0) {
+        for (int e = 0; e < 4; e++)
+          if (j >= ns || id0 + e >= enc) x[e] = -INFINITY;
+      }
+      if (HAS_CTL) {
+        const int sb = (s0 + j) * SLOT;
+        if (ctl_force >= 0) {
 #pragma unroll
-        for (int e = 0; e < 4; e++) x[e] = (sb + 4 * tid + e == ctl_force) ? ctl_fval : -INFINITY;
-      } else {
-        // this slot's patches: the next ones in the sorted list
-        while (pc < phi) {
-          const uint64_t pe = pl[pc];
-          const int off = (int)(uint32_t)(pe >> 32) - sb;
-          if (off >= SLOT) break;
-          if ((off >> 2) == tid) {
-            const float pv = __uint_as_float((uint32_t)pe);
+          for (int e = 0; e < 4; e++) x[e] = (sb + 4 * tid + e == ctl_force) ? ctl_fval : -INFINITY;
+        } else {
+          // this slot's patches: the next ones in the sorted list
+          while (pc < phi) {
+            const uint64_t pe = pl[pc];
+            const int off = (int)(uint32_t)(pe >> 32) - sb;
+            if (off >= SLOT) break;
+            if ((off >> 2) == tid) {
+              const float pv = __uint_as_float((uint32_t)pe);
 #pragma unroll
-            for (int e = 0; e < 4; e++) x[e] = ((off & 3) == e) ? pv : x[e];
+              for (int e = 0; e < 4; e++) x[e] = ((off & 3) == e) ? pv : x[e];
+            }
+            pc++;
           }
-          pc++;
+          const int pt = ctl_pull - sb;
+          if (pt >= 0 && pt < SLOT && (pt >> 2) == tid) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) x[e] = ((pt & 3) == e) ? ctl_pval : x[e];
+          }
         }
-        const int pt = ctl_pull - sb;
-        if (pt >= 0 && pt < SLOT && (pt >> 2) == tid) {
-#pragma unroll
-          for (int e = 0; e < 4; e++) x[e] = ((pt & 3) == e) ? ctl_pval : x[e];
+      }
+      q[j] = v4f{x[0], x[1], x[2], x[3]};
+      gm[j] = vmax(vmax3(x[0], x[1], x[2]), x[3]);
+      mr = vmax(mr, gm[j]);
+      if (STOCH || stoch) {
+        if (j == 0) {
+          const float c = gm[0] * inv_e;
+          c_s = (c > -INFINITY && c < INFINITY) ? c : 0.0f;
+          cL = c_s * LOG2E;
         }
+        float t[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) t[e] = xexp2(__builtin_fmaf(x[e] * inv_e, LOG2E, -cL));
+        sum += (t[0] + t[1]) + (t[2] + t[3]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; e++) nanl |= (x[e] != x[e]) ? 1u : 0u;
+      }
+      if (WANT_LSE) {
+        if (gm[j] > rc) {
+          racc = (racc != 0.0) ? racc * (double)xexp2((rc - gm[j]) * LOG2E) : 0.0;
+          rc = gm[j];
+        }
+#pragma unroll
+        for (int e = 0; e < 4; e++) racc += (double)xexp2((x[e] - rc) * LOG2E);
       }
     }
-    q[j] = v4f{x[0], x[1], x[2], x[3]};
-    gm[j] = vmax(vmax3(x[0], x[1], x[2]), x[3]);
-    mr = vmax(mr, gm[j]);
-    if (stoch) {
-      if (j == 0) {
-        const float c = gm[0] * inv_e;
-        c_s = (c > -INFINITY && c < INFINITY) ? c : 0.0f;
-        cL = c_s * LOG2E;
-      }
-      float t[4];
-#pragma unroll
-      for (int e = 0; e < 4; e++) t[e] = xexp2(__builtin_fmaf(x[e] * inv_e, LOG2E, -cL));
-      sum += (t[0] + t[1]) + (t[2] + t[3]);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 4; e++) nanl |= (x[e] != x[e]) ? 1u : 0u;
-    }
-    if (WANT_LSE) {
-      if (gm[j] > rc) {
-        racc = (racc != 0.0) ? racc * (double)xexp2((rc - gm[j]) * LOG2E) : 0.0;
-        rc = gm[j];
-      }
-#pragma unroll
-      for (int e = 0; e < 4; e++) racc += (double)xexp2((x[e] - rc) * LOG2E);
-    }
+  };
+  using Yes = std::true_type;
+  using No = std::false_type;
+  if (HAS_MASK || HAS_CTL || ns < SPC || (s0 + SPC) * SLOT > enc) {
+    stream(Yes{}, No{});
+  } else if constexpr (!HAS_MASK && !HAS_CTL) {
+    if (stoch) stream(No{}, Yes{});
+    else stream(No{}, No{});
   }
   const float m_w = red_maxf(mr);
   double P = 0.0, R = 0.0;

@@ -2120,7 +2120,13 @@ XS_DEV void finalize_row(const Args& a, const Cfg& cfg, int row, const uint64_t*
 // The speculative walk: a finalized row of a verify block takes its sequence's
 // ticket, and the sequence's last finalized row walks accept_drafts
 // (generate.rs:4020-4046) over the sequence's rows.  One wave, after the row's
-// token and status are written.
+// token and status are written.  The walk stops before row i when the budget
+// is spent (i >= budget) or the row failed (its status then becomes the
+// sequence's), and after committing row i when it is the bonus position, did
+// not match its draft, is end-of-generation, or completes the grammar.  Lane l
+// holds row b + l of each group of 64 (every load of a group in flight at
+// once), and the first stop is the lowest lane of a ballot: every row before
+// it matched its draft and was committed.
 XS_DEV void verify_walk(const Args& a, int row) {
   const int lane = lane_id();
   drain();  // this row's token and status are acknowledged
@@ -2128,32 +2134,46 @@ XS_DEV void verify_walk(const Args& a, int row) {
   int t = 0;
   if (lane == 0) t = __hip_atomic_fetch_add(&a.seq_ticket[seq * TSTRIDE], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   t = __builtin_amdgcn_readfirstlane(t);
-  if (t == a.span - 1 && lane == 0) {
-    st_agent(&a.seq_ticket[seq * TSTRIDE], 0);
-    const int span = a.span, D = span - 1;
-    const int64_t r0 = (int64_t)seq * span;
-    const int bud = a.budget ? a.budget[seq] : 0x7FFFFFFF;
-    int mcount = 0, ncom = 0, sst = XS_ROW_OK;
-    for (int i = 0; i < span; i++) {
-      if (ncom >= bud) break;
-      const int rs = ld_agent(&a.status[r0 + i]);
-      if (rs != XS_ROW_OK) {
-        sst = rs;
-        break;
+  if (t != a.span - 1) return;
+  if (lane == 0) st_agent(&a.seq_ticket[seq * TSTRIDE], 0);
+  const int span = a.span, D = span - 1;
+  const int64_t r0 = (int64_t)seq * span;
+  const int bud = a.budget ? a.budget[seq] : 0x7FFFFFFF;
+  int ncom = -1, mcount = 0, sst = XS_ROW_OK;
+  int b = 0;
+  for (; b < span && ncom < 0; b += 64) {
+    const int i = b + lane;
+    const int ic = min(i, span - 1);  // (clamped, not guarded: the loads go out together)
+    const int rs = ld_agent(&a.status[r0 + ic]);
+    const int s = ld_agent(&a.token[r0 + ic]);
+    const int dr = D > 0 ? a.drafts[(int64_t)seq * D + min(ic, D - 1)] : 0;
+    const bool fin = a.done_after != nullptr && a.done_after[r0 + ic] != 0;
+    bool eog = false;
+    for (int e = 0; e < a.n_eog; e++) eog |= (s == a.eog[e]);
+    const bool in = i < span;
+    const bool matched = i < D && s == dr;
+    const bool before = in && (i >= bud || rs != XS_ROW_OK);
+    const bool after = in && !before && (!matched || eog || fin);
+    const uint64_t bb = __ballot(before), stop = bb | __ballot(after);
+    int lim = 0x7FFFFFFF;  // rows of this group below lim are committed
+    if (stop) {
+      const int f = (int)__builtin_ctzll(stop);
+      if ((bb >> f) & 1ull) {
+        ncom = b + f;
+        mcount = b + f;
+        const int rsf = __builtin_amdgcn_readlane(rs, f);
+        if (b + f < bud) sst = rsf;
+      } else {
+        ncom = b + f + 1;
+        mcount = b + f + ((__ballot(matched) >> f) & 1ull ? 1 : 0);
       }
-      const int s = ld_agent(&a.token[r0 + i]);
-      const bool matched = i < D && s == a.drafts[(int64_t)seq * D + i];
-      a.committed[(int64_t)seq * span + ncom] = s;
-      ncom++;
-      if (matched) mcount++;
-      bool eog = false;
-      for (int e = 0; e < a.n_eog; e++) eog |= (s == a.eog[e]);
-      // a draft that completes the grammar ends the walk like an EOG
-      // (generate.rs:2452-2459): the caller computed it along the drafts
-      if (matched && a.done_after && a.done_after[r0 + i]) eog = true;
-      if (!matched || eog) break;
+      lim = ncom;
     }
-    for (int i = ncom; i < span; i++) a.committed[(int64_t)seq * span + i] = -1;
+    if (in) a.committed[r0 + i] = i < lim ? s : -1;
+  }
+  for (; b < span; b += 64)
+    if (b + lane < span) a.committed[r0 + b + lane] = -1;
+  if (lane == 0) {
     a.accepted[seq] = mcount;
     a.n_committed[seq] = ncom;
     a.seq_status[seq] = sst;

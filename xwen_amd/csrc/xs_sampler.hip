@@ -2084,22 +2084,16 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
 }
 
 // ---------------------------------------------------------------------------
-// Row finalize, run by the first wave of the row's last workgroup: one round
-// of coalesced agent-scope loads (every header word and the first EPRE
-// entries of every sub-record), then fin_fast, or fin_general when the row
-// falls outside the common case.  For a speculative block the row then takes
-// its sequence's ticket, and the sequence's last finalized row walks it
-// (accept_drafts).
-template <bool HAS_MASK, bool WANT_LSE, bool HAS_CTL>
-XS_DEV void finalize_row(const Args& a, const Cfg& cfg, int row, const uint64_t* rowrec, int nsp,
-                         int nsub, const float* rowp, const uint32_t* mrow, FinLds& F,
-                         float S_ser = -1.0f) {
+// Row finalize, run by the first wave of the row's last workgroup (or of
+// finalize_kernel's workgroup for the row).  First one round of coalesced
+// agent-scope loads: the row's sub-record headers and first EPRE entries,
+// sub-record `lane` per lane.  Every lane loads (its word lies inside the row's record: nsp >= 64),
+// and the lanes past nsub drop what they read: unguarded loads all go out at
+// once, where guarded ones were waited for in turn.
+template <bool WANT_LSE>
+XS_DEV void load_heads(const uint64_t* rowrec, int nsp, int nsub, uint64_t (&h)[NHW], uint64_t (&E)[EPRE]) {
   const int lane = lane_id();
-  uint64_t h[NHW], E[EPRE];
   const bool live = lane < nsub;
-  // every lane loads (its word lies inside the row's record: nsp >= 64), and
-  // the lanes past nsub drop what they read: unguarded loads all go out at
-  // once, where guarded ones were waited for in turn
 #pragma unroll
   for (int i = 0; i < NHW; i++)  // (word 2, the held_row partial, only when it is read)
     h[i] = (i == 2 && !WANT_LSE) ? 0ull : ld_agent(&rowrec[(uint32_t)(i * nsp + lane)]);
@@ -2109,12 +2103,30 @@ XS_DEV void finalize_row(const Args& a, const Cfg& cfg, int row, const uint64_t*
   for (int i = 0; i < NHW; i++) h[i] = live ? h[i] : 0ull;
 #pragma unroll
   for (int j = 0; j < EPRE; j++) E[j] = live ? E[j] : 0ull;
+}
+
+// Then fin_fast, or fin_general when the row falls outside the common case,
+// from the headers load_heads read.  For a speculative block the
+// row then takes its sequence's ticket, and the sequence's last finalized row
+// walks it (accept_drafts).
+template <bool HAS_MASK, bool WANT_LSE, bool HAS_CTL>
+XS_DEV void finalize_heads(const Args& a, const Cfg& cfg, int row, const uint64_t* rowrec, int nsp,
+                           int nsub, const float* rowp, const uint32_t* mrow, FinLds& F,
+                           const uint64_t (&h)[NHW], const uint64_t (&E)[EPRE], float S_ser = -1.0f) {
   CtlRow cr{};
   if (HAS_CTL) cr = a.ctl_row[row];
   const bool done = !(HAS_CTL && cr.active) && nsub <= 64 && cfg.kp <= 64 && !cfg.bad && !cfg.big &&
                     fin_fast<HAS_MASK, WANT_LSE>(a, cfg, row, nsub, h, E, rowrec, nsp, rowp, F, S_ser);
   if (!done) fin_general<HAS_MASK, WANT_LSE, HAS_CTL>(a, cfg, row, rowrec, nsp, nsub, rowp, mrow, cr, h, E, F, S_ser);
+}
 
+template <bool HAS_MASK, bool WANT_LSE, bool HAS_CTL>
+XS_DEV void finalize_row(const Args& a, const Cfg& cfg, int row, const uint64_t* rowrec, int nsp,
+                         int nsub, const float* rowp, const uint32_t* mrow, FinLds& F,
+                         float S_ser = -1.0f) {
+  uint64_t h[NHW], E[EPRE];
+  load_heads<WANT_LSE>(rowrec, nsp, nsub, h, E);
+  finalize_heads<HAS_MASK, WANT_LSE, HAS_CTL>(a, cfg, row, rowrec, nsp, nsub, rowp, mrow, F, h, E, S_ser);
 }
 
 // The speculative walk: a finalized row of a verify block takes its sequence's
@@ -3023,18 +3035,21 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
 template <bool HAS_MASK, bool WANT_LSE, bool HAS_CTL>
 __global__ __launch_bounds__(BLOCK) void finalize_kernel(Args a) {
   __shared__ TailLds Tl;
-  const int row = blockIdx.x, wave = wave_id();
+  const int row = blockIdx.x;
+  if (wave_id() != 0) return;  // one wave finalizes the row
   const int nc = a.n_chunks;
+  const int nsp = ((nc * NWAVE + 63) >> 6) << 6;
+  const uint64_t* const rowrec = a.rec + (int64_t)row * SRECW * nsp;
+  // the row's headers first: their round trip overlaps the row's parameters
+  uint64_t h[NHW], E[EPRE];
+  load_heads<WANT_LSE>(rowrec, nsp, nc * NWAVE, h, E);
   const Cfg cfg = a.greedy_all ? greedy_cfg() : make_cfg(a.params[row], a.enc, a.n_top, a.k_max);
   if (threadIdx.x == 0) st_agent(&a.row_ticket[row * TSTRIDE + 1], 0);  // held_row's running max key
   if (a.serial && serial_row<HAS_MASK, HAS_CTL>(a, cfg, row)) return;  // serial_kernel finalizes it
   const float* rowp = a.logits + (int64_t)row * a.ld;
   const uint32_t* mrow = HAS_MASK ? a.allowed + (int64_t)row * a.allowed_ld : nullptr;
-  const int nsp = ((nc * NWAVE + 63) >> 6) << 6;
-  const uint64_t* const rowrec = a.rec + (int64_t)row * SRECW * nsp;
   const bool held = WANT_LSE && (a.row_lse != nullptr || a.n_top > 0);
-  if (wave != 0) return;
-  finalize_row<HAS_MASK, WANT_LSE, HAS_CTL>(a, cfg, row, rowrec, nsp, nc * NWAVE, rowp, mrow, Tl.fin);
+  finalize_heads<HAS_MASK, WANT_LSE, HAS_CTL>(a, cfg, row, rowrec, nsp, nc * NWAVE, rowp, mrow, Tl.fin, h, E);
   if (held) held_fold<1>(a, row, rowp, rowrec, nsp, nc * NWAVE, Tl.fin);
   if (a.span > 0 && !deferred(cfg, Tl.fin)) verify_walk(a, row);
 }

@@ -638,6 +638,37 @@ constexpr int GMAX = 4;             // sub-record groups of 64 a finalizer handl
 constexpr int KGRP = 32;            // largest K' whose chunk bound comes from group maxima
 constexpr uint32_t KEY_NEG_INF = 0x007FFFFFu;  // fkey(-inf)
 
+// The k-th largest of the 64R keys x, as kth_largest returns it, where the
+// keys above KEY_NEG_INF (finite values) number at most 128: those are
+// compacted into scr (this wave's, 128 words of LDS) and sorted, which takes
+// a fraction of the 32 ballot rounds of the bitwise search.  When fewer than
+// k keys are finite the result is 0: at or below KEY_NEG_INF, a bound that
+// admits every finite value, as any such result does for the callers.
+// k <= 128; more finite keys take kth_largest.
+template <int R>
+XS_DEV uint32_t kth_largest_few(const uint32_t (&x)[R], int k, uint32_t* scr) {
+  uint64_t b[R];
+  int n = 0;
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    b[r] = __ballot(x[r] > KEY_NEG_INF);
+    n += (int)__popcll(b[r]);
+  }
+  if (n < k) return 0u;
+  if (n > 128) return kth_largest<R>(x, k);
+  int base = 0;
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    if (x[r] > KEY_NEG_INF) scr[base + lanes_below(b[r])] = x[r];
+    base += (int)__popcll(b[r]);
+  }
+  wave_lds_sync();
+  const int lane = lane_id();
+  uint32_t v[2] = {lane < n ? scr[lane] : 0u, lane + 64 < n ? scr[lane + 64] : 0u};
+  wave_sort_desc<2, true>(v);
+  return k <= 64 ? rdl(v[0], k - 1) : rdl(v[1], k - 65);
+}
+
 struct ChunkLds {
   uint32_t groupmax[BLOCK / 4];     // maxima of 4-lane groups
   uint32_t lanemax[BLOCK];          // lane maxima
@@ -1163,7 +1194,7 @@ XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, int nsub, const uin
   } else if (4 * nsub >= kp) {
     const uint32_t x[4] = {live ? (uint32_t)h[5] : 0u, live ? (uint32_t)(h[5] >> 32) : 0u,
                            live ? (uint32_t)h[6] : 0u, live ? (uint32_t)(h[6] >> 32) : 0u};
-    tau = kth_largest<4>(x, kp);
+    tau = kth_largest_few<4>(x, kp, reinterpret_cast<uint32_t*>(F.srt));
   }
   // Gather the survivors into LDS, then order them by rank: a survivor's
   // position is the number of survivors above it ((key, ~id) are distinct).
@@ -2768,8 +2799,8 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
   // for larger K' it is the 256 lane maxima, whose K'-th passes fewer
   // elements than the group maxima's would.  Every wave finds it for itself
   // (no second barrier) with a DPP bitonic sort; when fewer than K' groups
-  // hold a finite value, by a bitwise search over the lane maxima: the
-  // largest key with at least K' of them at or above it.
+  // hold a finite value, as the K'-th largest lane max (the finite ones,
+  // compacted and sorted).
   const uint32_t km = fkey(mr);
   {
     uint32_t g = max(km, xor_u32(km, 1));
@@ -2817,18 +2848,12 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
 #pragma unroll
       for (int r = 0; r < 4; r++) pub[r] = rdl(all[0], wave + 4 * r);
     } else if (tk <= KEY_NEG_INF && !none) {
+      // fewer than K' group maxima are finite, so at most 4(K' - 1) < 128 lane
+      // maxima are (the staging area is free until the filter)
       uint32_t all[4];
 #pragma unroll
       for (int r = 0; r < 4; r++) all[r] = Lc.lanemax[r * 64 + lane];
-      tk = 0;
-#pragma unroll
-      for (int bit = 31; bit >= 0; bit--) {
-        const uint32_t c = tk | (1u << bit);
-        int n = 0;
-#pragma unroll
-        for (int r = 0; r < 4; r++) n += (int)__popcll(__ballot(all[r] >= c));
-        if (n >= kp) tk = c;
-      }
+      tk = kth_largest_few<4>(all, kp, reinterpret_cast<uint32_t*>(Tl.stage[wave]));
     }
   }
 

@@ -177,3 +177,41 @@ def test_thousands_of_subnormal_ties(ctx, oracle, background):
         d = run_sample(ctx, x, T, K, P, U, cand_k=cand_k)
         assert (d["status"] == 0).all(), d["status"]
         check_rows(oracle, x, T, K, P, U, d, margins=False, label=f"subnormal ties {background} cand_k={cand_k}")
+
+
+def test_kth_largest_over_few_finite_keys(ctx, oracle):
+    """The K'-th largest key taken from compacted finite keys, at its edges.
+    In the chunk bound (fewer than K' = 21 finite group maxima in a chunk):
+    80 finite lane maxima in 20 four-lane groups, 20 (fewer than K'), 21
+    (exactly K'), and one id.  In the finalizer's four-key bound (fewer than
+    2K' sub-records with a finite first key): whole chunks allowed, 8 of them
+    (128 finite keys, the most the compaction takes), 9 and 10 (144 and 160:
+    the bitwise search), 11 (44 first keys: the one-key bound); and K' = 64
+    and 41, where the chunk bound comes from lane maxima."""
+    rng = np.random.default_rng(87)
+    rows = 10
+    x = rng.standard_normal((rows, V), dtype=np.float32) * np.float32(3.0)
+    allow = np.zeros((rows, V), bool)
+    chunk = 16 * 1024
+    base = 5 * chunk + 3 * 1024  # slot 3 of chunk 5
+    for g in range(20):          # group g covers ids 16g .. 16g + 15 of the slot (lanes 4g .. 4g + 3)
+        allow[0, base + 16 * g: base + 16 * g + 16] = True
+    for g in range(5):
+        allow[1, base + 16 * g: base + 16 * g + 16] = True
+        allow[2, base + 16 * g: base + 16 * g + 16] = True
+    allow[2, base + 16 * 7: base + 16 * 7 + 4] = True  # one more lane, in a sixth group
+    allow[3, base + 77] = True
+    picks = [1, 3, 5, 7, 9, 11, 13, 14, 2, 6, 10]
+    for r, c in zip(range(4, 10), [8, 9, 10, 11, 8, 10]):
+        for ch in picks[:c]:
+            allow[r, ch * chunk:(ch + 1) * chunk] = True
+    mask = workloads.pack_mask(allow)
+    K = np.array([20, 20, 20, 20, 20, 20, 20, 20, 63, 40])
+    T = np.array([1.0, 0.7] * 5)
+    P = np.array([0.9, 0.9, 1.0, 0.9, 0.9, 1.0, 0.9, 0.9, 0.95, 0.9])
+    U = _uniforms(rng, rows)
+    d = run_sample(ctx, x, T, K, P, U, mask=mask, cand_k=128)
+    assert (d["status"] == 0).all(), d["status"]
+    check_rows(oracle, x, T, K, P, U, d, mask=mask, margins=False, label="few finite keys")
+    for r in range(rows):
+        assert allow[r, d["token"][r]]

@@ -644,7 +644,8 @@ constexpr uint32_t KEY_NEG_INF = 0x007FFFFFu;  // fkey(-inf)
 // a fraction of the 32 ballot rounds of the bitwise search.  When fewer than
 // k keys are finite the result is 0: at or below KEY_NEG_INF, a bound that
 // admits every finite value, as any such result does for the callers.
-// k <= 128; more finite keys take kth_largest.
+// More than 128 finite keys take kth_largest (so does any k above 128 that
+// has k of them).
 template <int R>
 XS_DEV uint32_t kth_largest_few(const uint32_t (&x)[R], int k, uint32_t* scr) {
   uint64_t b[R];

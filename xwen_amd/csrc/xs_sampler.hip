@@ -2646,12 +2646,15 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
   double racc = 0.0;
   float rc = -__FLT_MAX__;
   uint32_t nanl = 0;
-  // The loop comes in three copies, so that the uniform tests leave the
+  // The loop comes in four copies, so that the uniform tests leave the
   // per-float4 path where they can: EDGE for a chunk with absent or partial
-  // slots (the row's last), and STOCH for a stochastic row of a chunk without
-  // them.  Masked and controlled rows keep one copy (a second one spills).
-  auto stream = [&](auto edge_c, auto stoch_c) __attribute__((always_inline)) {
+  // slots (the row's last), STOCH for a stochastic row of a chunk without
+  // them, and UNIT for such a row at T = 1, whose s = v * 1 is v itself (for
+  // every float, NaN and -0 included) and needs no multiply.  Masked and
+  // controlled rows keep one copy (a second one spills).
+  auto stream = [&](auto edge_c, auto stoch_c, auto unit_c) __attribute__((always_inline)) {
     constexpr bool EDGE = decltype(edge_c)::value, STOCH = decltype(stoch_c)::value;
+    constexpr bool UNIT = decltype(unit_c)::value;
 #pragma unroll
     for (int j = 0; j < SPC; j++) {
       float x[4] = {q[j].x, q[j].y, q[j].z, q[j].w};
@@ -2703,7 +2706,7 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
         }
         float t[4];
 #pragma unroll
-        for (int e = 0; e < 4; e++) t[e] = xexp2(__builtin_fmaf(x[e] * inv_e, LOG2E, -cL));
+        for (int e = 0; e < 4; e++) t[e] = xexp2(__builtin_fmaf(UNIT ? x[e] : x[e] * inv_e, LOG2E, -cL));
         sum += (t[0] + t[1]) + (t[2] + t[3]);
       } else {
 #pragma unroll
@@ -2714,10 +2717,11 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
   using Yes = std::true_type;
   using No = std::false_type;
   if (HAS_MASK || HAS_CTL || ns < SPC || (s0 + SPC) * SLOT > enc) {
-    stream(Yes{}, No{});
+    stream(Yes{}, No{}, No{});
   } else if constexpr (!HAS_MASK && !HAS_CTL) {
-    if (stoch) stream(No{}, Yes{});
-    else stream(No{}, No{});
+    if (stoch && cfg.scale) stream(No{}, Yes{}, No{});
+    else if (stoch) stream(No{}, Yes{}, Yes{});
+    else stream(No{}, No{}, No{});
   }
   if (WANT_LSE) {  // the held_row partial, against the lane max (every value is in registers)
     rc = (mr > -__FLT_MAX__) ? mr : -__FLT_MAX__;

@@ -228,3 +228,43 @@ def test_small_vocabularies_on_the_whole_row_path(oracle):
             check_rows(oracle, x, 1.0, K, P, U, d, enc=enc, mask=mask, ctls=ctls, label=f"enc {enc}")
         finally:
             c.close()
+
+
+def test_tokens_only_rows_sort_what_the_sums_see(bigctx, oracle):
+    """A call that returns tokens only, at top_k >= V, leaves p < 2^-26 out of
+    the sort and the chains: each such term is added to a serial sum above
+    0.5 and rounds back to it.  The same rows drawn with the full candidate
+    list (every id sorted) and tokens only must give the same tokens, and the
+    oracle's: rows with a few tall tokens (most terms left out), flat rows
+    (none), masked rows (the masked ids at p = 0), top_p 0.8, 0.95 and 1, and
+    uniforms from 0 to 1 - 2^-24."""
+    rng = np.random.default_rng(8133)
+    rows = 12
+    x = np.empty((rows, V), np.float32)
+    for r in range(rows):
+        kind = r % 3
+        if kind == 0:    # a few tall tokens over the bulk
+            x[r] = rng.normal(0, 2.5, V).astype(np.float32)
+            x[r, rng.integers(0, V, 8)] = rng.uniform(8, 14, 8).astype(np.float32)
+        elif kind == 1:  # flat
+            x[r] = rng.normal(0, 1, V).astype(np.float32)
+        else:            # one dominant token
+            x[r] = rng.normal(0, 3, V).astype(np.float32)
+            x[r, rng.integers(0, V)] = np.float32(30.0)
+    allow = rng.random((rows, V)) < 0.3
+    allow[np.arange(rows), np.argmax(x, axis=1)] = True
+    mask = workloads.pack_mask(allow)
+    K = np.array([V, 10**6] * 6)
+    T = np.array([1.0, 0.7, 1.3, 1.0] * 3)
+    P = np.array([0.8, 0.95, 1.0] * 4)
+    # (masked rows at top_p < 1 only: at top_p >= 1 a call with candidates
+    # takes the serial denominator, a tokens-only call the exact one)
+    for m, Pm in ((None, P), (mask, np.minimum(P, 0.95))):
+        for U in (workloads.uniforms(rng, rows),
+                  np.array([0.0, 2.0**-24, 0.5, 1 - 2.0**-24] * 3, np.float32),
+                  np.full(rows, 1 - 2.0**-24, np.float32)):
+            full = run_sample(bigctx, x, T, K, Pm, U, mask=m, cand_k=V)
+            toks = run_sample(bigctx, x, T, K, Pm, U, mask=m, cand_k=0)
+            assert (full["status"] == 0).all() and (toks["status"] == 0).all()
+            np.testing.assert_array_equal(toks["token"], full["token"])
+            check_rows(oracle, x, T, K, Pm, U, full, mask=m, label="tokens only vs full sort")

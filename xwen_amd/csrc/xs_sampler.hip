@@ -372,6 +372,8 @@ struct CtlRow {
 };
 constexpr int CTL_MAX = XS_CTL_MAX;
 constexpr int TSTRIDE = 32;  // one arrival ticket per 128-byte line: tickets of different rows never share one
+constexpr int TS_N = 1;     // whole-row path, big_ticket line: the row's sorted entries
+constexpr int TS_LAST = 2;  // and two words: the row's last (pkey, id) (KCUT below)
 
 struct Args {
   const float* logits;
@@ -434,6 +436,7 @@ struct Args {
   int32_t* big_ticket;       // [rows * TSTRIDE]: the sort passes' arrival tickets, zero between kernels
   int32_t big_tiles;         // tiles of BTILE ids per row
   int32_t big_nblk;          // chain blocks per row past the first CHEAD terms
+  int32_t big_cut;           // tokens only, enc <= 2^20: rows at top_k >= enc sort only p >= 2^-26
   // the serial denominator (serial_kernel): set on calls with a mask or
   // controls, whose rows at top_p >= 1 serial_kernel finalizes
   int32_t serial;
@@ -2053,7 +2056,10 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
     F.big.defer = defer ? 1 : 0;
     F.big.m_s = m_s;
     F.big.S = S;
-    if (cfg.big && a.big_state) a.big_state[row] = BigRow{defer ? 1 : 0, m_s, S, k, 1.0f};
+    if (cfg.big && a.big_state) {
+      a.big_state[row] = BigRow{defer ? 1 : 0, m_s, S, k, 1.0f};
+      if (defer) *reinterpret_cast<uint64_t*>(&a.big_ticket[row * TSTRIDE + TS_LAST]) = 0ull;
+    }
   }
   if (want_cands && stoch && st == XS_ROW_OK && !defer) {
     const int kw = (int)min((int64_t)k, a.cand_ld);  // a short cand_ld truncates the list
@@ -3702,6 +3708,18 @@ constexpr int QW = BTILE / NWAVE;   // a wave's quarter of a tile
 constexpr int CPT = 16;             // chain terms per thread and block
 constexpr int CBLK = CPT * BLOCK;   // chain terms per block
 constexpr int CHEAD = 128;          // chain terms added one at a time first
+// A tokens-only call's rows at top_k >= enc leave p < 1.75 * 2^-26 out of the
+// sort and the chains (their pkey above KCUT; KSENT marks them in the first
+// pass's source).  Such a row's p sum to about 1 and it holds at most 2^20
+// ids, so those terms sum to under 0.03, and the serial f32 sum of the others
+// (at most 2^20 additions, each off by at most 2^-24 relative) is at least
+// 0.9.  So each left-out term, raw (p) or renormalised (p / sum < 1.95 *
+// 2^-26), is below 2^-25, half an ulp of any sum of 0.5 or more, and every
+// addition of one rounds back to the sum.  No chain depends on them or their
+// order, except the draw's index past every cumulative weight, which takes
+// the row's last entry: the row's largest (pkey, id), kept aside.
+constexpr uint32_t KCUT = 0x7FFFFFFFu - 0x32E00000u;  // pkey(1.75 * 2^-26)
+constexpr uint32_t KSENT = 0xFFFFFFFFu;
 constexpr int NG = 4;               // binades whose grid units big_units_kernel sums per block
 constexpr int FTOP = 127;           // the highest of them: sums of probabilities stay below 2
 constexpr int NBU = 256;            // blocks whose units a chain holds in LDS
@@ -3742,13 +3760,13 @@ XS_DEV const BigRow* big_live(const Args& a, int row, Cfg& cfg) {
   return br->state ? br : nullptr;
 }
 
-// A tile's digit counts `c` (thread t: digit t) go out; the row's last tile to
-// arrive (an arrival ticket, as in sample_kernel's hand-off) turns every
-// tile's counts into the tile's first position of each digit, in place:
+// A tile's digit counts `c` (thread t: digit t) go out; the row's last of its
+// nt tiles to arrive (an arrival ticket, as in sample_kernel's hand-off) turns
+// every tile's counts into the tile's first position of each digit, in place:
 // digits ascending, and within a digit the tiles in order.
-XS_DEV void big_counts(const Args& a, int row, int tile, uint32_t c, int32_t* s4, int32_t& last) {
+XS_DEV void big_counts(const Args& a, int row, int tile, uint32_t c, int32_t* s4, int32_t& last, int nt) {
   int32_t* const H = reinterpret_cast<int32_t*>(a.big_hist) + (int64_t)row * a.big_hld;
-  const int tid = threadIdx.x, nt = a.big_tiles;
+  const int tid = threadIdx.x;
   st_agent(&H[(int64_t)tile * RBINS + tid], (int32_t)c);
   drain();
   __syncthreads();
@@ -3771,6 +3789,7 @@ XS_DEV void big_counts(const Args& a, int row, int tile, uint32_t c, int32_t* s4
   }
   int total;
   uint32_t pos = (uint32_t)block_excl_scan((int)tot, s4, &total);
+  if (tid == 0) a.big_ticket[row * TSTRIDE + TS_N] = total;  // the entries every pass sorts
 #pragma unroll 1
   for (int t0 = 0; t0 < nt; t0 += U) {
     int32_t v[U];
@@ -3824,6 +3843,8 @@ __global__ __launch_bounds__(BLOCK) void big_key_kernel(Args a) {
     phi = a.ctl_chunk[(int64_t)row * (a.n_chunks + 1) + chunk + 1];
   }
   const bool ctl_on = HAS_CTL && cr.active;
+  const bool cut = a.big_cut && br->kk == enc;  // p < 2^-26 stays out of the sort (KCUT)
+  uint64_t lastv = 0;                           // the tile's largest (pkey, id)
   if (tid < 64) expt[tid] = (&kExpT[0][0])[tid];
   hist[tid] = 0u;
   __syncthreads();
@@ -3844,7 +3865,10 @@ __global__ __launch_bounds__(BLOCK) void big_key_kernel(Args a) {
 #pragma unroll
     for (int e = 0; e < 4; e++) {
       k[e] = pkey(exact_p(x[e], cfg, m_s, S, expt));
-      count_digit(hist, rdigit(k[e], 0), id0 + e < enc);
+      const bool in = id0 + e < enc;
+      if (cut && in) lastv = max(lastv, ((uint64_t)k[e] << 32) | (uint32_t)(id0 + e));
+      if (cut && k[e] > KCUT) k[e] = KSENT;
+      count_digit(hist, rdigit(k[e], 0), in && k[e] != KSENT);
     }
     if (id0 + 3 < enc) {
 #pragma unroll
@@ -3855,8 +3879,25 @@ __global__ __launch_bounds__(BLOCK) void big_key_kernel(Args a) {
         if (id0 + e < enc) A[id0 + e] = ((uint64_t)k[e] << 32) | (uint32_t)(id0 + e);
     }
   }
+  if (cut) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) lastv = max(lastv, shfl_xor64(lastv, o));
+    if (lane_id() == 0 && lastv != 0)
+      __hip_atomic_fetch_max(reinterpret_cast<uint64_t*>(&a.big_ticket[row * TSTRIDE + TS_LAST]), lastv,
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
   __syncthreads();
-  big_counts(a, row, tile, hist[tid], s4, last);
+  big_counts(a, row, tile, hist[tid], s4, last, a.big_tiles);
+}
+
+// The entries a row's passes after the first sort: all of them, or those at
+// p >= 2^-26 (KCUT), as the first pass's counts found.
+XS_DEV int big_sorted(const Args& a, int row) { return a.big_ticket[row * TSTRIDE + TS_N]; }
+XS_DEV int big_sorted_tiles(const Args& a, int row) { return (big_sorted(a, row) + BTILE - 1) / BTILE; }
+// The sorted entries a row's chains add: its kk candidates, or those the cut
+// kept (every term past them is absorbed).
+XS_DEV int big_chain_len(const Args& a, int row, const BigRow* br) {
+  return (a.big_cut && br->kk == (int)a.enc) ? big_sorted(a, row) : br->kk;
 }
 
 // Grid: rows x big_tiles.  Pass `pass`'s digit counts of the reordered tiles.
@@ -3867,8 +3908,10 @@ __global__ __launch_bounds__(BLOCK) void big_hist_kernel(Args a, int pass) {
   const int row = blockIdx.x / a.big_tiles, tile = blockIdx.x % a.big_tiles;
   Cfg cfg;
   if (!big_live(a, row, cfg)) return;
+  const int ntl = big_sorted_tiles(a, row);  // the tiles the first pass filled
+  if (tile >= ntl) return;
   const int tid = threadIdx.x;
-  const int t0 = tile * BTILE, nt = min(BTILE, (int)a.enc - t0);
+  const int t0 = tile * BTILE, nt = min(BTILE, big_sorted(a, row) - t0);
   // the keys: the high words of the entries
   const uint32_t* src = reinterpret_cast<const uint32_t*>(a.big + (int64_t)row * 2 * a.big_ld +
                                                          ((pass & 1) ? a.big_ld : 0) + t0);
@@ -3883,7 +3926,7 @@ __global__ __launch_bounds__(BLOCK) void big_hist_kernel(Args a, int pass) {
 #pragma unroll
   for (int s = 0; s < EPL; s++) count_digit(hist, rdigit(k[s], pass), s * BLOCK + tid < nt);
   __syncthreads();
-  big_counts(a, row, tile, hist[tid], s4, last);
+  big_counts(a, row, tile, hist[tid], s4, last, ntl);
 }
 
 // One stable pass: the tile's entries go to their digit's place among all
@@ -3896,8 +3939,11 @@ __global__ __launch_bounds__(BLOCK) void big_scatter_kernel(Args a, int pass) {
   const int row = blockIdx.x / a.big_tiles, tile = blockIdx.x % a.big_tiles;
   Cfg cfg;
   if (!big_live(a, row, cfg)) return;
+  // the first pass reads every id (in id order, KSENT on those left out),
+  // the others the entries it sorted
+  if (pass > 0 && tile >= big_sorted_tiles(a, row)) return;
   const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
-  const int t0 = tile * BTILE, nt = min(BTILE, (int)a.enc - t0);
+  const int t0 = tile * BTILE, nt = min(BTILE, (pass == 0 ? (int)a.enc : big_sorted(a, row)) - t0);
   uint64_t* const A = a.big + (int64_t)row * 2 * a.big_ld;
   const uint64_t* src = A + ((pass & 1) ? a.big_ld : 0) + t0;
   uint64_t* dst = A + ((pass & 1) ? 0 : a.big_ld);
@@ -3919,7 +3965,8 @@ __global__ __launch_bounds__(BLOCK) void big_scatter_kernel(Args a, int pass) {
   wave_lds_sync();
 #pragma unroll 1
   for (int s = 0; s < EPL; s++) {
-    count_digit(cnt[wave], rdigit((uint32_t)(ent[wave][s * 64 + lane] >> 32), pass), q0 + s * 64 + lane < nt);
+    const uint32_t key = (uint32_t)(ent[wave][s * 64 + lane] >> 32);
+    count_digit(cnt[wave], rdigit(key, pass), q0 + s * 64 + lane < nt && key != KSENT);
     wave_lds_sync();
   }
   __syncthreads();
@@ -3935,8 +3982,8 @@ __global__ __launch_bounds__(BLOCK) void big_scatter_kernel(Args a, int pass) {
   // the entries, in order
 #pragma unroll 1
   for (int s = 0; s < EPL; s++) {
-    const bool valid = q0 + s * 64 + lane < nt;
     const uint64_t e = ent[wave][s * 64 + lane];
+    const bool valid = q0 + s * 64 + lane < nt && (uint32_t)(e >> 32) != KSENT;
     const uint32_t d = rdigit((uint32_t)(e >> 32), pass);
     const uint64_t pe = digit_peers(d, valid);
     const uint32_t at = valid ? cnt[wave][d] : 0u;
@@ -4198,7 +4245,7 @@ __global__ __launch_bounds__(BLOCK) void big_units_kernel(Args a, int which) {
   if (which == 0 && !renorm) return;
   const float sum = br->sum;
   if (which == 1 && renorm && !(sum > 0.0f)) return;  // no chain follows
-  const int kk = br->kk;
+  const int kk = big_chain_len(a, row, br);
   const int b0 = CHEAD + blk * CBLK;
   if (b0 >= kk) return;
   const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
@@ -4263,7 +4310,7 @@ __global__ __launch_bounds__(BLOCK) void big_sum_kernel(Args a) {
   Cfg cfg;
   const BigRow* br = big_live(a, row, cfg);
   if (!br || cfg.top_p >= 1.0f) return;
-  const int kk = br->kk;
+  const int kk = big_chain_len(a, row, br);
   const uint64_t* srt = a.big + (int64_t)row * 2 * a.big_ld + ((RPASS & 1) ? a.big_ld : 0);
   auto pw = [&](uint64_t e) __attribute__((always_inline)) { return pkey_p((uint32_t)(e >> 32)); };
   const int nbu = load_units(a, row, 0, L);
@@ -4280,6 +4327,7 @@ __global__ __launch_bounds__(BLOCK) void big_draw_kernel(Args a) {
   if (!br) return;
   const int tid = threadIdx.x;
   const int kk = br->kk;
+  const int n = big_chain_len(a, row, br);  // kk, or the entries the cut kept
   const uint64_t* srt = a.big + (int64_t)row * 2 * a.big_ld + ((RPASS & 1) ? a.big_ld : 0);
   auto pw = [&](uint64_t e) __attribute__((always_inline)) { return pkey_p((uint32_t)(e >> 32)); };
   const bool renorm = !(cfg.top_p >= 1.0f);
@@ -4296,8 +4344,8 @@ __global__ __launch_bounds__(BLOCK) void big_draw_kernel(Args a) {
       return renorm ? __fdiv_rn(v, sum) : v;
     };
     const int nbu = load_units(a, row, 1, L);
-    const ChainOut c = big_chain(srt, kk, 0.0f, renorm ? 1 : 0, cfg.top_p, ww, L, nbu, kk);
-    if (c.idx < kk) keep = c.idx + 1;
+    const ChainOut c = big_chain(srt, n, 0.0f, renorm ? 1 : 0, cfg.top_p, ww, L, nbu, n);
+    if (c.idx < n) keep = c.idx + 1;  // (not reached by the kept entries: not by any)
     const float tot = c.acc;  // the prefix through keep - 1
     if (!(tot > 0.0f)) {
       st = XS_ROW_ZERO_WEIGHT;
@@ -4305,8 +4353,13 @@ __global__ __launch_bounds__(BLOCK) void big_draw_kernel(Args a) {
       // the index: the cumulative weights (prefix through i, i < keep - 1; the
       // total from keep - 1 on) at or below x
       const float x = a.uniforms[row] * tot + 0.0f;
-      const ChainOut d = big_chain(srt, keep - 1, 0.0f, 2, x, ww, L, nbu, kk);
-      tok = (int)(uint32_t)srt[d.idx < keep - 1 ? d.idx : keep - 1];
+      const int m = min(keep - 1, n);
+      const ChainOut d = big_chain(srt, m, 0.0f, 2, x, ww, L, nbu, n);
+      const int idx = d.idx < m ? d.idx : keep - 1;
+      // past the kept entries (every cumulative weight at or below x) the
+      // index is the row's last: its largest (pkey, id)
+      tok = idx < n ? (int)(uint32_t)srt[idx]
+                    : (int)(uint32_t)*reinterpret_cast<const uint64_t*>(&a.big_ticket[row * TSTRIDE + TS_LAST]);
     }
   }
   if (tid == 0) {
@@ -4436,6 +4489,7 @@ int launch(xs_context* ctx, xs::Args& a, int64_t rows, int span, bool mask, bool
   a.big_ticket = ctx->big_ticket;
   a.big_tiles = (int32_t)((a.enc + xs::BTILE - 1) / xs::BTILE);
   a.big_nblk = (int32_t)(a.enc > xs::CHEAD ? (a.enc - xs::CHEAD + xs::CBLK - 1) / xs::CBLK : 0);
+  a.big_cut = (a.big && !a.cand_id && !a.cand_w && a.enc <= (1 << 20)) ? 1 : 0;
   if (a.big && rows * (int64_t)a.big_tiles > 0x7FFFFFFF) return XS_ERR_CAPACITY;  // the whole-row grids
   a.serial = (serial && (mask || ctl)) ? 1 : 0;
   a.ser_sum = ctx->ser_sum;

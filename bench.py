@@ -252,7 +252,8 @@ WORKLOAD_TEXT = {
     "c2": "C2 batched sampling: 64 rows x V=248,320 fp32, T 0.7 / top_k 20 / top_p 0.80, "
           "one uniform per row",
     "c2w": "C2 rows with top_k >= V, the whole-row (top-p-only) path: 64 rows x V=248,320 fp32, "
-           "T 0.7 / top_p 0.80, the candidate set the whole row sorted by (p desc, id asc)",
+           "T 0.7 / top_p 0.80, tokens only: the row sorted by (p desc, id asc) but for the ids "
+           "at p < 1.75 * 2^-26, whose additions to the serial sums all round back",
     "c3": "C3 grammar-constrained sampling: 32 rows x V=248,320 fp32 + packed u32 allow-masks "
           "(1% / 10% / 50% dense, one one-hot), T 1.0 / top_k 20 / top_p 0.95",
     "c3p1": "C3 at top_p 1.0 with the top-20 candidate list and the softmax denominator: the "

@@ -372,8 +372,7 @@ struct CtlRow {
 };
 constexpr int CTL_MAX = XS_CTL_MAX;
 constexpr int TSTRIDE = 32;  // one arrival ticket per 128-byte line: tickets of different rows never share one
-constexpr int TS_N = 1;     // whole-row path, big_ticket line: the row's sorted entries
-constexpr int TS_LAST = 2;  // and two words: the row's last (pkey, id) (KCUT below)
+constexpr int TS_N = 1;  // whole-row path, big_ticket line: the row's sorted entries (KCUT below)
 
 struct Args {
   const float* logits;
@@ -2056,10 +2055,7 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
     F.big.defer = defer ? 1 : 0;
     F.big.m_s = m_s;
     F.big.S = S;
-    if (cfg.big && a.big_state) {
-      a.big_state[row] = BigRow{defer ? 1 : 0, m_s, S, k, 1.0f};
-      if (defer) *reinterpret_cast<uint64_t*>(&a.big_ticket[row * TSTRIDE + TS_LAST]) = 0ull;
-    }
+    if (cfg.big && a.big_state) a.big_state[row] = BigRow{defer ? 1 : 0, m_s, S, k, 1.0f};
   }
   if (want_cands && stoch && st == XS_ROW_OK && !defer) {
     const int kw = (int)min((int64_t)k, a.cand_ld);  // a short cand_ld truncates the list
@@ -3716,10 +3712,16 @@ constexpr int CHEAD = 128;          // chain terms added one at a time first
 // 0.9.  So each left-out term, raw (p) or renormalised (p / sum < 1.95 *
 // 2^-26), is below 2^-25, half an ulp of any sum of 0.5 or more, and every
 // addition of one rounds back to the sum.  No chain depends on them or their
-// order, except the draw's index past every cumulative weight, which takes
-// the row's last entry: the row's largest (pkey, id), kept aside.
+// order.  (The draw's index never passes every cumulative weight: u <= 1 -
+// 2^-23 keeps x = rn(u * total) below the total, which is at least 0.9.  A
+// uniform outside that range takes the last kept entry.)  big_key_kernel
+// decides most ids with a plain f32 exp and a margin (PLO), and computes the
+// correctly rounded p only for the rest.
 constexpr uint32_t KCUT = 0x7FFFFFFFu - 0x32E00000u;  // pkey(1.75 * 2^-26)
 constexpr uint32_t KSENT = 0xFFFFFFFFu;
+// 1.75 * 2^-26 * (1 - 2^-10): an f32 estimate exp2(d * log2e) / S below it
+// (off by under 1e-5 relative for the d that reach it) is a p below the cut
+constexpr float PLO = 0x1.bf9p-26f;
 constexpr int NG = 4;               // binades whose grid units big_units_kernel sums per block
 constexpr int FTOP = 127;           // the highest of them: sums of probabilities stay below 2
 constexpr int NBU = 256;            // blocks whose units a chain holds in LDS
@@ -3807,6 +3809,7 @@ XS_DEV void big_counts(const Args& a, int row, int tile, uint32_t c, int32_t* s4
 // pass's digit counts.
 template <bool HAS_MASK, bool HAS_CTL>
 __global__ __launch_bounds__(BLOCK) void big_key_kernel(Args a) {
+  __shared__ struct { uint2 ent[NWAVE][SPT * 256]; } Kl;  // per wave: (value bits, id) for the exact p
   __shared__ double expt[64];
   __shared__ uint32_t hist[RBINS];
   __shared__ int32_t s4[NWAVE];
@@ -3843,12 +3846,14 @@ __global__ __launch_bounds__(BLOCK) void big_key_kernel(Args a) {
     phi = a.ctl_chunk[(int64_t)row * (a.n_chunks + 1) + chunk + 1];
   }
   const bool ctl_on = HAS_CTL && cr.active;
-  const bool cut = a.big_cut && br->kk == enc;  // p < 2^-26 stays out of the sort (KCUT)
-  uint64_t lastv = 0;                           // the tile's largest (pkey, id)
+  const bool cut = a.big_cut && br->kk == enc;  // p < 1.75 * 2^-26 stays out of the sort (KCUT)
   if (tid < 64) expt[tid] = (&kExpT[0][0])[tid];
   hist[tid] = 0u;
   __syncthreads();
   uint64_t* const A = a.big + (int64_t)row * 2 * a.big_ld;
+  const int lane = lane_id(), wave = wave_id();
+  int nl = 0;  // this wave's ids left for the exact p (a cut row)
+  const float invS = 1.0f / S;
 #pragma unroll
   for (int j = 0; j < SPT; j++) {
     if (j >= ns) break;  // (uniform)
@@ -3861,14 +3866,28 @@ __global__ __launch_bounds__(BLOCK) void big_key_kernel(Args a) {
       else if (HAS_MASK && !((mw[j] >> ((id0 + e) & 31)) & 1u)) x[e] = -INFINITY;
     }
     if (ctl_on) ctl_slot(x, sb, tid, pl, pc, phi, cr.pull_id, cr.pull_val, cr.force_id, cr.force_val);
+    if (cut) {
+      // the plain estimate decides the ids well below the cut; the others go
+      // to the wave's list, for the exact p below with every lane busy
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int id = id0 + e;
+        const bool in = id < enc;
+        const float sv = cfg.scale ? x[e] * cfg.inv : x[e];
+        const float pa = xexp2((sv - m_s) * LOG2E) * invS;
+        const bool need = in && !(pa < PLO);
+        const uint64_t b = __ballot(need);
+        if (need) Kl.ent[wave][nl + lanes_below(b)] = make_uint2(__float_as_uint(x[e]), (uint32_t)id);
+        nl += (int)__popcll(b);
+        if (in && !need) A[id] = ((uint64_t)KSENT << 32) | (uint32_t)id;
+      }
+      continue;
+    }
     uint32_t k[4];
 #pragma unroll
     for (int e = 0; e < 4; e++) {
       k[e] = pkey(exact_p(x[e], cfg, m_s, S, expt));
-      const bool in = id0 + e < enc;
-      if (cut && in) lastv = max(lastv, ((uint64_t)k[e] << 32) | (uint32_t)(id0 + e));
-      if (cut && k[e] > KCUT) k[e] = KSENT;
-      count_digit(hist, rdigit(k[e], 0), in && k[e] != KSENT);
+      count_digit(hist, rdigit(k[e], 0), id0 + e < enc);
     }
     if (id0 + 3 < enc) {
 #pragma unroll
@@ -3880,11 +3899,17 @@ __global__ __launch_bounds__(BLOCK) void big_key_kernel(Args a) {
     }
   }
   if (cut) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) lastv = max(lastv, shfl_xor64(lastv, o));
-    if (lane_id() == 0 && lastv != 0)
-      __hip_atomic_fetch_max(reinterpret_cast<uint64_t*>(&a.big_ticket[row * TSTRIDE + TS_LAST]), lastv,
-                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    wave_lds_sync();
+#pragma unroll 1
+    for (int b0 = 0; b0 < nl; b0 += 64) {
+      const int i = b0 + lane;
+      const bool v = i < nl;
+      const uint2 it = Kl.ent[wave][v ? i : 0];
+      uint32_t k = pkey(exact_p(__uint_as_float(it.x), cfg, m_s, S, expt));
+      if (k > KCUT) k = KSENT;  // (below the cut after all)
+      count_digit(hist, rdigit(k, 0), v && k != KSENT);
+      if (v) A[it.y] = ((uint64_t)k << 32) | it.y;
+    }
   }
   __syncthreads();
   big_counts(a, row, tile, hist[tid], s4, last, a.big_tiles);
@@ -4356,10 +4381,7 @@ __global__ __launch_bounds__(BLOCK) void big_draw_kernel(Args a) {
       const int m = min(keep - 1, n);
       const ChainOut d = big_chain(srt, m, 0.0f, 2, x, ww, L, nbu, n);
       const int idx = d.idx < m ? d.idx : keep - 1;
-      // past the kept entries (every cumulative weight at or below x) the
-      // index is the row's last: its largest (pkey, id)
-      tok = idx < n ? (int)(uint32_t)srt[idx]
-                    : (int)(uint32_t)*reinterpret_cast<const uint64_t*>(&a.big_ticket[row * TSTRIDE + TS_LAST]);
+      tok = (int)(uint32_t)srt[min(idx, n - 1)];  // (past n only for a uniform of 1 or more)
     }
   }
   if (tid == 0) {

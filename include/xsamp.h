@@ -255,8 +255,11 @@ typedef struct {
   int64_t allowed_words, allowed_ld;
   const int32_t* drafts;        /* [seqs, span - 1] */
   const int32_t* budget;        /* [seqs] max committed tokens, or NULL = unbounded */
-  int32_t n_eog;                /* 0..8 end-of-generation ids (Sampler::is_eog) */
-  int32_t eog[8];
+  /* end-of-generation ids (Sampler::is_eog, sampler.rs:245-247; the
+   * reference's eog is a Vec<u32>, sampler.rs:130): n_eog >= 0 ids at the
+   * device pointer eog (NULL when n_eog is 0) */
+  int32_t n_eog;
+  const int32_t* eog;           /* [n_eog] */
   /* outputs */
   int32_t* row_token;    /* [seqs * span] every row's sampled id */
   int32_t* row_status;   /* [seqs * span] */

@@ -143,7 +143,8 @@ def test_argmax_and_verify_argument_errors(setup):
 
     assert vf(span=0) == E
     assert vf(seqs=-1) == E
-    assert vf(n_eog=9) == E
+    assert vf(n_eog=2) == E                                  # two ids at a NULL list
+    assert vf(n_eog=-1) == E
     assert vf(drafts=None) == E                              # span > 1 needs drafts
     assert vf(accepted=None) == E
     assert vf(seqs=ROWS, span=4) == CAP                      # 32 rows > 8

@@ -3,7 +3,8 @@ rows at a time (xs_sampler.hip, verify_walk), so its stops are checked on
 either side of the 64- and 128-row group edges against the oracle's
 accept_drafts (generate.rs:4020-4046): a mismatched draft, a spent budget, an
 end-of-generation token, a failed (NaN) row, a draft that completes the
-grammar, and a sequence that accepts every draft and commits the bonus row."""
+grammar, and a sequence that accepts every draft and commits the bonus row.
+The end-of-generation list holds 71 ids."""
 import numpy as np
 import pytest
 
@@ -15,6 +16,9 @@ pytestmark = pytest.mark.gpu
 SPAN = 130   # three groups of 64 rows: 0-63, 64-127, 128-129
 ENC = 4096
 EOG_ID = 4001
+# an end-of-generation list longer than a fixed array would hold (the
+# reference's eog is a Vec<u32>): the planted id sits in its middle
+EOG_LIST = list(range(4100, 4130)) + [EOG_ID] + list(range(4200, 4240))
 
 
 def test_walks_across_group_edges(oracle):
@@ -50,7 +54,7 @@ def test_walks_across_group_edges(oracle):
         p = xsm.params_tensor(0.0, 1, 1.0, rows, "cuda")
         u = dev(np.zeros(rows, np.float32))
         out = xsm.verify_batch(ctx, dev(x), seqs, SPAN, p, u, dev(drafts), budget=dev(budgets),
-                               eog=[EOG_ID], done_after=dev(done.reshape(-1)))
+                               eog=EOG_LIST, done_after=dev(done.reshape(-1)))
         torch.cuda.synchronize()
         row_tok = out.row_token.cpu().numpy()
         row_st = out.row_status.cpu().numpy()

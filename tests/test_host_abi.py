@@ -92,7 +92,8 @@ def test_verify_and_argmax_argument_checks(host):
             setattr(a, k, v)
         return host.xs_host_check_verify(C.byref(LIM), C.byref(a))
     assert vf() == OK
-    assert vf(span=0) == E and vf(seqs=-1) == E and vf(n_eog=9) == E and vf(n_eog=-1) == E
+    assert vf(span=0) == E and vf(seqs=-1) == E and vf(n_eog=-1) == E
+    assert vf(n_eog=2) == E and vf(n_eog=2, eog=DEV) == OK and vf(n_eog=300, eog=DEV) == OK
     assert vf(drafts=None) == E and vf(drafts=None, span=1) == OK
     assert vf(accepted=None) == E and vf(seq_status=None) == E
     assert vf(seqs=3) == CAP                                      # 12 rows > 8

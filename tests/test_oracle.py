@@ -265,6 +265,85 @@ def test_serial_sum_spread_on_the_workload_rows(oracle):
     assert all(mx < 5e-3 for _, mx in spread.values())
 
 
+def test_serial_f32_fold_stops_at_two_to_the_24(oracle):
+    """SUM_SEQ_F32 is the reference's one-at-a-time f32 fold (sampler.rs:301-305):
+    2^25 equal logits make 2^25 terms of exactly 1, and a serial f32 sum stops
+    at 2^24 (2^24 + 1 rounds to even, back to 2^24); a pairwise or exact sum
+    reaches 2^25, so either would fail here."""
+    n = 1 << 25
+    _, mx, ssum = oracle.softmax_in_place(np.zeros(n, np.float32), 1.0, oracle.SUM_SEQ_F32)
+    assert mx == 0.0 and ssum == 2.0 ** 24
+    _, _, exact = oracle.softmax_in_place(np.zeros(n, np.float32), 1.0, oracle.SUM_F64)
+    assert exact == 2.0 ** 25
+
+
+def test_serial_f32_fold_runs_in_id_order(oracle):
+    """The fold adds the terms in id order from +0: a row whose max comes
+    first absorbs every later term below half an ulp of 1 (exp(-20) < 2^-25),
+    so its sum is exactly 1; the same terms with the max last accumulate first
+    and end near 1 + n exp(-20).  A reversed fold swaps the two results.  The
+    second value is checked against numpy's cumsum, a sequential f32 loop of
+    its own."""
+    n = 200_000
+    first = np.concatenate([[0.0], np.full(n, -20.0)]).astype(np.float32)
+    last = np.concatenate([np.full(n, -20.0), [0.0]]).astype(np.float32)
+    _, _, s_first = oracle.softmax_in_place(first, 1.0, oracle.SUM_SEQ_F32)
+    _, _, s_last = oracle.softmax_in_place(last, 1.0, oracle.SUM_SEQ_F32)
+    t = np.float32(oracle.exp(-20.0))
+    assert s_first == 1.0
+    want = np.cumsum(np.concatenate([np.full(n, t, np.float32), [np.float32(1.0)]]),
+                     dtype=np.float32)[-1]
+    assert s_last == want and abs(s_last - (1.0 + n * float(t))) < 1e-3
+
+
+def _lse_of(m: float, denom: float) -> float:
+    return float(np.float64(m) + math.log(denom))
+
+
+def test_held_row_fold_of_equal_terms_after_the_max(oracle):
+    """held_row's f64 fold (generate.rs:1931-1932) in id order from the max:
+    once the max's term 1.0 is in, each later term t lands on the 2^-52 grid
+    of [1, 2), so n equal terms t >= 2^-53 after the max give exactly
+    1 + n * rint(2^52 t) * 2^-52, and terms below 2^-53 are absorbed (the
+    denominator stays exactly 1, where an exact sum would not).  An exact or
+    pairwise sum differs from both closed forms."""
+    n = 100_000
+    for d in (-14.0, -20.0, -30.0, -36.0):   # t = exp(d) >= 2^-53, n t < 1
+        row = np.concatenate([[5.0], np.full(n, 5.0 + d)]).astype(np.float32)
+        dd = float(np.float32(np.float32(5.0 + d) - np.float32(5.0)))
+        t = math.exp(dd)
+        units = round(t * 2.0 ** 52)  # t * 2^52 is not a half-integer for these t
+        denom = 1.0 + n * units * 2.0 ** -52
+        assert denom < 2.0
+        st, mx, lse = oracle.held_row(row, row.size)
+        assert st == 0 and mx == 5.0
+        assert lse == _lse_of(5.0, denom), (d, lse, _lse_of(5.0, denom))
+        assert lse != _lse_of(5.0, math.fsum([1.0] + [t] * n)) or units * 2.0 ** -52 == t
+    for d in (-37.0, -38.5, -40.0):          # t < 2^-53: absorbed
+        row = np.concatenate([[5.0], np.full(n, 5.0 + d)]).astype(np.float32)
+        st, mx, lse = oracle.held_row(row, row.size)
+        assert st == 0 and lse == 5.0  # ln(1) = 0 exactly
+        assert _lse_of(5.0, math.fsum([1.0] + [math.exp(d)] * n)) != 5.0
+
+
+def test_held_row_fold_with_the_max_last(oracle):
+    """The same terms with the max at the end: the fold sums them first (in f64,
+    serially: a Python float loop is such a fold) and adds 1.0 last, so terms
+    below 2^-53 now count.  Distinguishes the id-order fold from a reversed
+    one, which would absorb them."""
+    n = 50_000
+    for d in (-40.0, -20.0):
+        row = np.concatenate([np.full(n, 5.0 + d), [5.0]]).astype(np.float32)
+        t = math.exp(float(np.float32(np.float32(5.0 + d) - np.float32(5.0))))
+        acc = 0.0
+        for _ in range(n):
+            acc += t
+        acc += 1.0
+        st, mx, lse = oracle.held_row(row, row.size)
+        assert st == 0 and mx == 5.0 and lse == _lse_of(5.0, acc)
+        assert acc > 1.0
+
+
 # --- the draw ----------------------------------------------------------------
 
 def test_weighted_index_boundaries(oracle):

@@ -121,3 +121,19 @@ def test_noalloc_limits():
     torch.cuda.synchronize()
     st = out.status.cpu().numpy()
     assert st[0] == _lib.ROW_BAD_PARAM and st[1] == _lib.ROW_OK
+
+
+def test_noalloc_first_call_inside_graph_capture():
+    """A fresh process whose first xs_sample_noalloc call is captured into a HIP
+    graph (the entry point's one-time set-up then runs under the capture):
+    three replays with new uniforms equal xs_sample bit for bit, and eager
+    calls leave the device's free memory unchanged (tests/noalloc_capture_child.py)."""
+    _need_gpu()
+    import os
+    import subprocess
+    import sys
+    child = os.path.join(os.path.dirname(os.path.abspath(__file__)), "noalloc_capture_child.py")
+    print("starting the capture child process", flush=True)
+    r = subprocess.run([sys.executable, "-u", child], capture_output=True, text=True, timeout=300)
+    print(r.stdout[-2000:], r.stderr[-2000:], flush=True)
+    assert r.returncode == 0 and "noalloc-capture ok" in r.stdout

@@ -64,7 +64,7 @@ class VerifyArgs(C.Structure):
         ("logits", _vp), ("seqs", _i64), ("span", _i64), ("ld", _i64), ("width", _i64),
         ("enc", _i64), ("params", _vp), ("uniforms", _vp),
         ("allowed", _vp), ("allowed_words", _i64), ("allowed_ld", _i64),
-        ("drafts", _vp), ("budget", _vp), ("n_eog", _i32), ("eog", _i32 * 8),
+        ("drafts", _vp), ("budget", _vp), ("n_eog", _i32), ("eog", _vp),
         ("row_token", _vp), ("row_status", _vp), ("accepted", _vp), ("committed", _vp),
         ("n_committed", _vp), ("seq_status", _vp),
         ("controls", _vp), ("ctl_ids", _vp), ("ctl_delta", _vp), ("done_after", _vp),

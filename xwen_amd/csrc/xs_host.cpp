@@ -62,7 +62,8 @@ int xs_host_check_verify(const xs_host_limits* lim, const xs_verify_args* in) {
   if (!lim || !in || !in->row_token || !in->row_status || !in->accepted || !in->committed ||
       !in->n_committed || !in->seq_status)
     return XS_ERR_ARG;
-  if (in->seqs < 0 || in->span < 1 || in->n_eog < 0 || in->n_eog > 8 || in->k_max < 0) return XS_ERR_ARG;
+  if (in->seqs < 0 || in->span < 1 || in->n_eog < 0 || in->k_max < 0) return XS_ERR_ARG;
+  if (in->n_eog > 0 && !in->eog) return XS_ERR_ARG;
   if (in->span > 1 && !in->drafts) return XS_ERR_ARG;
   if (in->seqs > INT64_MAX / in->span) return XS_ERR_CAPACITY;
   return check_common(lim, in->logits, in->seqs * in->span, in->ld, in->width, in->enc, in->params,

@@ -401,7 +401,7 @@ struct Args {
   const int32_t* budget;
   const uint8_t* done_after;  // [seqs * span] or null: committing this draft completes the grammar
   int32_t n_eog;
-  int32_t eog[8];
+  const int32_t* eog;  // [n_eog] device ids
   int32_t* accepted;
   int32_t* committed;
   int32_t* n_committed;
@@ -3712,9 +3712,12 @@ constexpr int CHEAD = 128;          // chain terms added one at a time first
 // 0.9.  So each left-out term, raw (p) or renormalised (p / sum < 1.95 *
 // 2^-26), is below 2^-25, half an ulp of any sum of 0.5 or more, and every
 // addition of one rounds back to the sum.  No chain depends on them or their
-// order.  (The draw's index never passes every cumulative weight: u <= 1 -
-// 2^-23 keeps x = rn(u * total) below the total, which is at least 0.9.  A
-// uniform outside that range takes the last kept entry.)  big_key_kernel
+// order.  (The draw's index never passes every cumulative weight: any u <=
+// 1 - 2^-24, the largest float below 1, keeps x = rn(u * total) below a
+// normal total such as this one (at least 0.9): u * total <= total - total *
+// 2^-24, which is more than half an ulp of total below it, or exactly the
+// float below it when total is a power of two.  A uniform of 1 or more takes
+// the last kept entry.)  big_key_kernel
 // decides most ids with a plain f32 exp and a margin (PLO), and computes the
 // correctly rounded p only for the rest.
 constexpr uint32_t KCUT = 0x7FFFFFFFu - 0x32E00000u;  // pkey(1.75 * 2^-26)
@@ -4775,7 +4778,7 @@ int xs_verify(xs_context* ctx, const xs_verify_args* in) {
   a.drafts = in->drafts;
   a.budget = in->budget;
   a.n_eog = in->n_eog;
-  for (int i = 0; i < 8; i++) a.eog[i] = i < in->n_eog ? in->eog[i] : -1;
+  a.eog = in->eog;
   a.accepted = in->accepted;
   a.committed = in->committed;
   a.n_committed = in->n_committed;

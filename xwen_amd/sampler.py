@@ -350,6 +350,7 @@ class Verdict:
     committed: object
     n_committed: object
     seq_status: object
+    eog_ids: object = None
 
 
 def verify_batch(ctx: Context, logits, seqs: int, span: int, params, uniforms, drafts, *,
@@ -384,8 +385,11 @@ def verify_batch(ctx: Context, logits, seqs: int, span: int, params, uniforms, d
     a.drafts = drafts.data_ptr() if span > 1 else None
     a.budget = budget.data_ptr() if budget is not None else None
     a.n_eog = len(eog)
-    for i, e in enumerate(eog):
-        a.eog[i] = int(e)
+    if len(eog):
+        # a device list of any length (the reference's eog is a Vec<u32>); the
+        # verdict holds it until the caller drops the outputs, past the launch
+        out.eog_ids = torch.as_tensor(np.asarray([int(e) for e in eog], np.int64).astype(np.int32)).to(dev)
+        a.eog = out.eog_ids.data_ptr()
     a.row_token = out.row_token.data_ptr()
     a.row_status = out.row_status.data_ptr()
     a.accepted = out.accepted.data_ptr()

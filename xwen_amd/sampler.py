@@ -170,6 +170,17 @@ class Context:
         self.h = h
         self.max_rows, self.vocab, self.k_max, self.ctl_max = max_rows, vocab, k_max, ctl_max
 
+    def eog_list(self, eog):
+        """The end-of-generation ids as an int32 device tensor, uploaded once per
+        distinct list (Sampler::new's eog, sampler.rs:130)."""
+        key = tuple(int(e) for e in eog)
+        cache = self.__dict__.setdefault("_eog", {})
+        if key not in cache:
+            torch = _torch()
+            cache[key] = torch.as_tensor(np.asarray(key, np.int64).astype(np.int32)).to(
+                torch.device("cuda", self.device))
+        return cache[key]
+
     def bind_current_stream(self):
         torch = _torch()
         s = torch.cuda.current_stream(self.device).cuda_stream
@@ -386,9 +397,10 @@ def verify_batch(ctx: Context, logits, seqs: int, span: int, params, uniforms, d
     a.budget = budget.data_ptr() if budget is not None else None
     a.n_eog = len(eog)
     if len(eog):
-        # a device list of any length (the reference's eog is a Vec<u32>); the
-        # verdict holds it until the caller drops the outputs, past the launch
-        out.eog_ids = torch.as_tensor(np.asarray([int(e) for e in eog], np.int64).astype(np.int32)).to(dev)
+        # a device list of any length (the reference's eog is a Vec<u32>), kept
+        # by the context per distinct list: a call under graph capture reuses
+        # the list an earlier eager call uploaded
+        out.eog_ids = ctx.eog_list(eog)
         a.eog = out.eog_ids.data_ptr()
     a.row_token = out.row_token.data_ptr()
     a.row_status = out.row_status.data_ptr()

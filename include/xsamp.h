@@ -334,6 +334,17 @@ const char* xs_version(void);
  * it to compare the device exp with the CPU oracle's over millions of inputs. */
 int xs_test_exp(const float* x, float* y, int64_t n, void* hip_stream);
 
+/* Test hook (no reference counterpart): the finalizer's serial fallback.  A
+ * controlled row (allow-mask or active controls) that no serial_kernel pass
+ * finalizes is drawn with the exact softmax sum, and its finalizer checks
+ * that the reference's serial f32 sum (sampler.rs:301-305) would draw the
+ * same token; a row the check cannot settle is summed serially by its own
+ * workgroup and drawn again.  *count (if not null) receives how many rows
+ * took that fallback on this context so far (the call synchronizes the
+ * context's stream); force != 0 sends every checked row of later calls
+ * there, force == 0 restores the check. */
+int xs_test_serial_fallback(xs_context* ctx, int32_t force, uint32_t* count);
+
 #ifdef __cplusplus
 }
 #endif

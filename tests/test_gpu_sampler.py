@@ -14,11 +14,15 @@ How each row is checked:
   * against the literal reference order (serial f32 sum, sampler.rs:301-305),
     tokens must agree on every row whose decision margins exceed MARGIN_EPS;
     rows below it are counted and reported, never re-seeded away.
-  * controlled rows (an allow-mask or sparse controls) at top_p >= 1, whose
-    weights p = e / sum reach the caller unrenormalized: the device
-    denominator must be the reference's serial f32 sum bit for bit (oracle
-    SUM_SEQ_F32), so the token and every weight equal the literal reference's
-    with no margin rule.
+  * controlled rows (an allow-mask or sparse controls), whose reference
+    denominator is its serial f32 sum (oracle SUM_SEQ_F32): the token and the
+    candidate ids equal the literal reference's on every row, with no margin
+    rule.  At top_p >= 1, where the weights p = e / sum reach the caller
+    unrenormalized, the device denominator is that serial sum bit for bit, so
+    every weight is the reference's too; elsewhere the device divides by the
+    exact sum (weights within PROB_RTOL of the reference's), unless the
+    finalizer found the token unsettled by it and summed the row serially
+    itself (then bit for bit again).
 """
 import math
 import os
@@ -37,6 +41,7 @@ MARGIN_EPS = 1e-5      # decision margin below which the serial-f32 order may fl
 V = workloads.V
 WORST = {}  # largest deviations seen, printed at the end of the module
 SERIAL_ROWS = [0]  # rows checked against the serial f32 denominator
+SERIAL_SEEN = {"controlled": 0, "serial_sum": 0}  # controlled rows, and those the device summed serially
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -61,8 +66,9 @@ def dev(x):
 
 
 def run_sample(ctx, logits, T, K, P, U, *, enc=None, width=None, mask=None, mask_words=None,
-               cand_k=128, n_top=0, ctls=None, k_max=0):
-    """One xs_sample call; `ctls` is one SampleControl (sparse part) or None per row."""
+               cand_k=128, n_top=0, ctls=None, k_max=0, stats=True):
+    """One xs_sample call; `ctls` is one SampleControl (sparse part) or None per row.
+    cand_k=0 and stats=False make it a tokens-only call."""
     from xwen_amd import sampler as xsm
     rows = logits.shape[0]
     lg = dev(np.asarray(logits, np.float32))
@@ -71,7 +77,7 @@ def run_sample(ctx, logits, T, K, P, U, *, enc=None, width=None, mask=None, mask
     m = None if mask is None else dev(np.asarray(mask, np.uint32).view(np.int32))
     controls = None if ctls is None else xsm.controls_tensor(ctls, "cuda")
     out = xsm.sample_batch(ctx, lg, p, u, enc=enc, width=width, allowed=m,
-                           allowed_words=mask_words, cand_k=cand_k, stats=True, n_top=n_top,
+                           allowed_words=mask_words, cand_k=cand_k, stats=stats, n_top=n_top,
                            controls=controls, k_max=k_max)
     torch.cuda.synchronize()
     return {k: (None if v is None else v.cpu().numpy()) for k, v in vars(out).items()}
@@ -88,12 +94,45 @@ def oracle_row(oracle, row, enc, T, k, p, u, mask_row=None, ctl=None, **kw):
                                     **kw)
 
 
-def serial_row(T, K, P, mask_row, ctl) -> bool:
-    """A row whose denominator is the serial f32 sum on the device: stochastic,
-    controlled (sample_controlled's non-noop branch, sampler.rs:222-229), and
-    top_p >= 1."""
+def controlled_row(T, K, P, mask_row, ctl) -> bool:
+    """A stochastic row on the reference's control path (sample_controlled's
+    non-noop branch, sampler.rs:222-229), whose denominator is its serial f32
+    sum (sampler.rs:301-305)."""
     controlled = mask_row is not None or (ctl is not None and not ctl.is_noop())
-    return not (T <= 0.0 or K <= 1) and P >= 1.0 and controlled
+    return not (T <= 0.0 or K <= 1) and controlled
+
+
+def serial_row(T, K, P, mask_row, ctl) -> bool:
+    """A row whose denominator is the serial f32 sum on the device in a call
+    that observes it (candidates or soft_sum): controlled and top_p >= 1."""
+    return controlled_row(T, K, P, mask_row, ctl) and P >= 1.0
+
+
+def check_controlled(oracle, row, enc, T, k, p, u, d, r, mrow, kw, tag):
+    """A controlled stochastic row against the literal reference (the oracle
+    with the serial f32 sum): status and token always; candidate ids, and the
+    weights within PROB_RTOL (bit for bit when the device used that sum).
+    Returns whether the device's denominator, when reported, is the serial sum."""
+    oseq = oracle_row(oracle, row, enc, T, k, p, u, mrow, sum_mode=oracle.SUM_SEQ_F32, **kw)
+    assert d["status"][r] == oseq.status, (tag, "status", d["status"][r], oseq.status)
+    SERIAL_SEEN["controlled"] += 1
+    if oseq.status != 0:
+        return False
+    assert d["token"][r] == oseq.token, (tag, "serial-f32 token", d["token"][r], oseq.token)
+    serial_sum = False
+    if d.get("soft_sum") is not None:
+        serial_sum = np.float32(d["soft_sum"][r]).view(np.uint32) == np.float32(oseq.ssum).view(np.uint32)
+        SERIAL_SEEN["serial_sum"] += int(serial_sum)
+    if d.get("cand_id") is not None:
+        ncmp = min(len(oseq.cand), d["cand_id"].shape[1])
+        assert list(d["cand_id"][r, :ncmp]) == [i for _, i in oseq.cand][:ncmp], (tag, "serial-f32 ids")
+        ws = np.array([w for w, _ in oseq.cand][:ncmp], np.float32)
+        if serial_sum:
+            np.testing.assert_array_equal(d["cand_w"][r, :ncmp].view(np.uint32), ws.view(np.uint32),
+                                          err_msg=tag)
+        else:
+            np.testing.assert_allclose(d["cand_w"][r, :ncmp], ws, rtol=PROB_RTOL, atol=1e-30, err_msg=tag)
+    return serial_sum
 
 
 def check_rows(oracle, logits, T, K, P, U, d, *, enc=None, mask=None, rows=None, margins=True,
@@ -138,15 +177,17 @@ def check_rows(oracle, logits, T, K, P, U, d, *, enc=None, mask=None, rows=None,
         o64 = oracle_row(oracle, logits[r], enc, T[r], K[r], P[r], U[r], mrow,
                          sum_mode=oracle.SUM_F64, **kw)
         rel = abs(float(S) - float(o64.ssum)) / float(o64.ssum)
-        if serial_row(T[r], K[r], P[r], mrow, kw.get("ctl")):
-            # the literal reference: its serial f32 sum, bit for bit
-            oseq = oracle_row(oracle, logits[r], enc, T[r], K[r], P[r], U[r], mrow,
-                              sum_mode=oracle.SUM_SEQ_F32, **kw)
-            assert np.float32(S).view(np.uint32) == np.float32(oseq.ssum).view(np.uint32), \
-                (tag, "serial sum", float(S), float(oseq.ssum))
-            assert d["token"][r] == oseq.token, (tag, "serial-f32 token")
-            WORST["serial_vs_exact"] = max(WORST.get("serial_vs_exact", 0.0), rel)
-            SERIAL_ROWS[0] += 1
+        if controlled_row(T[r], K[r], P[r], mrow, kw.get("ctl")):
+            # the literal reference (its serial f32 sum): token and ids always
+            serial_sum = check_controlled(oracle, logits[r], enc, T[r], K[r], P[r], U[r], d, r, mrow, kw, tag)
+            if serial_row(T[r], K[r], P[r], mrow, kw.get("ctl")):  # observed at top_p >= 1: bit for bit
+                assert serial_sum, (tag, "serial sum", float(S))
+            if serial_sum:
+                WORST["serial_vs_exact"] = max(WORST.get("serial_vs_exact", 0.0), rel)
+                SERIAL_ROWS[0] += 1
+            else:
+                WORST["denominator"] = max(WORST.get("denominator", 0.0), rel)
+                assert rel <= DENOM_RTOL, (tag, float(S), o64.ssum, rel)
             continue
         WORST["denominator"] = max(WORST.get("denominator", 0.0), rel)
         assert rel <= DENOM_RTOL, (tag, float(S), o64.ssum, rel)

@@ -309,10 +309,14 @@ struct Cfg {
   bool greedy, scale, full, bad;
   bool big;      // more candidates than the streaming selection holds: the
                  // whole-row kernels draw the row
+  bool force;    // a controlled row's check always sends it to the serial fallback (test hook)
+  float dthr;    // 2^-148 / S times every denominator the serial sum of enc terms can take
 };
 
-XS_DEV Cfg make_cfg(const xs_row_params& p, int64_t enc, int n_top, int k_max) {
+XS_DEV Cfg make_cfg(const xs_row_params& p, int64_t enc, int n_top, int k_max, int force = 0) {
   Cfg c;
+  c.force = force != 0;
+  c.dthr = (1.01f + (float)enc * 0x1p-24f * 1.02f) * 0x1p-148f;
   c.greedy = (p.temperature <= 0.0) || (p.top_k <= 1);
   c.scale = p.temperature != 1.0;
   c.inv = (float)(1.0 / p.temperature);
@@ -347,7 +351,8 @@ XS_DEV Cfg greedy_cfg() {
   c.k = 0;
   c.kp = 1;
   c.greedy = true;
-  c.scale = c.full = c.bad = c.big = false;
+  c.scale = c.full = c.bad = c.big = c.force = false;
+  c.dthr = 0.0f;
   return c;
 }
 
@@ -436,9 +441,16 @@ struct Args {
   int32_t big_tiles;         // tiles of BTILE ids per row
   int32_t big_nblk;          // chain blocks per row past the first CHEAD terms
   int32_t big_cut;           // tokens only, enc <= 2^20: rows at top_k >= enc sort only p >= 2^-26
-  // the serial denominator (serial_kernel): set on calls with a mask or
-  // controls, whose rows at top_p >= 1 serial_kernel finalizes
+  // the serial denominator (serial_kernel), on calls with a mask or controls:
+  // bit 0, the call observes it (candidates or soft_sum), and serial_kernel
+  // finalizes its controlled rows at top_p >= 1; bit 1, the call may hold
+  // rows of top_k >= 128, and serial_kernel finalizes its controlled ones
   int32_t serial;
+  // the finalizer's fallback to the serial sum (ser_local) for the other
+  // controlled rows: rows sent there are counted (null: not counted), and
+  // ser_force sends every checked row there (a test hook)
+  uint32_t* ser_count;
+  int32_t ser_force;
   // split launch: sample_kernel's workgroups publish and exit; finalize_kernel
   // (one workgroup per row) finalizes every row afterwards
   int32_t split;
@@ -711,13 +723,37 @@ struct FinLds {
   uint32_t zmap[KSEL / 32];         // a whole short row: the ids with p > 0
   HeldLds held;
   BigStash big;
+  int32_t need_ser;                 // the exact denominator did not settle this controlled row's token
+  float ser_ms;                     // and its scaled max, for the serial sum
+};
+// The serial denominator's segments (serial_kernel, ser_local): SEG ids each,
+// one wave's float4s of one slot.
+constexpr int SEG = 256;               // ids per segment
+constexpr int SER_QCAP = 128;          // per wave: terms queued for the correctly rounded exp
+// What one workgroup needs to sum one row's serial denominator by itself
+// (ser_local): one chunk's segment sums, prefixes, grid units and flags, the
+// queue of terms for the correctly rounded exp, the chunk's summaries for the
+// walk, a segment of recounted terms, and the running sums.
+struct SerLocal {
+  double expt[64];
+  double segsum[SPC * NWAVE];
+  double segpre[SPC * NWAVE];
+  uint32_t R[SPC * NWAVE][2];
+  uint32_t meta[SPC * NWAVE];
+  float qd[NWAVE][SER_QCAP];
+  uint8_t qt[NWAVE][SER_QCAP];
+  uint64_t sum[SPC * NWAVE][2];
+  float scr[SEG];
+  double X;                         // exact sum of the chunks walked so far
+  uint32_t sb;                      // the serial sum's bits after them
 };
 // The chunk pass stages each wave's entries here before it publishes them;
 // after the hand-off only the row's last workgroup uses the memory again, as
-// its finalizer's.
+// its finalizer's (and, for a row the finalizer sends back, its serial sum's).
 union TailLds {
   uint64_t stage[NWAVE][CAPW];
   FinLds fin;
+  SerLocal ser;
 };
 // p = rn(e / S) of one controlled logit v (the reference's softmax_in_place:
 // v *= inv unless T == 1, then exp(v - max), then / sum; sampler.rs:289-310).
@@ -727,6 +763,12 @@ XS_DEV float exact_p(float v, const Cfg& cfg, float m_s, float S, TAB T) {
   const float s = cfg.scale ? v * cfg.inv : v;
   const float e = cr_expf(s - m_s, T);
   return __fdiv_rn(e, S);
+}
+// The softmax numerator e = exp(v * inv - max) of the same logit (p = e / S).
+template <typename TAB>
+XS_DEV float exact_e(float v, const Cfg& cfg, float m_s, TAB T) {
+  const float s = cfg.scale ? v * cfg.inv : v;
+  return cr_expf(s - m_s, T);
 }
 
 // The largest float below f (f > -inf, not NaN).
@@ -1146,6 +1188,139 @@ XS_DEV void held_fold(const Args& a, int row, const float* rowp, const uint64_t*
 }
 
 // ---------------------------------------------------------------------------
+// Whether the exact denominator settles a controlled row's token.
+//
+// On a controlled row the reference divides by its serial f32 sum S' of the
+// softmax terms (sampler.rs:301-305); the finalizer divided by S, the exact
+// sum rounded to f32.  A serial sum of n terms >= 0 lies within a factor
+// 1 +- n 2^-24 of the exact one, and every weight rn(e / D) of a denominator
+// D is e / D up to one rounding: the scale 1 / D is common to the weights,
+// the serial sums of weights, their renormalisation and u times their total,
+// so it cancels from every decision of the draw, and only roundings remain.
+// The token drawn with S is therefore the one drawn with S' when:
+//  - consecutive entries of the selection (logit order: e non-increasing)
+//    have equal e (equal p for every D, ordered by id), or e so far apart
+//    that no D rounds them to one p: e_a - e_b > 2^-22 e_a (more than an ulp
+//    of the larger p) and e_a - e_b > 2^-148 D (more than a subnormal ulp).
+//    Every D then yields the same candidates in the same order.  A call that
+//    takes tokens only passes over entries with e < 2^-65: their weights are
+//    under 2^-64 of the largest, never drawn, and move a sum by less than the
+//    2^-50 slack below;
+//  - a run of equal e that crosses the top-k boundary and reaches the last
+//    selected entry lies far above everything outside the selection (at most
+//    e(next_below(vL)), or +0 when every finite value is selected);
+//  - the top-p cut and the draw hold with a margin over the roundings of both
+//    computations: a serial prefix c_j of renormalised weights is C_j (1 + r)
+//    with |r| <= (k + j + 2) 2^-24 (each p, the k-term sum, the division, j
+//    additions); x = rn(u T_w) is within (k + keep + 3) 2^-24 of u times its
+//    exact total; twice each (S and S'), plus the p's subnormal ulps.
+// A row that fails is summed serially by its finalizing wave (ser_local)
+// and finalized again with S'.  The order part (order_settled) runs as soon
+// as the selection's e are known, the margins (draw_settled) after the draw.
+template <int R>
+XS_DEV float at_lane(const float (&v)[R], int i) {  // element i of a list held R per lane (i uniform)
+  float out = 0.0f;
+#pragma unroll
+  for (int r = 0; r < R; r++)
+    if ((i >> 6) == r) out = rdlf(v[r], i & 63);
+  return out;
+}
+// The largest logit of the row below vL, the selection's last, or a bound
+// above it: each sub-record's entries are every element of its wave at or
+// above its filter floor (header word 7), and every floor lies at or below vL
+// (a wave with K' elements above vL would have put them in the selection), so
+// what lies below vL is an entry below vL or lies below some floor.  A
+// sub-record whose entries past the preloaded EPRE may hold the answer, or
+// whose floor is unknown (+inf after an overflow), gives next_below(vL).  One
+// wave; E: sub-records 0..63's first EPRE entries, as load_heads read them.
+XS_DEV float below_selection(const uint64_t* rowrec, int nsp, int nsub, const uint64_t (&E)[EPRE], float vL) {
+  const int lane = lane_id();
+  float best = -INFINITY;
+  for (int g = 0; g * 64 < nsub; g++) {
+    const int s = g * 64 + lane;
+    const bool live = s < nsub;
+    const int sc = min(s, nsp - 1);  // (clamped, not guarded: the loads go out together)
+    const uint64_t h3 = ld_agent(&rowrec[3 * nsp + sc]), h4 = ld_agent(&rowrec[4 * nsp + sc]);
+    const uint64_t h7 = ld_agent(&rowrec[7 * nsp + sc]);
+    uint64_t e[EPRE];
+#pragma unroll
+    for (int j = 0; j < EPRE; j++) e[j] = g == 0 ? E[j] : ld_agent(&rowrec[(SHDR + j) * nsp + sc]);
+    const int cnt = live ? (int)min((uint32_t)h4, (uint32_t)CAPW) : 0;
+    float mb = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < EPRE; j++) {
+      const float x = keyf(pk_key(e[j]));
+      if (j < cnt && x < vL) mb = fmaxf(mb, x);
+    }
+    const bool srt = ((h3 >> 32) & 4u) != 0;
+    const bool complete = cnt <= EPRE || (srt && keyf(pk_key(e[EPRE - 1])) < vL);
+    const float fl = __uint_as_float((uint32_t)h7);
+    float b = -INFINITY;
+    if (live) b = (complete && fl <= vL) ? fmaxf(mb, next_below(fl)) : next_below(vL);
+    best = fmaxf(best, b);
+  }
+  return wave_maxf(best);
+}
+
+template <int R>
+XS_DEV bool order_settled(const float (&ee)[R], int nsel, int kp, int k, bool full, float e_below, float S,
+                          float dthr, bool cands) {
+  const int lane = lane_id();
+  const float thr = S * dthr;  // 2^-148 D for every D the serial sum can take (f32: the constants carry 1 %)
+  const float NEG = 0x1p-65f;
+  auto robust = [&](float ea, float eb) __attribute__((always_inline)) {
+    const float g = ea - eb;  // (ea >= eb >= 0: exact when eb >= ea / 2, far above the bounds otherwise)
+    return ea == eb || (g > ea * 0x1p-21f && g > thr);
+  };
+  bool bad = false;
+#pragma unroll
+  for (int r = 0; r < R; r++) {  // consecutive selected entries i, i + 1
+    const float first_next = (r + 1 < R) ? rdlf(ee[r + 1 < R ? r + 1 : r], 0) : 0.0f;
+    const float en = lane == 63 ? first_next : __shfl(ee[r], (lane + 1) & 63);
+    const int i = r * 64 + lane;
+    if (i + 1 < nsel && (cands || ee[r] >= NEG) && !robust(ee[r], en)) bad = true;
+  }
+  bool ubad = false;  // (uniform)
+  const bool all_sel = nsel < kp;  // every finite value is selected; the rest are +0
+  if (nsel >= 1 && all_sel) {
+    const float el = at_lane(ee, nsel - 1);
+    if ((cands || el >= NEG) && !robust(el, 0.0f)) ubad = true;
+  }
+  if (!full && nsel > k && nsel >= 1) {
+    const float e1 = at_lane(ee, k - 1), eL = at_lane(ee, nsel - 1);
+    const float below = all_sel ? 0.0f : e_below;
+    if (e1 == eL && (cands || e1 >= NEG) && !(below < eL && robust(eL, below))) ubad = true;
+  }
+  return __ballot(bad) == 0 && !ubad;
+}
+template <int R>
+XS_DEV bool draw_settled(const float (&c)[R], float tot, float x, int idx, int keep, int k, bool cut_found,
+                         bool renorm, float S, float top_p) {
+  // Lane-parallel: lane j tests its own prefix c_j where a decision uses it,
+  // against uu (k + j + 4) c_j plus the slack; one ballot.  (f32 without
+  // divisions: a difference of close values is exact, the margins carry
+  // 2 %, and the p's subnormal ulps, 2^-150 / sum in renormalised units, are
+  // bounded with 1 / sum <= S.)
+  const int lane = lane_id();
+  const float uu = 0x1p-23f * 1.02f;
+  const float sl = (float)(2 * k + 8) * 0x1p-148f * S + 0x1p-50f;
+  const float mt = uu * (float)(k + keep + 4) * tot + sl;  // x's own share
+  const int jc = cut_found ? keep - 1 : k - 1;               // the top-p decision's prefix
+  bool bad = false;
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    const int j = r * 64 + lane;
+    const float cj = c[r];
+    const float m = uu * (float)(k + j + 4) * cj;
+    if (renorm && j == jc && !(cut_found ? cj - top_p > m + sl : top_p - cj > m + sl)) bad = true;
+    if (renorm && cut_found && j == keep - 2 && !(top_p - cj > m + sl)) bad = true;
+    if (j == idx - 1 && !(x - cj > m + mt)) bad = true;            // cum_(idx-1) <= x
+    if (j == idx && j < keep - 1 && !(cj - x > m + mt)) bad = true;  // x < cum_idx (at keep - 1: the total)
+  }
+  return __ballot(bad) == 0;
+}
+
+// ---------------------------------------------------------------------------
 // Row finalize, common case: at most 64 sub-records (one per lane), K' <= 64,
 // at most SURV survivors, and no boundary
 // tie that needs the id-ordered row scan.  Returns false (having written
@@ -1276,18 +1451,43 @@ XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, int nsub, const uin
   uint64_t pk = 0ull;
   float w = 0.0f;
   int tok = -1;
+  // a masked row not given the serial sum: its token is checked against the
+  // roundings that sum could change (order_settled, draw_settled); with one
+  // finite value the token is that id for every denominator
+  const bool check = HAS_MASK && S_ser < 0.0f && nsel > 1;
+  bool unsettled = false;
   if (stoch && st == XS_ROW_OK) {
     const float vL = nsel > 0 ? keyf(pk_key(rdl64(sel, nsel - 1))) : -INFINITY;
     const bool need_below = !cfg.full && vL != -INFINITY;
     const bool in = lane < nsel;
-    float pe = 0.0f;
-    if (in || (lane == nsel && need_below)) pe = exact_p(in ? keyf(pk_key(sel)) : next_below(vL), cfg, m_s, S, T);
+    float pe = 0.0f, ee = 0.0f;
+    if (in || (lane == nsel && need_below)) {
+      ee = exact_e(in ? keyf(pk_key(sel)) : next_below(vL), cfg, m_s, T);
+      pe = __fdiv_rn(ee, S);  // exact_p
+    }
     if (in) {
       pw = pe;
       pk = ((uint64_t)__float_as_uint(pe + 0.0f) << 32) | (uint64_t)(0xFFFFFFFFu - pk_id(sel));
     }
-    float pbelow = 0.0f;
-    if (need_below) pbelow = nsel < 64 ? rdlf(pe, nsel) : exact_p(next_below(vL), cfg, m_s, S, T);
+    float pbelow = 0.0f, ebelow = 0.0f;
+    if (need_below) {
+      if (nsel < 64) {
+        pbelow = rdlf(pe, nsel);
+        ebelow = rdlf(ee, nsel);
+      } else {
+        ebelow = exact_e(next_below(vL), cfg, m_s, T);
+        pbelow = __fdiv_rn(ebelow, S);
+      }
+    }
+    if (!in) ee = 0.0f;
+    if (check) {
+      const float ea[1] = {ee};
+      // a run of equal e across the top-k boundary: bounded below by the
+      // row's actual next logit rather than next_below(vL)
+      if (!cfg.full && nsel == kp && nsel > k && rdlf(ee, k - 1) == rdlf(ee, nsel - 1))
+        ebelow = exact_e(below_selection(rowrec, nsp, nsub, E, vL), cfg, m_s, T);
+      unsettled = !order_settled<1>(ea, nsel, kp, k, cfg.full, ebelow, S, cfg.dthr, want_cands);
+    }
     // (p desc, id asc): p is non-increasing along the logit order, so only
     // runs of equal p can be out of order
     const uint64_t nxt = shfl64(pk, (lane + 1) & 63);
@@ -1333,11 +1533,13 @@ XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, int nsub, const uin
       return acc;
     };
     bool zero = false;
-    if (!(cfg.top_p >= 1.0f)) {
+    const bool renorm = !(cfg.top_p >= 1.0f);
+    float sumc = 1.0f;
+    if (renorm) {
       float unused;
-      const float sum = chain(-0.0f, unused);  // folds from -0.0 as Rust's f32 Sum does
-      if (!(sum > 0.0f)) zero = true;  // all weights zero: returned unchanged
-      else w = __fdiv_rn(w, sum);
+      sumc = chain(-0.0f, unused);  // folds from -0.0 as Rust's f32 Sum does
+      if (!(sumc > 0.0f)) zero = true;  // all weights zero: returned unchanged
+      else w = __fdiv_rn(w, sumc);
     }
     if (zero) {
       st = XS_ROW_ZERO_WEIGHT;
@@ -1345,8 +1547,10 @@ XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, int nsub, const uin
       float c;
       (void)chain(0.0f, c);
       int keep = k;
-      if (!(cfg.top_p >= 1.0f)) {
+      bool found = false;
+      if (renorm) {
         const uint64_t bm = __ballot(lane < k && c >= cfg.top_p);
+        found = bm != 0ull;
         if (bm) keep = (int)__builtin_ctzll(bm) + 1;
         if (lane >= keep) w = 0.0f;
       }
@@ -1358,10 +1562,23 @@ XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, int nsub, const uin
         const float cum = lane < keep - 1 ? c : tot;
         const int idx = (int)__popcll(__ballot(lane < k - 1 && cum <= x_draw));
         tok = (int)pk_id(rdl64(pk, idx));
+        if (check) {
+          const float ca[1] = {c};
+          unsettled = unsettled || cfg.force ||
+                      !draw_settled<1>(ca, tot, x_draw, idx, keep, k, found, renorm, S, cfg.top_p);
+        }
       }
     }
   } else if (st == XS_ROW_OK) {
     tok = (int)pk_id(rdl64(sel, 0));
+  }
+
+  if (unsettled) {  // (nothing written) the workgroup sums the serial denominator
+    if (lane == 0) {
+      F.need_ser = 1;
+      F.ser_ms = m_s;
+    }
+    return true;
   }
 
   // held_row: the statistics for held_fold, which writes row_lse and the
@@ -1616,6 +1833,13 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
   // same pass, by the lane just past the selection
   const float vL = nsel > 0 ? keyf(pk_key(last_sel)) : -INFINITY;
   float pbelow = 0.0f;
+  float ee[2] = {0.0f, 0.0f};  // e of selection entry r*64+lane (the numerators of pw)
+  float ebelow = 0.0f;
+  // a controlled row not given the serial sum: its token is checked against
+  // the roundings that sum could change (order_settled, draw_settled); with
+  // one finite value the token is that id for every denominator
+  const bool check = (HAS_MASK || ctl_on) && S_ser < 0.0f && nsel > 1;
+  bool unsettled = false;
   bool lazy_order = false;  // the (p desc, id asc) repair left to the draw
   if (stoch && st == XS_ROW_OK && !cfg.big) {
     const bool need_below = !cfg.full && vL != -INFINITY;
@@ -1625,26 +1849,33 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
         const int i = r * 64 + lane;
         const bool in = i < nsel;
         if (in || (i == nsel && need_below)) {
-          const float pe = exact_p(in ? keyf(pk_key(sel[r])) : next_below(vL), cfg, m_s, S, T);
-          if (in) {
-            pw[r] = pe;
-            pk[r] = ((uint64_t)__float_as_uint(pe + 0.0f) << 32) | (uint64_t)(0xFFFFFFFFu - pk_id(sel[r]));
-          } else {
-            pw[r] = pe;  // lane nsel: the boundary value, read below and then cleared
-          }
+          const float e = exact_e(in ? keyf(pk_key(sel[r])) : next_below(vL), cfg, m_s, T);
+          const float pe = __fdiv_rn(e, S);  // exact_p
+          pw[r] = pe;  // (lane nsel: the boundary value, read below and then cleared)
+          ee[r] = e;
+          if (in) pk[r] = ((uint64_t)__float_as_uint(pe + 0.0f) << 32) | (uint64_t)(0xFFFFFFFFu - pk_id(sel[r]));
         }
       }
     }
     if (need_below) {
       if (nsel < 128) {
         pbelow = rdlf(nsel < 64 ? pw[0] : pw[1], nsel & 63);
+        ebelow = rdlf(nsel < 64 ? ee[0] : ee[1], nsel & 63);
       } else {
-        pbelow = exact_p(next_below(vL), cfg, m_s, S, T);
+        ebelow = exact_e(next_below(vL), cfg, m_s, T);
+        pbelow = __fdiv_rn(ebelow, S);
       }
     }
     if (lane == (nsel & 63)) {
-      if (nsel < 64) pw[0] = 0.0f;
-      else if (nsel < 128) pw[1] = 0.0f;
+      if (nsel < 64) pw[0] = ee[0] = 0.0f;
+      else if (nsel < 128) pw[1] = ee[1] = 0.0f;
+    }
+    if (check) {
+      // a run of equal e across the top-k boundary: bounded below by the
+      // row's actual next logit rather than next_below(vL)
+      if (!cfg.full && nsel == kp && nsel > k && at_lane(ee, k - 1) == at_lane(ee, nsel - 1))
+        ebelow = exact_e(below_selection(rr, nsp, nsub, E, vL), cfg, m_s, T);
+      unsettled = !order_settled<2>(ee, nsel, kp, k, cfg.full, ebelow, S, cfg.dthr, want_cands);
     }
     bool bad = false;
     const uint64_t n0 = shfl64(pk[0], (lane + 1) & 63);
@@ -1955,15 +2186,17 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
         return rdlf(i < 64 ? pre[0] : pre[1], i & 63);
       };
       bool zero = false;
-      if (!(cfg.top_p >= 1.0f)) {
+      const bool renorm = !(cfg.top_p >= 1.0f);
+      float sumc = 1.0f;
+      if (renorm) {
         float pre[2];
         prefix(-0.0f, pre, INFINITY);  // the serial sum folds from -0.0 as Rust's f32 Sum does
-        const float sum = at(pre, k - 1);
-        if (!(sum > 0.0f)) {
+        sumc = at(pre, k - 1);
+        if (!(sumc > 0.0f)) {
           zero = true;  // all weights zero: truncate_top_p returns them unchanged
         } else {
-          w[0] = __fdiv_rn(w[0], sum);
-          w[1] = __fdiv_rn(w[1], sum);
+          w[0] = __fdiv_rn(w[0], sumc);
+          w[1] = __fdiv_rn(w[1], sumc);
         }
       }
       if (zero) {
@@ -1972,9 +2205,11 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
         float c[2];
         prefix(0.0f, c, cfg.top_p >= 1.0f ? INFINITY : cfg.top_p);
         int keep = k;
-        if (!(cfg.top_p >= 1.0f)) {
+        bool found = false;
+        if (renorm) {
           const uint64_t b0m = __ballot(lane < k && c[0] >= cfg.top_p);
           const uint64_t b1m = __ballot(64 + lane < k && c[1] >= cfg.top_p);
+          found = (b0m | b1m) != 0ull;
           keep = b0m ? (int)__builtin_ctzll(b0m) + 1 : (b1m ? 64 + (int)__builtin_ctzll(b1m) + 1 : k);
           if (lane >= keep) w[0] = 0.0f;
           if (64 + lane >= keep) w[1] = 0.0f;
@@ -2015,9 +2250,19 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
               tok = (int)y;
             }
           }
+          if (check)
+            unsettled = unsettled || cfg.force ||
+                        !draw_settled<2>(c, tot, x_draw, idx, keep, k, found, renorm, S, cfg.top_p);
         }
       }
     }
+  }
+  if (unsettled) {  // (nothing written) the workgroup sums the serial denominator
+    if (lane == 0) {
+      F.need_ser = 1;
+      F.ser_ms = m_s;
+    }
+    return;
   }
 
   // held_row: the statistics for held_fold, which writes row_lse and the
@@ -2149,6 +2394,7 @@ XS_DEV void finalize_heads(const Args& a, const Cfg& cfg, int row, const uint64_
                            const uint64_t (&h)[NHW], const uint64_t (&E)[EPRE], float S_ser = -1.0f) {
   CtlRow cr{};
   if (HAS_CTL) cr = a.ctl_row[row];
+  if (lane_id() == 0) F.need_ser = 0;
   const bool done = !(HAS_CTL && cr.active) && nsub <= 64 && cfg.kp <= 64 && !cfg.bad && !cfg.big &&
                     fin_fast<HAS_MASK, WANT_LSE>(a, cfg, row, nsub, h, E, rowrec, nsp, rowp, F, S_ser);
   if (!done) fin_general<HAS_MASK, WANT_LSE, HAS_CTL>(a, cfg, row, rowrec, nsp, nsub, rowp, mrow, cr, h, E, F, S_ser);
@@ -2308,12 +2554,10 @@ XS_DEV bool deferred(const Cfg& cfg, const FinLds& F) {
 // there its terms one at a time in f32, as the reference does.  Segments
 // where the exact sum may pass a power of two, or that hold a half-way term,
 // keep their correctly rounded terms in a side buffer for that.
-constexpr int SEG = 256;               // ids per segment
 constexpr uint32_t GSAT = 1u << 23;    // grid units that always carry into the next binade
 constexpr int SER_NB = 64;             // segments per row whose terms are kept
 constexpr int SER_WIN = 1024;          // segment summaries the walk stages at a time
 constexpr int SER_LDS = 32;            // kept segments staged in LDS
-constexpr int SER_QCAP = 128;          // per wave: terms queued for the correctly rounded exp
 constexpr double SER_DELTA = 1.0 / 512;  // margin on the exact prefix for a binade change
 constexpr float LOG2E_LO = 1.925963033500011e-08f;  // log2(e) - LOG2E
 constexpr float LN2F = 0.6931471805599453f;
@@ -2322,11 +2566,15 @@ constexpr float LN2F = 0.6931471805599453f;
 // present (10), every term +0 (11), and 1 + the kept-terms slot (16..)
 constexpr uint32_t SM_TIE0 = 1u << 8, SM_TIE1 = 1u << 9, SM_TWO = 1u << 10, SM_ZERO = 1u << 11;
 
-// A row whose denominator is the serial sum and reaches the caller:
-// stochastic, controlled, top_p >= 1 (the weights are not renormalized).
+// A row that serial_kernel finalizes: stochastic and controlled, and either
+// at top_p >= 1 in a call that observes the denominator (the weights reach
+// the caller unrenormalized), or drawn by the whole-row kernels (whose
+// order of every p follows the denominator).  The other controlled rows are
+// finalized with the exact sum and checked (draw_settled).
 template <bool HAS_MASK, bool HAS_CTL>
 XS_DEV bool serial_row(const Args& a, const Cfg& cfg, int row) {
-  if (cfg.greedy || cfg.bad || !(cfg.top_p >= 1.0f)) return false;
+  if (cfg.greedy || cfg.bad) return false;
+  if (!(((a.serial & 1) && cfg.top_p >= 1.0f) || ((a.serial & 2) && cfg.big))) return false;
   if (HAS_MASK) return true;
   return HAS_CTL && a.ctl_row[row].active != 0;
 }
@@ -2445,6 +2693,29 @@ XS_DEV void seg_terms(const Args& a, const Cfg& cfg, int row, int g, float m_s, 
   for (int e = 0; e < 4; e++) ev[e] = cr_expf((cfg.scale ? x[e] * cfg.inv : x[e]) - m_s, T);
 }
 
+// The queued terms of one wave (qd, qt of the LDS struct L): each correctly
+// rounded, its units and half-way flags added to its segment's summary (LDS
+// atomics).
+template <typename L_T>
+XS_DEV void ser_flush_t(L_T& L, int wave, int n, const double* T) {
+  const int lane = lane_id();
+  wave_lds_sync();  // the queue and the segments' binades are written
+  for (int i0 = 0; i0 < n; i0 += 64) {
+    const int i = i0 + lane;
+    if (i < n) {
+      const int t = L.qt[wave][i];
+      const float e = cr_expf(L.qd[wave][i], T);
+      const uint32_t mt = L.meta[t];
+      const int FB = (int)(mt & 0xFFu);
+      bool t0, t1 = false;
+      atomicAdd(&L.R[t][0], grid_units(__float_as_uint(e), FB, t0));
+      if (mt & SM_TWO) atomicAdd(&L.R[t][1], grid_units(__float_as_uint(e), FB + 1, t1));
+      if (t0 || t1) atomicOr(&L.meta[t], (t0 ? SM_TIE0 : 0u) | (t1 ? SM_TIE1 : 0u));
+    }
+  }
+  wave_lds_sync();
+}
+
 // One segment added to the running sum's bits sb, its SEG terms at evp (LDS,
 // in id order): grid units up to the first term that carries into the next
 // binade or lies half-way, that term by the f32 add (the reference's own
@@ -2500,10 +2771,11 @@ XS_DEV uint32_t ser_segment(uint32_t sb, const float* evp) {
 // in sum), from the running sum's bits sb.  One wave; lane i holds the
 // summary of the i-th segment of each group of 64.  A segment added term by
 // term has its terms in LDS (evl[0 .. nbl)), or copied from the side buffer,
-// or recounted from the logits, into evl[SER_LDS].
+// or recounted from the logits, into scr (one segment of LDS).
 template <bool HAS_MASK, bool HAS_CTL>
 XS_DEV uint32_t ser_walk(const Args& a, const Cfg& cfg, int row, uint32_t sb, const uint64_t (*sum)[2], int w0,
-                         int wn, float (*evl)[SEG], int nbl, const uint64_t* skeep, float m_s, const double* T) {
+                         int wn, float (*evl)[SEG], int nbl, const uint64_t* skeep, float m_s, const double* T,
+                         float* scr) {
   const int lane = lane_id();
 #pragma unroll 1
   for (int b0 = 0; b0 < wn; b0 += 64) {
@@ -2547,9 +2819,9 @@ XS_DEV uint32_t ser_walk(const Args& a, const Cfg& cfg, int row, uint32_t sb, co
         } else {
           seg_terms<HAS_MASK, HAS_CTL>(a, cfg, row, w0 + b0 + f, m_s, T, ev);
         }
-        reinterpret_cast<float4*>(evl[SER_LDS])[lane] = make_float4(ev[0], ev[1], ev[2], ev[3]);
+        reinterpret_cast<float4*>(scr)[lane] = make_float4(ev[0], ev[1], ev[2], ev[3]);
         wave_lds_sync();
-        evp = evl[SER_LDS];
+        evp = scr;
       }
       sb = ser_segment(sb, evp);
       wave_lds_sync();  // (the scratch row is rewritten by the next recount)
@@ -2559,6 +2831,200 @@ XS_DEV uint32_t ser_walk(const Args& a, const Cfg& cfg, int row, uint32_t sb, co
   return sb;
 }
 
+
+// ---------------------------------------------------------------------------
+// The serial denominator of one row, summed by the wave that finalizes it:
+// the fallback for a controlled row whose token the exact sum does not settle
+// (order_settled, draw_settled), rare by construction.  Chunk after chunk it
+// does serial_kernel's per-chunk work -- each term's exp argument, the exact
+// sums and prefixes of the chunk's 64 segments, their grid units at the
+// binades those prefixes lie in, the half-way flags -- then walks the
+// chunk's segments onto the running serial sum (ser_walk; a segment its
+// summary does not settle is recounted from the logits).  One wave does it
+// all, so the workgroup's other waves need not stay for the finalizer's
+// verdict; the logits are read once per phase, four segments at a time.
+template <bool HAS_MASK, bool HAS_CTL>
+XS_DEV float ser_local(const Args& a, const Cfg& cfg, int row, float m_s, SerLocal& L) {
+  constexpr int NB = 4;  // segments loaded at a time
+  constexpr int NSEG = SPC * NWAVE;  // segments per chunk
+  const int lane = lane_id();
+  const int enc = (int)a.enc, nc = a.n_chunks;
+  const v4f* rp4 = reinterpret_cast<const v4f*>(a.logits + (int64_t)row * a.ld);
+  const uint32_t* mrow = HAS_MASK ? a.allowed + (int64_t)row * a.allowed_ld : nullptr;
+  const int fmax = (enc - 1) >> 2;
+  CtlRow cr{};
+  if (HAS_CTL) cr = a.ctl_row[row];
+  const bool ctl_on = HAS_CTL && cr.active;
+  const uint64_t* pl = ctl_on ? a.patch + (int64_t)row * a.ctl_cap : nullptr;
+  L.expt[lane] = (&kExpT[0][0])[lane];
+  double X = 0.0;   // exact sum of the chunks walked so far
+  uint32_t sb = 0;  // the serial sum's bits after them, from +0
+  wave_lds_sync();
+#pragma unroll 1
+  for (int chunk = 0; chunk < nc; chunk++) {
+    const int s0 = chunk * SPC;
+    const int nseg = min(SPC, a.nslots - s0) * NWAVE;  // segment t: slot t / NWAVE, quarter t % NWAVE
+    const int pc0 = ctl_on ? a.ctl_chunk[(int64_t)row * (nc + 1) + chunk] : 0;
+    const int phi = ctl_on ? a.ctl_chunk[(int64_t)row * (nc + 1) + chunk + 1] : 0;
+    v4f q[NB];
+    uint32_t mw[NB];
+    auto load = [&](int tb) __attribute__((always_inline)) {
+#pragma unroll
+      for (int u = 0; u < NB; u++) {
+        const int t = tb + u;  // (clamped: segments past nseg are not used)
+        const int f = min((s0 + t / NWAVE) * BLOCK + (t % NWAVE) * 64 + lane, fmax);
+        q[u] = rp4[f];
+        if (HAS_MASK) mw[u] = mrow[f >> 3];
+      }
+    };
+    // the exp arguments d = v * inv - max of segment t's float4 on this lane,
+    // the values masked and controlled as the streaming pass saw them (each
+    // slot's patches scanned from the slot's first, once per quarter)
+    int pc = pc0, pc_slot = pc0;
+    auto args = [&](int t, int u, float (&dv)[4]) __attribute__((always_inline)) {
+      const int j = t / NWAVE, pos = (t % NWAVE) * 64 + lane;
+      float x[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
+      if (HAS_MASK) {
+        const uint32_t bits = mw[u] >> ((((s0 + j) * BLOCK + pos) & 7) * 4);
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+          if (!((bits >> e) & 1u)) x[e] = -INFINITY;
+      }
+      if ((s0 + j + 1) * SLOT > enc) {
+        const int id0 = (s0 + j) * SLOT + 4 * pos;
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+          if (id0 + e >= enc) x[e] = -INFINITY;
+      }
+      if (ctl_on) {
+        if (t % NWAVE == 0) pc_slot = pc;
+        pc = pc_slot;
+        ctl_slot(x, (s0 + j) * SLOT, pos, pl, pc, phi, cr.pull_id, cr.pull_val, cr.force_id, cr.force_val);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; e++) dv[e] = (cfg.scale ? x[e] * cfg.inv : x[e]) - m_s;
+    };
+    // 1. each segment's exact sum (short exp); a segment whose terms all lie
+    //    below -104 adds +0 at any grid
+#pragma unroll 1
+    for (int tb = 0; tb < NSEG; tb += NB) {
+      if (tb < nseg) load(tb);
+#pragma unroll
+      for (int u = 0; u < NB; u++) {
+        const int t = tb + u;
+        double ssum = 0.0;
+        bool any = false;
+        if (t < nseg) {
+          float dv[4], tt = 0.0f;
+          args(t, u, dv);
+#pragma unroll
+          for (int e = 0; e < 4; e++) tt += fast_expf(dv[e]);
+          ssum = wave_sumd((double)tt);
+          any = __ballot(dv[0] >= -104.0f || dv[1] >= -104.0f || dv[2] >= -104.0f || dv[3] >= -104.0f) != 0;
+        }
+        if (lane == 0) {
+          L.segsum[t] = ssum;
+          L.meta[t] = any ? 0u : SM_ZERO;
+          L.R[t][0] = 0u;
+          L.R[t][1] = 0u;
+        }
+      }
+    }
+    wave_lds_sync();
+    // 2. the exact sum before each segment (lane t), in row order
+    double ctot;
+    {
+      double inc = L.segsum[lane];
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const double t = __shfl_up(inc, d);
+        if (lane >= d) inc += t;
+      }
+      const double ex = __shfl_up(inc, 1);
+      L.segpre[lane] = X + (lane == 0 ? 0.0 : ex);
+      ctot = __shfl(inc, 63);
+    }
+    wave_lds_sync();
+    // 3. each segment's grid units at the binade its prefix lies in (and the
+    //    next, near a power of two), from the short exp where its error bound
+    //    settles them, else queued for the correctly rounded one
+    pc = pc_slot = pc0;
+    int qn = 0;
+#pragma unroll 1
+    for (int tb = 0; tb < NSEG; tb += NB) {
+      if (tb < nseg) load(tb);
+#pragma unroll
+      for (int u = 0; u < NB; u++) {
+        const int t = tb + u;
+        if (t < nseg) {
+          const double X0 = L.segpre[t];
+          const int FB = f32_field((float)(X0 * (1.0 - SER_DELTA)));
+          const bool two = f32_field((float)(X0 * (1.0 + SER_DELTA))) != FB;
+          if (lane == 0) L.meta[t] |= (uint32_t)FB | (two ? SM_TWO : 0u);
+          float dv[4];
+          args(t, u, dv);
+          uint32_t r0 = 0, r1 = 0;
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const float ef = fast_expf(dv[e]);
+            uint32_t u0, u1 = 0;
+            bool settled = fast_units(ef, FB, u0);
+            if (two) settled = fast_units(ef, FB + 1, u1) && settled;
+            const bool amb = !(dv[e] < -104.0f) && (!settled || dv[e] < -87.0f);
+            if (!amb) {
+              r0 += u0;
+              r1 += u1;
+            }
+            const uint64_t b = __ballot(amb);
+            if (b) {
+              if (qn + 64 > SER_QCAP) {
+                ser_flush_t(L, 0, qn, L.expt);
+                qn = 0;
+              }
+              const int pos = qn + lanes_below(b);
+              if (amb) {
+                L.qd[0][pos] = dv[e];
+                L.qt[0][pos] = (uint8_t)t;
+              }
+              qn += __popcll(b);
+            }
+          }
+          const uint32_t s0u = wave_sum_u32(r0), s1u = wave_sum_u32(r1);
+          if (lane == 0) {
+            atomicAdd(&L.R[t][0], s0u);
+            atomicAdd(&L.R[t][1], s1u);
+          }
+        }
+      }
+    }
+    ser_flush_t(L, 0, qn, L.expt);
+    // 4. the chunk's segments onto the running sum, in order
+    L.sum[lane][0] = (uint64_t)L.R[lane][0] | ((uint64_t)L.R[lane][1] << 32);
+    L.sum[lane][1] = (uint64_t)L.meta[lane] << 32;
+    wave_lds_sync();
+    sb = ser_walk<HAS_MASK, HAS_CTL>(a, cfg, row, sb, L.sum, s0 * NWAVE, nseg, nullptr, 0, nullptr, m_s, L.expt,
+                                     L.scr);
+    X += ctot;
+    wave_lds_sync();
+  }
+  return __uint_as_float(sb);
+}
+
+// After the finalizing wave's finalize_row: when it left a controlled row
+// unsettled (F.need_ser), the wave sums the row's serial denominator
+// (ser_local) and finalizes the row again with it, which settles it by
+// construction.  Rows sent here are counted.
+template <bool HAS_MASK, bool WANT_LSE, bool HAS_CTL>
+XS_DEV void ser_fallback(const Args& a, const Cfg& cfg, int row, const uint64_t* rowrec, int nsp, int nsub,
+                         const float* rowp, const uint32_t* mrow, TailLds& Tl) {
+  wave_lds_sync();  // lane 0 wrote the verdict
+  if (!Tl.fin.need_ser) return;
+  const float m_s = Tl.fin.ser_ms;
+  wave_lds_sync();  // read before ser_local reuses the memory
+  const float S_ser = ser_local<HAS_MASK, HAS_CTL>(a, cfg, row, m_s, Tl.ser);
+  if (lane_id() == 0 && a.ser_count) atomicAdd(a.ser_count, 1u);
+  finalize_row<HAS_MASK, WANT_LSE, HAS_CTL>(a, cfg, row, rowrec, nsp, nsub, rowp, mrow, Tl.fin, S_ser);
+}
 
 // ---------------------------------------------------------------------------
 // The kernel.  Grid: rows x n_chunks workgroups of BLOCK lanes; chunk c of a
@@ -2599,7 +3065,7 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
   }
   // The row's parameters are read only now, so that round trip overlaps the
   // loads instead of delaying them.
-  const Cfg cfg = a.greedy_all ? greedy_cfg() : make_cfg(a.params[row], a.enc, a.n_top, a.k_max);
+  const Cfg cfg = a.greedy_all ? greedy_cfg() : make_cfg(a.params[row], a.enc, a.n_top, a.k_max, a.ser_force);
   const bool stoch = !cfg.greedy && !cfg.bad;
   const int kp = cfg.kp;
   // Sparse controls: the chunk's patches (final values written by
@@ -3049,9 +3515,12 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
   // The first wave finalizes the row; held_row outputs then get the reference's
   // serial fold (held_fold); a verify block's rows then walk accept_drafts
   // (verify_walk), except a row with more candidates than the selection
-  // holds: the whole-row kernels draw it and walk its block.
+  // holds: the whole-row kernels draw it and walk its block.  On a masked or
+  // controlled launch a row whose token the exact sum does not settle is
+  // summed serially by the same wave and finalized again (ser_fallback).
   if (wave != 0) return;
   finalize_row<HAS_MASK, WANT_LSE, HAS_CTL>(a, cfg, row, rowrec, nsp, nc * NWAVE, rowp, mrow, Tl.fin);
+  if (HAS_MASK || HAS_CTL) ser_fallback<HAS_MASK, WANT_LSE, HAS_CTL>(a, cfg, row, rowrec, nsp, nc * NWAVE, rowp, mrow, Tl);
   if (held) held_fold<1>(a, row, rowp, rowrec, nsp, nc * NWAVE, Tl.fin);
   if (a.span > 0 && !deferred(cfg, Tl.fin)) verify_walk(a, row);
 }
@@ -3075,13 +3544,14 @@ __global__ __launch_bounds__(BLOCK) void finalize_kernel(Args a) {
   // the row's headers first: their round trip overlaps the row's parameters
   uint64_t h[NHW], E[EPRE];
   load_heads<WANT_LSE>(rowrec, nsp, nc * NWAVE, h, E);
-  const Cfg cfg = a.greedy_all ? greedy_cfg() : make_cfg(a.params[row], a.enc, a.n_top, a.k_max);
+  const Cfg cfg = a.greedy_all ? greedy_cfg() : make_cfg(a.params[row], a.enc, a.n_top, a.k_max, a.ser_force);
   if (threadIdx.x == 0) st_agent(&a.row_ticket[row * TSTRIDE + 1], 0);  // held_row's running max key
   if (a.serial && serial_row<HAS_MASK, HAS_CTL>(a, cfg, row)) return;  // serial_kernel finalizes it
   const float* rowp = a.logits + (int64_t)row * a.ld;
   const uint32_t* mrow = HAS_MASK ? a.allowed + (int64_t)row * a.allowed_ld : nullptr;
   const bool held = WANT_LSE && (a.row_lse != nullptr || a.n_top > 0);
   finalize_heads<HAS_MASK, WANT_LSE, HAS_CTL>(a, cfg, row, rowrec, nsp, nc * NWAVE, rowp, mrow, Tl.fin, h, E);
+  if (HAS_MASK || HAS_CTL) ser_fallback<HAS_MASK, WANT_LSE, HAS_CTL>(a, cfg, row, rowrec, nsp, nc * NWAVE, rowp, mrow, Tl);
   if (held) held_fold<1>(a, row, rowp, rowrec, nsp, nc * NWAVE, Tl.fin);
   if (a.span > 0 && !deferred(cfg, Tl.fin)) verify_walk(a, row);
 }
@@ -3124,22 +3594,7 @@ union SerTail {
 // fast units are added the same way).  Out of line: the pass calls it from
 // many places, and seldom.
 __device__ __attribute__((noinline)) void ser_flush(SerLds& L, int wave, int n, const double* T) {
-  const int lane = lane_id();
-  wave_lds_sync();  // the queue and the segments' binades are written
-  for (int i0 = 0; i0 < n; i0 += 64) {
-    const int i = i0 + lane;
-    if (i < n) {
-      const int t = L.qt[wave][i];
-      const float e = cr_expf(L.qd[wave][i], T);
-      const uint32_t mt = L.meta[t];
-      const int FB = (int)(mt & 0xFFu);
-      bool t0, t1 = false;
-      atomicAdd(&L.R[t][0], grid_units(__float_as_uint(e), FB, t0));
-      if (mt & SM_TWO) atomicAdd(&L.R[t][1], grid_units(__float_as_uint(e), FB + 1, t1));
-      if (t0 || t1) atomicOr(&L.meta[t], (t0 ? SM_TIE0 : 0u) | (t1 ? SM_TIE1 : 0u));
-    }
-  }
-  wave_lds_sync();
+  ser_flush_t(L, wave, n, T);
 }
 
 // Four terms correctly rounded, out of line (only kept segments need them).
@@ -3155,7 +3610,7 @@ __global__ __launch_bounds__(BLOCK) void serial_kernel(Args a) {
   const int nc = a.n_chunks;
   const int row = blockIdx.x / nc;
   const int chunk = blockIdx.x - row * nc;
-  const Cfg cfg = make_cfg(a.params[row], a.enc, a.n_top, a.k_max);
+  const Cfg cfg = make_cfg(a.params[row], a.enc, a.n_top, a.k_max, a.ser_force);
   if (!serial_row<HAS_MASK, HAS_CTL>(a, cfg, row)) return;
   const int enc = (int)a.enc;
   const int s0 = chunk * SPC;
@@ -3416,7 +3871,9 @@ __global__ __launch_bounds__(BLOCK) void serial_kernel(Args a) {
       const int wn = min(SER_WIN, nseg - w0);
       for (int i = tid; i < 2 * wn; i += BLOCK) (&St.w.sum[0][0])[i] = ld_agent(&ssum[2 * (int64_t)w0 + i]);
       __syncthreads();
-      if (wave == 0) sb = ser_walk<HAS_MASK, HAS_CTL>(a, cfg, row, sb, St.w.sum, w0, wn, St.w.ev, nbl, skeep, m_s, Ls.expt);
+      if (wave == 0)
+        sb = ser_walk<HAS_MASK, HAS_CTL>(a, cfg, row, sb, St.w.sum, w0, wn, St.w.ev, nbl, skeep, m_s, Ls.expt,
+                                         St.w.ev[SER_LDS]);
       __syncthreads();
     }
     S_ser = __uint_as_float(sb);
@@ -3759,7 +4216,7 @@ XS_DEV void count_digit(uint32_t* cnt, uint32_t d, bool valid) {
 // The row's whole-row state for the kernels below: null when the call does not
 // draw the row on this path.
 XS_DEV const BigRow* big_live(const Args& a, int row, Cfg& cfg) {
-  cfg = a.greedy_all ? greedy_cfg() : make_cfg(a.params[row], a.enc, a.n_top, a.k_max);
+  cfg = a.greedy_all ? greedy_cfg() : make_cfg(a.params[row], a.enc, a.n_top, a.k_max, a.ser_force);
   if (!cfg.big || cfg.bad) return nullptr;  // (then big_state[row] is not this call's)
   const BigRow* br = a.big_state + row;
   return br->state ? br : nullptr;
@@ -4438,6 +4895,8 @@ struct xs_context {
   int32_t big_tiles_max;
   uint64_t* ser_sum;    // [max_rows, max_chunks * SPC * NWAVE, 2] serial_kernel's segment summaries
   uint64_t* ser_e;      // [max_rows, SER_NB, SEG / 2] its kept terms
+  uint32_t* ser_count;  // [1] rows the finalizers summed serially themselves (ser_local), or null
+  int32_t ser_force;    // test hook: every checked row takes that fallback
 };
 
 namespace {
@@ -4490,7 +4949,8 @@ void launch2(xs_context* ctx, xs::Args& a, int64_t rows, dim3 g1, const int32_t*
 
 // order: null, or a host permutation of the rows (checked by the caller,
 // rows <= XS_ORDER_MAX).  serial: the call can observe the serial denominator
-// of its controlled rows at top_p >= 1 (serial_kernel then finalizes them).
+// of its controlled rows at top_p >= 1 (serial_kernel then finalizes them);
+// the controlled rows of top_k >= 128 always take it.
 int launch(xs_context* ctx, xs::Args& a, int64_t rows, int span, bool mask, bool lse, bool serial,
            const int32_t* order = nullptr) {
   const bool ctl = a.controls != nullptr;
@@ -4516,7 +4976,10 @@ int launch(xs_context* ctx, xs::Args& a, int64_t rows, int span, bool mask, bool
   a.big_nblk = (int32_t)(a.enc > xs::CHEAD ? (a.enc - xs::CHEAD + xs::CBLK - 1) / xs::CBLK : 0);
   a.big_cut = (a.big && !a.cand_id && !a.cand_w && a.enc <= (1 << 20)) ? 1 : 0;
   if (a.big && rows * (int64_t)a.big_tiles > 0x7FFFFFFF) return XS_ERR_CAPACITY;  // the whole-row grids
-  a.serial = (serial && (mask || ctl)) ? 1 : 0;
+  const bool big_rows = a.big && !a.greedy_all && a.k_max > XS_K_MAX;
+  a.serial = (mask || ctl) ? ((serial ? 1 : 0) | (big_rows ? 2 : 0)) : 0;
+  a.ser_count = ctx->ser_count;
+  a.ser_force = ctx->ser_force;
   a.ser_sum = ctx->ser_sum;
   a.ser_e = ctx->ser_e;
   a.ser_ld = (int64_t)ctx->max_chunks * xs::SPC * xs::NWAVE;
@@ -4575,6 +5038,8 @@ int xs_create_ex(int device, int64_t max_rows, int64_t vocab, int32_t k_max, int
   const int64_t nseg = (int64_t)mc * xs::SPC * xs::NWAVE;
   ok = ok && hipMalloc((void**)&c->ser_sum, max_rows * nseg * 2 * sizeof(uint64_t)) == hipSuccess;
   ok = ok && hipMalloc((void**)&c->ser_e, max_rows * xs::SER_NB * (xs::SEG / 2) * sizeof(uint64_t)) == hipSuccess;
+  ok = ok && hipMalloc((void**)&c->ser_count, sizeof(uint32_t)) == hipSuccess;
+  ok = ok && hipMemset(c->ser_count, 0, sizeof(uint32_t)) == hipSuccess;
   if (k_max > XS_K_MAX) {  // top_k past the streaming selection: the whole-row path's buffers
     ok = ok && hipMalloc((void**)&c->big, (size_t)max_rows * 2 * vocab * sizeof(uint64_t)) == hipSuccess;
     ok = ok && hipMalloc((void**)&c->big_state, (size_t)max_rows * sizeof(xs::BigRow)) == hipSuccess;
@@ -4610,6 +5075,7 @@ int xs_destroy(xs_context* c) {
   if (c->big_ticket) (void)hipFree(c->big_ticket);
   (void)hipFree(c->ser_sum);
   (void)hipFree(c->ser_e);
+  if (c->ser_count) (void)hipFree(c->ser_count);
   free(c);
   return XS_OK;
 }
@@ -4680,10 +5146,10 @@ int sample_impl(xs_context* ctx, const xs_sample_args* in, bool clear_tickets) {
     hipLaunchKernelGGL(xs::zero_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, ctx->stream,
                        ctx->row_ticket, n);
   }
-  // the serial denominator shows in the candidate list and weights and in
-  // soft_sum; a call that takes only tokens draws with the exact sum, whose
-  // token differs from the serial one's only where u falls within rounding
-  // of a cumulative-weight boundary
+  // the serial denominator shows in the candidate weights and in soft_sum of
+  // rows at top_p >= 1; every other controlled row draws with the exact sum,
+  // and a row whose token that sum does not settle is summed serially by its
+  // finalizer (draw_settled, ser_local)
   const bool serial = in->cand_id || in->cand_w || in->soft_sum;
   return launch(ctx, a, in->rows, 1, in->allowed != nullptr, lse, serial, in->row_order);
 }
@@ -4791,7 +5257,8 @@ int xs_verify(xs_context* ctx, const xs_verify_args* in) {
   a.n_chunks = chunks_for(in->enc);
   a.nslots = (int32_t)slots_for(in->enc);
   a.rec = ctx->rec;
-  return launch(ctx, a, rows, (int)in->span, in->allowed != nullptr, false, true);  // tokens are all it returns
+  // tokens are all it returns: the exact sum, checked (draw_settled)
+  return launch(ctx, a, rows, (int)in->span, in->allowed != nullptr, false, false);
 }
 
 int xs_argmax_probs(xs_context* ctx, const xs_argmax_args* in) {
@@ -4813,6 +5280,17 @@ int xs_argmax_probs(xs_context* ctx, const xs_argmax_args* in) {
   a.nslots = (int32_t)slots_for(in->width);
   a.rec = ctx->rec;
   return launch(ctx, a, in->rows, 1, false, true, false);
+}
+
+int xs_test_serial_fallback(xs_context* c, int32_t force, uint32_t* count) {
+  if (!c) return XS_ERR_ARG;
+  if (hipSetDevice(c->device) != hipSuccess) return XS_ERR_HIP;
+  if (count) {
+    if ((c->stream ? hipStreamSynchronize(c->stream) : hipDeviceSynchronize()) != hipSuccess) return XS_ERR_HIP;
+    if (hipMemcpy(count, c->ser_count, sizeof(uint32_t), hipMemcpyDeviceToHost) != hipSuccess) return XS_ERR_HIP;
+  }
+  c->ser_force = force != 0 ? 1 : 0;
+  return XS_OK;
 }
 
 int xs_test_exp(const float* x, float* y, int64_t n, void* s) {

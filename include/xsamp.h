@@ -58,7 +58,9 @@ extern "C" {
  *                      control list past the context's ctl_max (XS_CTL_MAX by
  *                      default, xs_create_ex) entries (no reference
  *                      counterpart: the reference has no such limits)
- *   XS_ROW_INTERNAL    reserved; this build never reports it               */
+ *   XS_ROW_INTERNAL    reserved; this build never reports it
+ *   XS_ROW_ID_OOR      a scored id (score_ids) outside the encodable ids
+ *                      (last_logprobs_for, generate.rs:1874-1879)           */
 #define XS_ROW_OK 0
 #define XS_ROW_NAN 1
 #define XS_ROW_NO_FINITE 2
@@ -68,6 +70,7 @@ extern "C" {
 #define XS_ROW_NARROW 6
 #define XS_ROW_BAD_PARAM 7
 #define XS_ROW_INTERNAL 8
+#define XS_ROW_ID_OOR 9
 
 /* Largest top_k the streaming selection serves (it keeps top_k + 1 entries).
  * A context created with k_max above it serves every top_k up to k_max --
@@ -154,13 +157,13 @@ typedef struct {
  * (softmax_in_place, sampler.rs:301-305), other rows through candle's softmax.
  * Where that sum reaches an output -- a stochastic controlled row at
  * top_p >= 1, whose weights are p = e / sum unrenormalized, in a call that
- * asks for cand_id, cand_w or soft_sum -- it is reproduced bit for bit (a
- * second kernel per call).  Everywhere else the denominator is the exact sum of
- * the same correctly rounded terms, within 2e-6 of either reference sum; it
- * cancels from renormalized weights, and a token drawn with it differs from
- * the serial sum's only where the uniform falls within rounding of a
- * cumulative-weight boundary.  xs_verify, whose outputs are tokens, always
- * reproduces it on its controlled rows at top_p >= 1. */
+ * asks for cand_id, cand_w or soft_sum, and every controlled row of top_k >=
+ * 128 -- it is reproduced bit for bit (a second kernel per call).  Elsewhere
+ * the denominator is the exact sum of the same correctly rounded terms,
+ * within 2e-6 of either reference sum, and on controlled rows the finalizer
+ * proves that the serial sum would draw the same token (and candidate ids),
+ * summing a row it cannot prove serially itself: the token of every
+ * controlled row is the reference's on every call shape, xs_verify's too. */
 typedef struct {
   const float* logits;   /* [rows, ld] row-major f32; 16-byte aligned, ld % 4 == 0 */
   int64_t rows;
@@ -215,7 +218,32 @@ typedef struct {
    * options are per row: a caller batching rows of several top_k passes the
    * largest min(top_k, enc) among them. */
   int32_t k_max;
+  /* Scoring reads of the held row (generate.rs:1871-1899, batch.rs:1504-1521,
+   * :1628-1669), normalized by the same f64 lse as row_lse; the held_row
+   * outputs' rules apply (no allow-mask, no controls), and each may be asked
+   * for alone (lse is then computed without being written).  Not available
+   * through xs_sample_noalloc (XS_ERR_ARG). */
+  double* top_logprob64;          /* [rows, top_ld] the n_top log-probs in f64, or NULL */
+  const int32_t* score_ids;       /* [rows, score_ld] ids to score, or NULL (last_logprobs_for) */
+  int32_t n_score;                /* ids per row, 0..XS_SCORE_MAX */
+  int64_t score_ld;
+  double* score_logprob;          /* [rows, score_ld] f64(v[id]) - lse; an id outside
+                                     [0, enc) makes the row XS_ROW_ID_OOR (token -1)
+                                     and its entry NaN */
+  /* Per-class probability masses: class c of row r holds id t when bit t%32
+   * of word t/32 of class_masks[(r * n_class + c) * class_ld ..] is set (the
+   * allow-mask layout); class_mass[r * n_class + c] = sum over those ids of
+   * exp(f64(v) - lse), the sums escape_mass forms from last_probs. */
+  const uint32_t* class_masks;    /* [rows, n_class, class_ld] or NULL */
+  int32_t n_class;                /* 0..XS_CLASS_MAX */
+  int64_t class_ld;               /* words per class mask, >= ceil(enc / 32) */
+  double* class_mass;             /* [rows, n_class] */
+  double* probs;                  /* [rows, probs_ld] exp(f64(v) - lse) of ids 0..enc-1
+                                     (last_probs), or NULL */
+  int64_t probs_ld;
 } xs_sample_args;
+#define XS_SCORE_MAX 4096
+#define XS_CLASS_MAX 8
 #define XS_ORDER_MAX 1024
 
 int xs_sample(xs_context* ctx, const xs_sample_args* args);

@@ -20,10 +20,12 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("XS_ORACLE_LIB") or os.path.join(HERE, "_build", "libxs_oracle.so")
 
 OK, NAN, NO_FINITE, MASK_SHORT, FORCE_OOR, ZERO_WEIGHT, NARROW = range(7)
+ID_OOR = 9
 SUM_SEQ_F32, SUM_F64, SUM_GIVEN = 0, 1, 2
 
 _f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
 _f64p = np.ctypeslib.ndpointer(np.float64, flags="C_CONTIGUOUS")
+_i64p = np.ctypeslib.ndpointer(np.int64, flags="C_CONTIGUOUS")
 _u32p = np.ctypeslib.ndpointer(np.uint32, flags="C_CONTIGUOUS")
 
 
@@ -105,6 +107,12 @@ def lib():
         L.xo_held_row.restype = C.c_int32
         L.xo_held_row.argtypes = [_f32p, C.c_int64, C.c_int64, C.POINTER(C.c_float),
                                   C.POINTER(C.c_double)]
+        L.xo_last_logprobs_for.restype = C.c_int32
+        L.xo_last_logprobs_for.argtypes = [_f32p, C.c_int64, C.c_int64, _i64p, C.c_int64, _f64p]
+        L.xo_last_probs.restype = C.c_int32
+        L.xo_last_probs.argtypes = [_f32p, C.c_int64, C.c_int64, _f64p]
+        L.xo_class_masses.restype = None
+        L.xo_class_masses.argtypes = [_f64p, C.c_int64, _u32p, C.c_int64, C.c_int64, _f64p]
         L.xo_det_logits.restype = None
         L.xo_det_logits.argtypes = [C.c_int64, C.c_uint64, C.c_float, _f32p]
         _lib = L
@@ -319,6 +327,32 @@ def held_row(row, enc: int):
     mx, lse = C.c_float(0), C.c_double(0)
     st = lib().xo_held_row(r, r.size, enc, C.byref(mx), C.byref(lse))
     return st, mx.value, lse.value
+
+
+def last_logprobs_for(row, enc: int, ids):
+    """(status, f64 log-probs of ids): generate.rs:1871-1883."""
+    r = f32(row)
+    i = np.ascontiguousarray(np.asarray(ids, np.int64)) if len(ids) else np.zeros(1, np.int64)
+    out = np.zeros(max(len(ids), 1), np.float64)
+    st = lib().xo_last_logprobs_for(r, r.size, enc, i, len(ids), out)
+    return st, out[:len(ids)]
+
+
+def last_probs(row, enc: int):
+    """(status, f64 probabilities of ids 0..enc-1): generate.rs:1893-1899."""
+    r = f32(row)
+    out = np.zeros(max(enc, 1), np.float64)
+    st = lib().xo_last_probs(r, r.size, enc, out)
+    return st, out[:enc]
+
+
+def class_masses(probs, masks) -> np.ndarray:
+    """escape_mass's per-class sums (batch.rs:1638-1662): masks [n_class, words] u32."""
+    p = np.ascontiguousarray(np.asarray(probs, np.float64))
+    m = np.ascontiguousarray(np.asarray(masks, np.uint32))
+    out = np.zeros(max(m.shape[0], 1), np.float64)
+    lib().xo_class_masses(p, p.size, m, m.shape[0], m.shape[1], out)
+    return out[:m.shape[0]]
 
 
 def det_logits(n: int, seed: int, scale: float) -> np.ndarray:

@@ -583,6 +583,46 @@ int32_t xo_held_row(const float* row, int64_t width, int64_t enc, float* max_out
   return XO_OK;
 }
 
+/* last_logprobs_for -- generate.rs:1871-1883: held_row's (values, lse), then
+ * f64(v[id]) - lse for every id; an id outside [0, enc) fails the call. */
+int32_t xo_last_logprobs_for(const float* row, int64_t width, int64_t enc, const int64_t* ids,
+                             int64_t n, double* out) {
+  float max;
+  double lse;
+  const int32_t st = xo_held_row(row, width, enc, &max, &lse);
+  if (st != XO_OK) return st;
+  for (int64_t i = 0; i < n; i++) {
+    if (ids[i] < 0 || ids[i] >= enc) return XO_ID_OOR;
+    out[i] = (double)row[ids[i]] - lse;
+  }
+  return XO_OK;
+}
+
+/* last_probs -- generate.rs:1893-1899: exp(f64(v) - lse) for every encodable
+ * id, normalized as last_logprobs_for is. */
+int32_t xo_last_probs(const float* row, int64_t width, int64_t enc, double* out) {
+  float max;
+  double lse;
+  const int32_t st = xo_held_row(row, width, enc, &max, &lse);
+  if (st != XO_OK) return st;
+  for (int64_t i = 0; i < enc; i++) out[i] = exp((double)row[i] - lse);
+  return XO_OK;
+}
+
+/* escape_mass's class sums -- batch.rs:1638-1662: the probabilities of the ids
+ * a class holds, added one after another in id order (inside += p).  Class c
+ * holds id t when bit t%32 of word t/32 of masks[c * mask_ld ..] is set. */
+void xo_class_masses(const double* probs, int64_t enc, const uint32_t* masks, int64_t n_class,
+                     int64_t mask_ld, double* out) {
+  for (int64_t c = 0; c < n_class; c++) {
+    const uint32_t* m = masks + c * mask_ld;
+    double s = 0.0;
+    for (int64_t t = 0; t < enc; t++)
+      if ((m[t >> 5] >> (t & 31)) & 1u) s += probs[t];
+    out[c] = s;
+  }
+}
+
 /* det_logits -- sampler.rs:903-914 (the reference tests' input generator):
  * 64-bit LCG, u = (s >> 40) / 2^24, value (u - 0.5) * 2 * scale. */
 void xo_det_logits(int64_t n, uint64_t seed, float scale, float* out) {

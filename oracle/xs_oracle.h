@@ -32,7 +32,14 @@
  *   xo_accept_drafts     generate.rs:4119-4204 (the nine walks).
  *   xo_draft_argmax_probs generate.rs:5520-5552 (f64 scalar, 1e-5).
  *   xo_keep_confident    generate.rs:5560-5597.
- *   xo_held_row          f64 brute force (decimal) on small rows.
+ *   xo_held_row          f64 brute force (decimal) on small rows; the serial
+ *                        f64 fold pinned by closed forms on dominant rows.
+ *   xo_last_logprobs_for /
+ *   xo_last_probs /
+ *   xo_class_masses      60-digit decimal on small rows (each log-prob, each
+ *                        probability, each class sum), the out-of-range error,
+ *                        and the closed forms p = 1 / D of a dominant id and
+ *                        sum of p = D_exact / D_fold.
  *   xo_select_option /
  *   xo_truncate_nucleus  batch.rs:2970-3016 (greedy on both conditions, a
  *                        top_k of 2 never reaching the third option, a tight
@@ -58,7 +65,8 @@ enum {
   XO_MASK_SHORT = 3,   /* allow-mask narrower than the encodable ids (:437-442) */
   XO_FORCE_OOR = 4,    /* forced id outside the vocabulary (:472-477) */
   XO_ZERO_WEIGHT = 5,  /* WeightedIndex saw no mass (:238-240) */
-  XO_NARROW = 6        /* logit row narrower than the encodable bound (:196-200) */
+  XO_NARROW = 6,       /* logit row narrower than the encodable bound (:196-200) */
+  XO_ID_OOR = 9        /* a scored id outside the encodable ids (generate.rs:1874-1879) */
 };
 
 /* How softmax_in_place forms its denominator. */
@@ -135,6 +143,11 @@ int32_t xo_draft_argmax_probs(const float* logits, int64_t n, int64_t vocab, uin
 int64_t xo_keep_confident(const uint32_t* ids, const float* probs, int64_t n, float p_min);
 int32_t xo_held_row(const float* row, int64_t width, int64_t enc, float* max_out,
                     double* lse_out);
+int32_t xo_last_logprobs_for(const float* row, int64_t width, int64_t enc, const int64_t* ids,
+                             int64_t n, double* out);
+int32_t xo_last_probs(const float* row, int64_t width, int64_t enc, double* out);
+void xo_class_masses(const double* probs, int64_t enc, const uint32_t* masks, int64_t n_class,
+                     int64_t mask_ld, double* out);
 void xo_det_logits(int64_t n, uint64_t seed, float scale, float* out);
 int64_t xo_truncate_nucleus(const double* prob, int64_t n, double top_p);
 int32_t xo_select_option(const double* scores, int64_t n, double temperature, int64_t top_k,

@@ -52,6 +52,9 @@ int main(void) {
   F(xs_sample_args, controls); F(xs_sample_args, ctl_delta);
   F(xs_verify_args, controls); F(xs_verify_args, ctl_delta); F(xs_verify_args, done_after);
   F(xs_sample_args, row_order); F(xs_sample_args, k_max); F(xs_verify_args, k_max);
+  F(xs_sample_args, top_logprob64); F(xs_sample_args, n_score); F(xs_sample_args, score_logprob);
+  F(xs_sample_args, class_masks); F(xs_sample_args, class_ld); F(xs_sample_args, class_mass);
+  F(xs_sample_args, probs); F(xs_sample_args, probs_ld);
   return 0;
 }
 ''')

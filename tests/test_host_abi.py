@@ -71,6 +71,27 @@ def test_sample_argument_checks(host):
     assert host.xs_host_check_sample(C.byref(narrow), C.byref(_sample())) == CAP
 
 
+def test_scoring_argument_checks(host):
+    """The scoring reads (score_ids, class masks, probs): each output needs its
+    input and room for the row's ids, and like the held_row outputs they do
+    not combine with an allow-mask or controls."""
+    chk = lambda **kw: host.xs_host_check_sample(C.byref(LIM), C.byref(_sample(**kw)))
+    assert chk(score_ids=DEV, score_logprob=DEV, n_score=5, score_ld=5) == OK
+    assert chk(score_ids=DEV, n_score=5, score_ld=5) == E            # no output
+    assert chk(score_logprob=DEV, n_score=5, score_ld=5) == E        # no ids
+    assert chk(score_ids=DEV, score_logprob=DEV, n_score=5, score_ld=4) == E
+    assert chk(score_ids=DEV, score_logprob=DEV, n_score=_lib.SCORE_MAX + 1, score_ld=10**5) == E
+    assert chk(score_ids=DEV, score_logprob=DEV, n_score=-1, score_ld=5) == E
+    assert chk(class_masks=DEV, class_mass=DEV, n_class=2, class_ld=7760) == OK
+    assert chk(class_masks=DEV, class_mass=DEV, n_class=2, class_ld=7759) == E
+    assert chk(class_masks=DEV, n_class=2, class_ld=7760) == E
+    assert chk(class_masks=DEV, class_mass=DEV, n_class=_lib.CLASS_MAX + 1, class_ld=7760) == E
+    assert chk(probs=DEV, probs_ld=248_320) == OK and chk(probs=DEV, probs_ld=248_319) == E
+    assert chk(probs=DEV, probs_ld=248_320, allowed=DEV, allowed_words=7760, allowed_ld=7760) == E
+    assert chk(score_ids=DEV, score_logprob=DEV, n_score=1, score_ld=1, controls=DEV) == E
+    assert chk(top_logprob64=DEV, n_top=20, top_ld=19) == E
+
+
 def test_row_order_must_be_a_permutation(host):
     def chk(order, rows=4):
         o = np.ascontiguousarray(np.asarray(order, np.int32))

@@ -440,6 +440,68 @@ def test_held_row_against_decimal(oracle):
     assert oracle.held_row([1.0, 2.0], 3)[0] == STATUS["NARROW"]
 
 
+def test_last_logprobs_and_probs_against_decimal(oracle):
+    """last_logprobs_for and last_probs (generate.rs:1871-1899) on small rows
+    against 60-digit decimal from the same f32 values: each log-prob
+    f64(v) - lse and each probability exp(f64(v) - lse) to 1e-13, the class
+    sums of escape_mass (batch.rs:1638-1662) likewise, and an out-of-range id
+    is the reference's error."""
+    decimal.getcontext().prec = 60
+    D = decimal.Decimal
+    rng = np.random.default_rng(19)
+    for trial in range(4):
+        row = rng.normal(0, 4, 300).astype(np.float32)
+        if trial % 2:
+            row[17] = np.float32(row.max() + 30.0)  # a dominant id
+        enc = 280
+        vals = row[:enc]
+        m = max(vals)
+        denom = sum(D(float(np.float32(v - m))).exp() for v in vals)
+        lse = D(float(m)) + denom.ln()
+        ids = [0, 17, 279, int(np.argmax(vals)), 5]
+        st, lp = oracle.last_logprobs_for(row, enc, ids)
+        assert st == 0
+        for i, got in zip(ids, lp):
+            want = float(D(float(vals[i])) - lse)
+            assert abs(got - want) <= 1e-13 * abs(want) + 1e-13, (trial, i, got, want)
+        st, p = oracle.last_probs(row, enc)
+        assert st == 0 and p.size == enc
+        want_p = [float((D(float(v)) - lse).exp()) for v in vals]
+        np.testing.assert_allclose(p, want_p, rtol=1e-13, atol=0)
+        classes = np.zeros((2, (enc + 31) // 32), np.uint32)
+        allow = rng.random((2, enc)) < 0.3
+        for c in range(2):
+            for t in np.nonzero(allow[c])[0]:
+                classes[c, t >> 5] |= np.uint32(1 << (t & 31))
+        got_c = oracle.class_masses(p, classes)
+        for c in range(2):
+            want_c = float(sum((D(float(vals[t])) - lse).exp() for t in np.nonzero(allow[c])[0]))
+            assert abs(got_c[c] - want_c) <= 1e-13 * want_c, (trial, c)
+    assert oracle.last_logprobs_for(row, 280, [280])[0] == oracle.ID_OOR
+    assert oracle.last_logprobs_for(row, 280, [-1])[0] == oracle.ID_OOR
+    assert oracle.last_probs([1.0, float("nan")], 2)[0] == STATUS["NAN"]
+
+
+def test_last_probs_of_a_dominant_row_follow_the_fold(oracle):
+    """A dominant id followed by n equal terms t >= 2^-53: the fold's
+    denominator is exactly 1 + n rint(2^52 t) 2^-52 (held_row's serial f64
+    sum), so the dominant id's probability is exactly exp(-ln(D)) and the row's
+    probabilities sum to (1 + n t) / D -- not to 1, which an exactly summed
+    denominator would give."""
+    n = 50_000
+    d = -25.0
+    row = np.concatenate([[5.0], np.full(n, 5.0 + d)]).astype(np.float32)
+    dd = float(np.float32(np.float32(5.0 + d) - np.float32(5.0)))
+    t = math.exp(dd)
+    denom = 1.0 + n * round(t * 2.0 ** 52) * 2.0 ** -52
+    st, p = oracle.last_probs(row, row.size)
+    assert st == 0
+    lse = 5.0 + math.log(denom)
+    assert p[0] == math.exp(5.0 - lse)
+    assert abs(math.fsum(p) - (1.0 + n * t) / denom) < 1e-12
+    assert abs(p[1] - t / denom) < 1e-18
+
+
 def test_det_logits_matches_independent_lcg(oracle):
     for n, seed, scale in [(64, 1, 1.0), (100, 4242, 12.0), (33, 90210, 3.0)]:
         np.testing.assert_array_equal(oracle.det_logits(n, seed, scale),

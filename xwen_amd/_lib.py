@@ -16,8 +16,10 @@ HEADER = os.path.join(ROOT, "include", "xsamp.h")
 
 XS_OK, XS_ERR_ARG, XS_ERR_HIP, XS_ERR_CAPACITY = 0, -1, -2, -3
 ROW_OK, ROW_NAN, ROW_NO_FINITE, ROW_MASK_SHORT, ROW_FORCE_OOR, ROW_ZERO_WEIGHT, ROW_NARROW, \
-    ROW_BAD_PARAM, ROW_INTERNAL = range(9)
+    ROW_BAD_PARAM, ROW_INTERNAL, ROW_ID_OOR = range(10)
 K_MAX = 127
+SCORE_MAX = 4096
+CLASS_MAX = 8
 TOP_MAX = 128
 CTL_MAX = 2048
 ORDER_MAX = 1024
@@ -56,6 +58,10 @@ class SampleArgs(C.Structure):
         ("controls", _vp), ("ctl_ids", _vp), ("ctl_delta", _vp),
         ("row_order", _vp),  # host array [rows] (int32), or NULL
         ("k_max", _i32),     # this call's bound on min(top_k, enc), 0 = the context's
+        ("top_logprob64", _vp),
+        ("score_ids", _vp), ("n_score", _i32), ("score_ld", _i64), ("score_logprob", _vp),
+        ("class_masks", _vp), ("n_class", _i32), ("class_ld", _i64), ("class_mass", _vp),
+        ("probs", _vp), ("probs_ld", _i64),
     ]
 
 

@@ -35,6 +35,15 @@ int check_common(const xs_host_limits* lim, const float* logits, int64_t rows, i
 
 extern "C" {
 
+bool xs_host_wants_lse(const xs_sample_args* in) {
+  return in->row_max || in->row_lse || in->top_id || in->top_logprob || in->top_logprob64 ||
+         in->score_ids || in->class_masks || in->probs;
+}
+
+bool xs_host_wants_scores(const xs_sample_args* in) {
+  return in->score_ids || in->class_masks || in->probs;
+}
+
 int xs_host_check_sample(const xs_host_limits* lim, const xs_sample_args* in) {
   if (!lim || !in || !in->token || !in->status) return XS_ERR_ARG;
   const int rc = check_common(lim, in->logits, in->rows, in->ld, in->width, in->enc, in->params,
@@ -43,8 +52,17 @@ int xs_host_check_sample(const xs_host_limits* lim, const xs_sample_args* in) {
   if ((in->cand_id || in->cand_w) && in->cand_ld < 1) return XS_ERR_ARG;
   if (in->k_max < 0) return XS_ERR_ARG;
   if (in->n_top < 0 || in->n_top > XS_TOP_MAX) return XS_ERR_ARG;
-  if ((in->top_id || in->top_logprob) && in->top_ld < in->n_top) return XS_ERR_ARG;
-  const bool lse = in->row_max || in->row_lse || in->top_id || in->top_logprob;
+  if ((in->top_id || in->top_logprob || in->top_logprob64) && in->top_ld < in->n_top) return XS_ERR_ARG;
+  // the scoring reads (generate.rs:1871-1899)
+  if (in->score_logprob && !in->score_ids) return XS_ERR_ARG;
+  if (in->score_ids && (!in->score_logprob || in->n_score < 0 || in->n_score > XS_SCORE_MAX ||
+                        in->score_ld < in->n_score))
+    return XS_ERR_ARG;
+  if ((in->class_masks != nullptr) != (in->class_mass != nullptr)) return XS_ERR_ARG;
+  if (in->class_masks && (in->n_class < 0 || in->n_class > XS_CLASS_MAX || in->class_ld < (in->enc + 31) / 32))
+    return XS_ERR_ARG;
+  if (in->probs && in->probs_ld < in->enc) return XS_ERR_ARG;
+  const bool lse = xs_host_wants_lse(in);
   if (lse && (in->allowed || in->controls)) return XS_ERR_ARG;
   if (in->row_order) {  // a permutation of 0..rows-1
     if (in->rows > XS_ORDER_MAX) return XS_ERR_ARG;

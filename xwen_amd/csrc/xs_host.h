@@ -26,4 +26,8 @@ typedef struct {
 int xs_host_check_sample(const xs_host_limits* lim, const xs_sample_args* in);
 int xs_host_check_verify(const xs_host_limits* lim, const xs_verify_args* in);
 int xs_host_check_argmax(const xs_host_limits* lim, const xs_argmax_args* in);
+// Whether a sample call needs the rows' held_row lse (any held_row or scoring
+// output), and whether it asks for the scoring reads that score_kernel writes.
+bool xs_host_wants_lse(const xs_sample_args* in);
+bool xs_host_wants_scores(const xs_sample_args* in);
 }

@@ -399,7 +399,21 @@ struct Args {
   int32_t n_top;
   int32_t* top_id;
   float* top_logprob;
+  double* top_logprob64;
   int64_t top_ld;
+  // scoring reads (score_kernel), normalized by row_lse (the context's
+  // lse workspace when the caller takes no row_lse)
+  const int32_t* score_ids;
+  int32_t n_score;
+  int64_t score_ld;
+  double* score_logprob;
+  const uint32_t* class_masks;
+  int32_t n_class;
+  int64_t class_ld;
+  double* class_mass;
+  double* probs;
+  int64_t probs_ld;
+  uint64_t* score_part;  // [rows, n_chunks, XS_CLASS_MAX] the chunks' class sums (f64 bits)
   // verify walk (span == 0: plain batch)
   int32_t span;
   const int32_t* drafts;
@@ -1177,12 +1191,15 @@ XS_DEV void held_fold(const Args& a, int row, const float* rowp, const uint64_t*
   }
   const double lse = H.ok ? (double)m_v + log(D) : __builtin_nan("");
   if (lane == 0 && a.row_lse) a.row_lse[row] = lse;
-  if (a.top_logprob) {
+  if (a.top_logprob || a.top_logprob64) {
 #pragma unroll
     for (int r = 0; r < 2; r++) {
       const int i = r * 64 + lane;
-      if (i < a.n_top)
-        a.top_logprob[(int64_t)row * a.top_ld + i] = i < H.n_have ? (float)((double)H.vals[i] - lse) : __builtin_nanf("");
+      if (i < a.n_top) {
+        const double lp = i < H.n_have ? (double)H.vals[i] - lse : __builtin_nan("");
+        if (a.top_logprob) a.top_logprob[(int64_t)row * a.top_ld + i] = (float)lp;
+        if (a.top_logprob64) a.top_logprob64[(int64_t)row * a.top_ld + i] = lp;
+      }
     }
   }
 }
@@ -3557,6 +3574,104 @@ __global__ __launch_bounds__(BLOCK) void finalize_kernel(Args a) {
 }
 
 // ---------------------------------------------------------------------------
+// score_kernel: the scoring reads of held rows, launched after sample_kernel
+// has written each row's lse (held_row, generate.rs:1905-1933).  Grid: rows x
+// n_chunks, the chunks of sample_kernel.  Each workgroup forms, for the ids of
+// its chunk, p = exp(f64(v) - lse) -- the reference's last_probs term
+// (generate.rs:1893-1899), written out when `probs` is asked for -- and adds
+// the p of each class's ids, as escape_mass sums last_probs over its classes
+// (batch.rs:1638-1662).  The row's last workgroup to arrive (an arrival
+// ticket, slot 3 of the row's ticket line) adds the chunks' class sums in
+// chunk order.  Chunk 0's workgroup also reads the scored ids:
+// f64(v[id]) - lse, and an id outside [0, enc) fails the row as
+// last_logprobs_for does (generate.rs:1871-1883).  A row whose held_row
+// failed (NaN lse) keeps its status; its scores are NaN.
+__global__ __launch_bounds__(BLOCK) void score_kernel(Args a) {
+  __shared__ double expt[64];
+  __shared__ double part[NWAVE][XS_CLASS_MAX];
+  __shared__ int32_t last;
+  const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
+  const int nc = a.n_chunks;
+  const int row = blockIdx.x / nc, chunk = blockIdx.x - row * nc;
+  const int enc = (int)a.enc;
+  const int ncl = a.class_masks ? a.n_class : 0;
+  if (tid < 64) expt[tid] = (&kExpT[0][0])[tid];
+  const double lse = a.row_lse[row];
+  const bool ok = !__builtin_isnan(lse);
+  const float* rowp = a.logits + (int64_t)row * a.ld;
+  __syncthreads();
+  double acc[XS_CLASS_MAX];
+#pragma unroll
+  for (int c = 0; c < XS_CLASS_MAX; c++) acc[c] = 0.0;
+  const int s0 = chunk * SPC;
+  const int ns = min(SPC, a.nslots - s0);
+  for (int j = 0; j < ns; j++) {
+    const int id0 = ((s0 + j) * BLOCK + tid) * 4;
+    if (id0 < enc) {  // (the float4 lies inside the row: ld % 4 == 0 and id0 < enc <= ld)
+      const float4 v = reinterpret_cast<const float4*>(rowp)[id0 >> 2];
+      const float xv[4] = {v.x, v.y, v.z, v.w};
+      uint32_t w[XS_CLASS_MAX];
+#pragma unroll
+      for (int c = 0; c < XS_CLASS_MAX; c++)
+        w[c] = c < ncl ? a.class_masks[((int64_t)row * a.n_class + c) * a.class_ld + (id0 >> 5)] : 0u;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int id = id0 + e;
+        if (id < enc) {
+          const double p = ok ? exp_f64((double)xv[e] - lse, expt) : __builtin_nan("");
+          if (a.probs) a.probs[(int64_t)row * a.probs_ld + id] = p;
+#pragma unroll
+          for (int c = 0; c < XS_CLASS_MAX; c++)
+            if (c < ncl && ((w[c] >> (id & 31)) & 1u)) acc[c] += p;
+        }
+      }
+    }
+  }
+  if (chunk == 0 && a.score_ids) {
+    bool oor = false;
+    for (int i = tid; i < a.n_score; i += BLOCK) {
+      const int id = a.score_ids[(int64_t)row * a.score_ld + i];
+      const bool out = id < 0 || id >= enc;
+      oor |= out;
+      a.score_logprob[(int64_t)row * a.score_ld + i] = (out || !ok) ? __builtin_nan("") : (double)rowp[id] - lse;
+    }
+    if (__syncthreads_or(oor) && ok && tid == 0) {
+      a.status[row] = XS_ROW_ID_OOR;
+      a.token[row] = -1;
+    }
+  }
+  if (ncl == 0) return;
+  // the chunk's class sums: waves in order, then the row's chunks in order
+#pragma unroll
+  for (int c = 0; c < XS_CLASS_MAX; c++) {
+    if (c < ncl) {
+      const double t = wave_sumd(acc[c]);
+      if (lane == 0) part[wave][c] = t;
+    }
+  }
+  __syncthreads();
+  uint64_t* const prow = a.score_part + (int64_t)row * nc * XS_CLASS_MAX;
+  if (tid < ncl) {
+    double t = 0.0;
+#pragma unroll
+    for (int w = 0; w < NWAVE; w++) t += part[w][tid];
+    st_agent(&prow[chunk * XS_CLASS_MAX + tid], (uint64_t)__double_as_longlong(t));
+  }
+  drain();
+  __syncthreads();
+  if (tid == 0) {
+    const int t = __hip_atomic_fetch_add(&a.row_ticket[row * TSTRIDE + 3], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last = (t == nc - 1) ? 1 : 0;
+    if (t == nc - 1) st_agent(&a.row_ticket[row * TSTRIDE + 3], 0);
+  }
+  __syncthreads();
+  if (!last || tid >= ncl) return;
+  double m = 0.0;
+  for (int k = 0; k < nc; k++) m += __longlong_as_double((long long)ld_agent(&prow[k * XS_CLASS_MAX + tid]));
+  a.class_mass[(int64_t)row * a.n_class + tid] = m;
+}
+
+// ---------------------------------------------------------------------------
 // serial_kernel: the serial denominator of a call's controlled rows at
 // top_p >= 1, launched after sample_kernel on calls with a mask or controls
 // that can observe it (sample_kernel's last workgroup leaves those rows
@@ -4897,6 +5012,8 @@ struct xs_context {
   uint64_t* ser_e;      // [max_rows, SER_NB, SEG / 2] its kept terms
   uint32_t* ser_count;  // [1] rows the finalizers summed serially themselves (ser_local), or null
   int32_t ser_force;    // test hook: every checked row takes that fallback
+  double* lse_ws;       // [max_rows] held_row lse of calls that score without taking row_lse
+  uint64_t* score_part; // [max_rows, max_chunks, XS_CLASS_MAX] score_kernel's chunk class sums
 };
 
 namespace {
@@ -5039,6 +5156,8 @@ int xs_create_ex(int device, int64_t max_rows, int64_t vocab, int32_t k_max, int
   ok = ok && hipMalloc((void**)&c->ser_sum, max_rows * nseg * 2 * sizeof(uint64_t)) == hipSuccess;
   ok = ok && hipMalloc((void**)&c->ser_e, max_rows * xs::SER_NB * (xs::SEG / 2) * sizeof(uint64_t)) == hipSuccess;
   ok = ok && hipMalloc((void**)&c->ser_count, sizeof(uint32_t)) == hipSuccess;
+  ok = ok && hipMalloc((void**)&c->lse_ws, max_rows * sizeof(double)) == hipSuccess;
+  ok = ok && hipMalloc((void**)&c->score_part, (size_t)max_rows * mc * XS_CLASS_MAX * sizeof(uint64_t)) == hipSuccess;
   ok = ok && hipMemset(c->ser_count, 0, sizeof(uint32_t)) == hipSuccess;
   if (k_max > XS_K_MAX) {  // top_k past the streaming selection: the whole-row path's buffers
     ok = ok && hipMalloc((void**)&c->big, (size_t)max_rows * 2 * vocab * sizeof(uint64_t)) == hipSuccess;
@@ -5076,6 +5195,8 @@ int xs_destroy(xs_context* c) {
   (void)hipFree(c->ser_sum);
   (void)hipFree(c->ser_e);
   if (c->ser_count) (void)hipFree(c->ser_count);
+  if (c->lse_ws) (void)hipFree(c->lse_ws);
+  if (c->score_part) (void)hipFree(c->score_part);
   free(c);
   return XS_OK;
 }
@@ -5098,7 +5219,9 @@ int sample_impl(xs_context* ctx, const xs_sample_args* in, bool clear_tickets) {
   const xs_host_limits lim = limits_of(ctx);
   const int rc = xs_host_check_sample(&lim, in);
   if (rc) return rc;
-  const bool lse = in->row_max || in->row_lse || in->top_id || in->top_logprob;
+  const bool lse = xs_host_wants_lse(in);
+  const bool scores = xs_host_wants_scores(in);
+  if (scores && !ctx->lse_ws) return XS_ERR_ARG;  // (the static workspace of xs_sample_noalloc holds none)
   if (hipSetDevice(ctx->device) != hipSuccess) return XS_ERR_HIP;
   int32_t data_err = XS_ROW_OK;
   if (in->width < in->enc) data_err = XS_ROW_NARROW;
@@ -5128,10 +5251,22 @@ int sample_impl(xs_context* ctx, const xs_sample_args* in, bool clear_tickets) {
   a.soft_max = in->soft_max;
   a.soft_sum = in->soft_sum;
   a.row_max = in->row_max;
-  a.row_lse = in->row_lse;
-  a.n_top = (in->top_id || in->top_logprob) ? in->n_top : 0;
+  a.row_lse = in->row_lse ? in->row_lse : (scores ? ctx->lse_ws : nullptr);
+  a.n_top = (in->top_id || in->top_logprob || in->top_logprob64) ? in->n_top : 0;
   a.top_id = in->top_id;
   a.top_logprob = in->top_logprob;
+  a.top_logprob64 = in->top_logprob64;
+  a.score_ids = in->score_ids;
+  a.n_score = in->score_ids ? in->n_score : 0;
+  a.score_ld = in->score_ld;
+  a.score_logprob = in->score_logprob;
+  a.class_masks = in->class_masks;
+  a.n_class = in->class_masks ? in->n_class : 0;
+  a.class_ld = in->class_ld;
+  a.class_mass = in->class_mass;
+  a.probs = in->probs;
+  a.probs_ld = in->probs_ld;
+  a.score_part = ctx->score_part;
   a.top_ld = in->top_ld;
   a.controls = in->controls;
   a.ctl_ids = in->ctl_ids;
@@ -5151,7 +5286,11 @@ int sample_impl(xs_context* ctx, const xs_sample_args* in, bool clear_tickets) {
   // and a row whose token that sum does not settle is summed serially by its
   // finalizer (draw_settled, ser_local)
   const bool serial = in->cand_id || in->cand_w || in->soft_sum;
-  return launch(ctx, a, in->rows, 1, in->allowed != nullptr, lse, serial, in->row_order);
+  const int lrc = launch(ctx, a, in->rows, 1, in->allowed != nullptr, lse, serial, in->row_order);
+  if (lrc != XS_OK || !scores || in->rows == 0) return lrc;
+  // the scoring reads, once every row's lse is written
+  hipLaunchKernelGGL(xs::score_kernel, dim3((unsigned)(in->rows * a.n_chunks)), dim3(xs::BLOCK), 0, ctx->stream, a);
+  return hipGetLastError() == hipSuccess ? XS_OK : XS_ERR_HIP;
 }
 }  // namespace
 

@@ -50,6 +50,7 @@ ROW_STATUS_NAMES = {
                         "larger k_max), or a control list holds more entries than the context's "
                         "ctl_max (XS_CTL_MAX unless the context was created with a larger one)",
     _lib.ROW_INTERNAL: "internal error (reserved)",
+    _lib.ROW_ID_OOR: "a scored token id is outside the encodable ids",
 }
 
 
@@ -229,22 +230,32 @@ class Draws:
     row_lse: object = None
     top_id: object = None
     top_logprob: object = None
+    top_logprob64: object = None
+    score_logprob: object = None
+    class_mass: object = None
+    probs: object = None
 
 
 def sample_batch(ctx: Context, logits, params, uniforms, *, enc: int | None = None,
                  width: int | None = None, allowed=None, allowed_words: int | None = None,
                  cand_k: int = 0, stats: bool = False, n_top: int = 0, out: Draws | None = None,
                  controls: Controls | None = None, order=None, k_max: int = 0,
+                 score_ids=None, class_masks=None, probs: bool = False,
                  check: bool = True) -> Draws:
     """One xs_sample call.  logits: float32 [rows, ld] CUDA tensor (ld % 4 == 0);
     params: the uint8 tensor from params_tensor; uniforms: float32 [rows];
     order: an optional host permutation of the rows (see cost_order), the
     order in which the launch starts them; k_max: this call's bound on
     min(top_k, enc), 0 for the context's (127 or less skips the whole-row
-    kernels of a context sized for more)."""
+    kernels of a context sized for more).  The scoring reads of the held row
+    (generate.rs:1871-1899): score_ids, an int32 [rows, n] CUDA tensor of ids
+    (f64 log-probs out); class_masks, a [rows, n_class, words] u32 (as int32)
+    CUDA tensor of allow-mask-layout class masks (f64 class masses out);
+    probs, the whole f64 distribution."""
     a, out, keep = _sample_args(logits, params, uniforms, enc=enc, width=width, allowed=allowed,
                                 allowed_words=allowed_words, cand_k=cand_k, stats=stats,
-                                n_top=n_top, out=out, controls=controls, order=order, k_max=k_max)
+                                n_top=n_top, out=out, controls=controls, order=order, k_max=k_max,
+                                score_ids=score_ids, class_masks=class_masks, probs=probs)
     rc = ctx.lib.xs_sample(ctx.h, C.byref(a))
     del keep
     if check:
@@ -273,7 +284,8 @@ def sample_batch_noalloc(logits, params, uniforms, *, stream=None, check: bool =
 def _sample_args(logits, params, uniforms, *, enc: int | None = None, width: int | None = None,
                  allowed=None, allowed_words: int | None = None, cand_k: int = 0,
                  stats: bool = False, n_top: int = 0, out: Draws | None = None,
-                 controls: Controls | None = None, order=None, k_max: int = 0):
+                 controls: Controls | None = None, order=None, k_max: int = 0,
+                 score_ids=None, class_masks=None, probs: bool = False):
     """xs_sample_args for one call, the output tensors, and the host arrays the
     call reads (kept alive by the caller through the call)."""
     torch = _torch()
@@ -296,6 +308,13 @@ def _sample_args(logits, params, uniforms, *, enc: int | None = None, width: int
             out.row_lse = torch.empty(rows, dtype=torch.float64, device=dev)
             out.top_id = torch.empty((rows, n_top), dtype=torch.int32, device=dev)
             out.top_logprob = torch.empty((rows, n_top), dtype=torch.float32, device=dev)
+            out.top_logprob64 = torch.empty((rows, n_top), dtype=torch.float64, device=dev)
+        if score_ids is not None:
+            out.score_logprob = torch.empty(tuple(score_ids.shape), dtype=torch.float64, device=dev)
+        if class_masks is not None:
+            out.class_mass = torch.empty((rows, class_masks.shape[1]), dtype=torch.float64, device=dev)
+        if probs:
+            out.probs = torch.empty((rows, enc), dtype=torch.float64, device=dev)
     a = _lib.SampleArgs()
     a.logits = logits.data_ptr()
     a.rows, a.ld, a.width, a.enc = rows, ld, width, enc
@@ -322,7 +341,22 @@ def _sample_args(logits, params, uniforms, *, enc: int | None = None, width: int
         a.n_top = out.top_id.shape[1]
         a.top_id = out.top_id.data_ptr()
         a.top_logprob = out.top_logprob.data_ptr()
+        if out.top_logprob64 is not None:
+            a.top_logprob64 = out.top_logprob64.data_ptr()
         a.top_ld = out.top_id.shape[1]
+    if score_ids is not None:
+        a.score_ids = score_ids.data_ptr()
+        a.n_score = score_ids.shape[1]
+        a.score_ld = score_ids.shape[1]
+        a.score_logprob = out.score_logprob.data_ptr()
+    if class_masks is not None:
+        a.class_masks = class_masks.data_ptr()
+        a.n_class = class_masks.shape[1]
+        a.class_ld = class_masks.shape[2]
+        a.class_mass = out.class_mass.data_ptr()
+    if out.probs is not None:
+        a.probs = out.probs.data_ptr()
+        a.probs_ld = out.probs.shape[1]
     if controls is not None:
         a.controls = controls.rows.data_ptr()
         a.ctl_ids = controls.ids.data_ptr()
@@ -515,6 +549,70 @@ class Sampler:
 
     def sample(self, logits, uniforms=None):
         return self.sample_controlled(logits, None, uniforms)
+
+
+class HeldRow:
+    """The scoring reads of held logit rows (Generator::last_logprobs_for /
+    last_probs, generate.rs:1871-1899) on the device: every read is normalized
+    by held_row's f64 lse over the encodable ids (raw logits, no temperature),
+    and nothing but the asked-for values leaves the device.  logits: float32
+    [rows, ld] CUDA tensor (ld % 4 == 0).  Each call is one xs_sample launch
+    with greedy rows (no uniform is drawn) and the scoring outputs."""
+
+    def __init__(self, ctx: Context, logits, *, enc: int | None = None):
+        self.ctx, self.logits = ctx, logits
+        self.rows, ld = logits.shape
+        self.enc = ld if enc is None else enc
+
+    def _call(self, **kw) -> Draws:
+        torch = _torch()
+        dev = self.logits.device
+        p = params_tensor(0.0, 1, 1.0, self.rows, dev)
+        u = torch.zeros(self.rows, dtype=torch.float32, device=dev)
+        self.ctx.bind_current_stream()
+        out = sample_batch(self.ctx, self.logits, p, u, enc=self.enc, **kw)
+        st = out.status.cpu().numpy()
+        if st.any():
+            raise SampleError(st)
+        return out
+
+    def lse(self) -> np.ndarray:
+        return self._call(n_top=1).row_lse.cpu().numpy()
+
+    def last_logprobs_for(self, ids) -> np.ndarray:
+        """f64 log-probs [rows, n] of ids [rows, n] (one list for every row
+        when 1-D); an id outside [0, enc) raises, as the reference's error."""
+        torch = _torch()
+        i = np.asarray(ids, np.int32)
+        if i.ndim == 1:
+            i = np.broadcast_to(i, (self.rows, i.size))
+        t = torch.as_tensor(np.ascontiguousarray(i), device=self.logits.device)
+        return self._call(score_ids=t).score_logprob.cpu().numpy()
+
+    def last_probs(self):
+        """The f64 distribution [rows, enc], left on the device."""
+        return self._call(probs=True).probs
+
+    def class_masses(self, class_masks) -> np.ndarray:
+        """f64 [rows, n_class]: each class's probability mass, class_masks a
+        u32 [rows, n_class, words] (or [n_class, words] for every row) array in
+        the allow-mask layout."""
+        torch = _torch()
+        m = np.asarray(class_masks, np.uint32)
+        if m.ndim == 2:
+            m = np.broadcast_to(m, (self.rows,) + m.shape)
+        t = torch.as_tensor(np.ascontiguousarray(m).view(np.int32), device=self.logits.device)
+        return self._call(class_masks=t).class_mass.cpu().numpy()
+
+
+def escape_mass(inside: float, outside: float) -> float:
+    """escape_mass's ratio (batch.rs:1664-1669) from its two class masses: the
+    share of the content mass outside the field's options, clamped to [0, 1],
+    and 0 when every scrap of mass was formatting."""
+    content = inside + outside
+    if content <= 0.0:
+        return 0.0
+    return min(max(outside / content, 0.0), 1.0)
 
 
 def argmax_probs_device(ctx: Context, logits, *, width: int | None = None):

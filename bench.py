@@ -130,7 +130,8 @@ def calibrate_copy(nbytes: int, reps: int) -> None:
                       "launches": reps}), flush=True)
 
 
-def setup(name, nbuf, dev, torch, workloads, xsm, _lib, lib, k_max=None, call_k_max=0) -> dict:
+def setup(name, nbuf, dev, torch, workloads, xsm, _lib, lib, k_max=None, call_k_max=0,
+          tokens_only=False) -> dict:
     """Build one workload's inputs (resident in HBM, `nbuf` rotating copies)
     and its launch.  c2 is the headline configuration; c3-c5 are the other
     measured configurations of the path."""
@@ -188,11 +189,16 @@ def setup(name, nbuf, dev, torch, workloads, xsm, _lib, lib, k_max=None, call_k_
         if name in ("c3", "c3p1"):
             extra["mask"] = torch.as_tensor(wl.mask.view(np.int32)).to(dev)
             row_bytes += 4 * wl.mask.shape[1]
-        if name == "c3p1":  # the top-20 candidate list and the denominator
+        # the outputs each configuration names: C1 the renormalised top-k
+        # probabilities, C2 the top-20 (id, prob) per row, C3 at top_p 1 the
+        # top-20 list with the softmax denominator
+        if name in ("c1", "c2", "c3p1") and not tokens_only:
             for o in outs:
                 o.cand_id = torch.empty((rows, 20), **i32)
                 o.cand_w = torch.empty((rows, 20), dtype=torch.float32, device=dev)
                 o.n_cand = torch.empty(rows, **i32)
+        if name == "c3p1":
+            for o in outs:
                 o.soft_sum = torch.empty(rows, dtype=torch.float32, device=dev)
         if name == "c5":
             for o in outs:
@@ -214,6 +220,7 @@ def setup(name, nbuf, dev, torch, workloads, xsm, _lib, lib, k_max=None, call_k_
             if outs[i].cand_id is not None:
                 a.cand_id, a.cand_w = outs[i].cand_id.data_ptr(), outs[i].cand_w.data_ptr()
                 a.n_cand, a.cand_ld = outs[i].n_cand.data_ptr(), 20
+            if outs[i].soft_sum is not None:
                 a.soft_sum = outs[i].soft_sum.data_ptr()
             if outs[i].top_id is not None:
                 a.row_max, a.row_lse = outs[i].row_max.data_ptr(), outs[i].row_lse.data_ptr()
@@ -245,12 +252,13 @@ def setup(name, nbuf, dev, torch, workloads, xsm, _lib, lib, k_max=None, call_k_
 
 
 WORKLOAD_TEXT = {
-    "c1": "C1 single-row decode: 1 row x V=248,320 fp32, T 1.0 / top_k 20 / top_p 0.95 "
-          "(latency per row; 300 rotating copies)",
+    "c1": "C1 single-row decode: 1 row x V=248,320 fp32, T 1.0 / top_k 20 / top_p 0.95, "
+          "outputs the token and the renormalised top-20 probabilities (latency per row; 300 "
+          "rotating copies)",
     "c1g": "C1 single-row greedy decode: 1 row x V=248,320 fp32, T 0 (latency per row; "
            "300 rotating copies)",
     "c2": "C2 batched sampling: 64 rows x V=248,320 fp32, T 0.7 / top_k 20 / top_p 0.80, "
-          "one uniform per row",
+          "one uniform per row; outputs 64 token ids plus the top-20 (id, prob) per row",
     "c2w": "C2 rows with top_k >= V, the whole-row (top-p-only) path: 64 rows x V=248,320 fp32, "
            "T 0.7 / top_p 0.80, tokens only: the row sorted by (p desc, id asc) but for the ids "
            "at p < 1.75 * 2^-26, whose additions to the serial sums all round back",
@@ -286,6 +294,9 @@ def main() -> int:
     ap.add_argument("--call-k-max", type=int, default=0,
                     help="the calls' own bound on min(top_k, enc) (xs_sample_args.k_max; 0 = the "
                          "context's): 127 or less leaves the whole-row kernels out")
+    ap.add_argument("--tokens-only", action="store_true",
+                    help="take only tokens and statuses from c1 / c2 (their configurations also "
+                         "name the top-20 candidates), to price those outputs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path "
@@ -306,7 +317,8 @@ def main() -> int:
 
     dev = torch.device("cuda:0")
     lib = _lib.load()
-    S = setup(args.workload, args.nbuf, dev, torch, workloads, xsm, _lib, lib, args.k_max, args.call_k_max)
+    S = setup(args.workload, args.nbuf, dev, torch, workloads, xsm, _lib, lib, args.k_max, args.call_k_max,
+              args.tokens_only)
     wl, rows, ctx, step, outs, alg_bytes = S["wl"], S["rows"], S["ctx"], S["step"], S["outs"], S["alg_bytes"]
     V = wl.logits.shape[1]
 
@@ -382,8 +394,11 @@ def main() -> int:
         config["k_max"] = args.k_max
     if args.call_k_max:
         config["call_k_max"] = args.call_k_max
+    if args.tokens_only:
+        config["outputs"] = "token ids only (--tokens-only)"
     if headline:
         config.update({"temperature": 0.7, "top_k": 20, "top_p": 0.8})
+        config.setdefault("outputs", "token ids + top-20 (id, prob) per row (cand_id, cand_w)")
     config.update({"launch": "hipGraph" if graph is not None else "eager",
                    "rotating_buffers": nbuf, "buffer_bytes_total": nbuf * alg_bytes})
     result = {

@@ -125,6 +125,8 @@ def load() -> C.CDLL:
     L.xs_test_exp.argtypes = [_vp, _vp, _i64, _vp]
     L.xs_test_serial_fallback.restype = C.c_int
     L.xs_test_serial_fallback.argtypes = [_vp, _i32, C.POINTER(C.c_uint32)]
+    L.xs_test_xcd.restype = C.c_int
+    L.xs_test_xcd.argtypes = [_vp, _i32, C.POINTER(C.c_int32)]
     _lib = L
     return L
 

@@ -468,6 +468,10 @@ struct Args {
   // split launch: sample_kernel's workgroups publish and exit; finalize_kernel
   // (one workgroup per row) finalizes every row afterwards
   int32_t split;
+  // sample_kernel's grid: rows in groups of 2^xcd_log2 (the device's XCD
+  // count, or 1), nrows of them; xcd_test 2 makes the rows of several chunks
+  // fail their placement check (a test hook)
+  int32_t xcd_log2, nrows, xcd_test;
   uint64_t* ser_sum;  // [rows, ser_ld, 2]: segment summaries
   uint64_t* ser_e;    // [rows, SER_NB, SEG / 2]: kept segments' terms, two f32 per word
   int64_t ser_ld;     // segments per row of ser_sum
@@ -492,6 +496,20 @@ XS_DEV void st_agent(uint64_t* p, uint64_t v) { __hip_atomic_store(p, v, __ATOMI
 XS_DEV void st_agent(int32_t* p, int32_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 XS_DEV uint64_t ld_agent(const uint64_t* p) { return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 XS_DEV int32_t ld_agent(const int32_t* p) { return __hip_atomic_load(const_cast<int32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+
+// Sub-record stores and loads: sc0, which misses the CU's L1 and is served by
+// the XCD's L2.  sample_kernel places all workgroups of a row on one XCD (the
+// grid mapping in sample_kernel), so a row's sub-records go from its chunk
+// workgroups to its finalizer through that L2 alone, without the write-through
+// to memory and the memory round trips of sc1.  The row's arrival ticket
+// proves the placement (row_ticket_add); a row whose workgroups did not share
+// the finalizer's XCD is failed, never read.  Kernels launched later read the
+// sub-records after the launch boundary has written the L2 back.
+XS_DEV void st_sub(uint64_t* p, uint64_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
+XS_DEV uint64_t ld_sub(const uint64_t* p) { return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
+
+// The XCD (XCC_ID hardware register, bits 3:0) the calling wave runs on.
+XS_DEV uint32_t xcc_id() { return (uint32_t)__builtin_amdgcn_s_getreg(20 | (3 << 11)) & 15u; }
 
 // Wait until every memory operation this wave issued has completed.
 XS_DEV void drain() {
@@ -925,7 +943,7 @@ XS_DEV int wave_overflow(const float* rowp, const uint32_t* mrow, int s0, int ns
           const uint64_t b = __ballot(hit);
           if (b) {
             const int pos = n + lanes_below(b);
-            if (hit && pos < CAPW) st_agent(&sub[(int64_t)(SHDR + pos) * nsp], pack(fkey(x), (uint32_t)((s0 + h * H + u) * SLOT + 4 * tid + e)));
+            if (hit && pos < CAPW) st_sub(&sub[(int64_t)(SHDR + pos) * nsp], pack(fkey(x), (uint32_t)((s0 + h * H + u) * SLOT + 4 * tid + e)));
             n += __popcll(b);
           }
         }
@@ -957,7 +975,7 @@ XS_DEV int wave_overflow(const float* rowp, const uint32_t* mrow, int s0, int ns
           for (int e = 0; e < 4; e++)
             if (t[e]) {
               if (pos < need && n + pos < CAPW)
-                st_agent(&sub[(int64_t)(SHDR + n + pos) * nsp], pack(eq, (uint32_t)((s0 + h * H + u) * SLOT + 4 * tid + e)));
+                st_sub(&sub[(int64_t)(SHDR + n + pos) * nsp], pack(eq, (uint32_t)((s0 + h * H + u) * SLOT + 4 * tid + e)));
               pos++;
             }
           const int tot = (int)rdl((uint32_t)incl, 63);
@@ -1091,10 +1109,10 @@ XS_DEV void held_fold(const Args& a, int row, const float* rowp, const uint64_t*
       const bool has = s < nsub;
       // (s < nsp: the words lie inside the row's record; loaded unguarded,
       // so that all go out at once, and dropped where !has)
-      const uint64_t h1 = ld_agent(&rowrec[1 * nsp + s]), h2 = ld_agent(&rowrec[2 * nsp + s]);
-      const uint64_t h3 = ld_agent(&rowrec[3 * nsp + s]), h4 = ld_agent(&rowrec[4 * nsp + s]);
-      const uint64_t h7 = ld_agent(&rowrec[7 * nsp + s]), h8 = ld_agent(&rowrec[8 * nsp + s]);
-      const uint64_t h9 = ld_agent(&rowrec[9 * nsp + s]);
+      const uint64_t h1 = ld_sub(&rowrec[1 * nsp + s]), h2 = ld_sub(&rowrec[2 * nsp + s]);
+      const uint64_t h3 = ld_sub(&rowrec[3 * nsp + s]), h4 = ld_sub(&rowrec[4 * nsp + s]);
+      const uint64_t h7 = ld_sub(&rowrec[7 * nsp + s]), h8 = ld_sub(&rowrec[8 * nsp + s]);
+      const uint64_t h9 = ld_sub(&rowrec[9 * nsp + s]);
       const int c = s / NWAVE;
       const float mw = __uint_as_float((uint32_t)h3);
       const bool fold_data = ((h3 >> 32) & 8u) != 0;
@@ -1121,7 +1139,7 @@ XS_DEV void held_fold(const Args& a, int row, const float* rowp, const uint64_t*
         for (int j0 = 0; j0 < cnt; j0 += 8) {
           uint64_t e[8];  // (clamped inside the sub-record, not guarded: eight loads in flight)
 #pragma unroll
-          for (int u = 0; u < 8; u++) e[u] = ld_agent(&rowrec[(int64_t)(SHDR + min(j0 + u, CAPW - 1)) * nsp + s]);
+          for (int u = 0; u < 8; u++) e[u] = ld_sub(&rowrec[(int64_t)(SHDR + min(j0 + u, CAPW - 1)) * nsp + s]);
 #pragma unroll
           for (int u = 0; u < 8; u++) {
             const float x = keyf(pk_key(e[u])) - m_v;
@@ -1257,11 +1275,11 @@ XS_DEV float below_selection(const uint64_t* rowrec, int nsp, int nsub, const ui
     const int s = g * 64 + lane;
     const bool live = s < nsub;
     const int sc = min(s, nsp - 1);  // (clamped, not guarded: the loads go out together)
-    const uint64_t h3 = ld_agent(&rowrec[3 * nsp + sc]), h4 = ld_agent(&rowrec[4 * nsp + sc]);
-    const uint64_t h7 = ld_agent(&rowrec[7 * nsp + sc]);
+    const uint64_t h3 = ld_sub(&rowrec[3 * nsp + sc]), h4 = ld_sub(&rowrec[4 * nsp + sc]);
+    const uint64_t h7 = ld_sub(&rowrec[7 * nsp + sc]);
     uint64_t e[EPRE];
 #pragma unroll
-    for (int j = 0; j < EPRE; j++) e[j] = g == 0 ? E[j] : ld_agent(&rowrec[(SHDR + j) * nsp + sc]);
+    for (int j = 0; j < EPRE; j++) e[j] = g == 0 ? E[j] : ld_sub(&rowrec[(SHDR + j) * nsp + sc]);
     const int cnt = live ? (int)min((uint32_t)h4, (uint32_t)CAPW) : 0;
     float mb = -INFINITY;
 #pragma unroll
@@ -1433,7 +1451,7 @@ XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, int nsub, const uin
     uint64_t e[4];
 #pragma unroll
     for (int u = 0; u < 4; u++)  // (clamped inside the sub-record, not guarded: all four in flight)
-      e[u] = ld_agent(rowrec + (int64_t)(SHDR + min(j0 + u, CAPW - 1)) * nsp + lane);
+      e[u] = ld_sub(rowrec + (int64_t)(SHDR + min(j0 + u, CAPW - 1)) * nsp + lane);
 #pragma unroll
     for (int u = 0; u < 4; u++) put(e[u], j0 + u < lim && e[u] >= floor_e);
     if (srt && j0 + 3 < lim && e[3] < floor_e) lim = j0;
@@ -1669,7 +1687,7 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
       for (int t = 1; t < NHW; t++) v = i == t ? h[t] : v;
       return has(0) ? v : 0ull;
     }
-    const uint64_t v = ld_agent(&rr[i * nsp + min(g * 64 + lane, nsp - 1)]);  // (clamped, not guarded)
+    const uint64_t v = ld_sub(&rr[i * nsp + min(g * 64 + lane, nsp - 1)]);  // (clamped, not guarded)
     return has(g) ? v : 0ull;
   };
 
@@ -1779,7 +1797,7 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
       uint64_t e[4];
 #pragma unroll
       for (int u = 0; u < 4; u++)  // (clamped inside the sub-record, not guarded: all four in flight)
-        e[u] = ld_agent(rr + (int64_t)(SHDR + min(j + u, CAPW - 1)) * nsp + s);
+        e[u] = ld_sub(rr + (int64_t)(SHDR + min(j + u, CAPW - 1)) * nsp + s);
 #pragma unroll
       for (int u = 0; u < 4; u++) put(e[u], j + u < lim && e[u] >= fl_e);
       if (srt && j + 3 < lim && e[3] < fl_e) lim = j;
@@ -1809,7 +1827,7 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
       for (int g = 0; g < GMAX; g++) {
         const int s = g * 64 + lane;
         const int n = has(g) ? (int)min((uint32_t)hdr(g, 4), (uint32_t)CAPW) : 0;
-        for (int j = 0; j < n; j++) c += ld_agent(rr + (int64_t)(SHDR + j) * nsp + s) >= cnd ? 1 : 0;
+        for (int j = 0; j < n; j++) c += ld_sub(rr + (int64_t)(SHDR + j) * nsp + s) >= cnd ? 1 : 0;
       }
       if (wave_sumi(c) >= kp) ans = cnd;
     }
@@ -1999,7 +2017,7 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
                 uint64_t e[4];
 #pragma unroll
                 for (int u = 0; u < 4; u++)  // (clamped inside the sub-record, not guarded)
-                  e[u] = ld_agent(rr + (int64_t)(SHDR + min(j + u, CAPW - 1)) * nsp + s);
+                  e[u] = ld_sub(rr + (int64_t)(SHDR + min(j + u, CAPW - 1)) * nsp + s);
                 uint32_t hb = 0;  // bit u: entry j + u ties
 #pragma unroll
                 for (int u = 0; u < 4; u++) {
@@ -2392,9 +2410,9 @@ XS_DEV void load_heads(const uint64_t* rowrec, int nsp, int nsub, uint64_t (&h)[
   const bool live = lane < nsub;
 #pragma unroll
   for (int i = 0; i < NHW; i++)  // (word 2, the held_row partial, only when it is read)
-    h[i] = (i == 2 && !WANT_LSE) ? 0ull : ld_agent(&rowrec[(uint32_t)(i * nsp + lane)]);
+    h[i] = (i == 2 && !WANT_LSE) ? 0ull : ld_sub(&rowrec[(uint32_t)(i * nsp + lane)]);
 #pragma unroll
-  for (int j = 0; j < EPRE; j++) E[j] = ld_agent(&rowrec[(uint32_t)((SHDR + j) * nsp + lane)]);
+  for (int j = 0; j < EPRE; j++) E[j] = ld_sub(&rowrec[(uint32_t)((SHDR + j) * nsp + lane)]);
 #pragma unroll
   for (int i = 0; i < NHW; i++) h[i] = live ? h[i] : 0ull;
 #pragma unroll
@@ -3040,14 +3058,37 @@ XS_DEV void ser_fallback(const Args& a, const Cfg& cfg, int row, const uint64_t*
   wave_lds_sync();  // read before ser_local reuses the memory
   const float S_ser = ser_local<HAS_MASK, HAS_CTL>(a, cfg, row, m_s, Tl.ser);
   if (lane_id() == 0 && a.ser_count) atomicAdd(a.ser_count, 1u);
-  finalize_row<HAS_MASK, WANT_LSE, HAS_CTL>(a, cfg, row, rowrec, nsp, nsub, rowp, mrow, Tl.fin, S_ser);
+  // The record's address and stride pass through an empty asm statement, so
+  // the compiler forms this finalize_row's addresses afresh instead of
+  // keeping the first one's live across it (18 such registers spilled to
+  // scratch in the masked and controlled kernels).
+  const uint64_t* rr = rowrec;
+  int np = __builtin_amdgcn_readfirstlane(nsp);
+  asm volatile("" : "+s"(rr), "+s"(np));
+  finalize_row<HAS_MASK, WANT_LSE, HAS_CTL>(a, cfg, row, rr, np, nsub, rowp, mrow, Tl.fin, S_ser);
+}
+
+// The row's arrival ticket counts its workgroups (bits 0-7; a row has at most
+// GMAX * 64 / NWAVE = 64 chunks) and sums their XCDs x (bits 8-17, at most
+// 64 * 15) and x^2 (bits 18-31, at most 64 * 225): the fields never carry
+// into each other.  The last workgroup, on XCD y, holds the totals of all nc
+// workgroups; sum x = nc y and sum x^2 = nc y^2 make sum (x - y)^2 = 0, so
+// every workgroup of the row ran on XCD y and its sub-records are in y's L2.
+XS_DEV uint32_t row_ticket_add(uint32_t x) { return 1u | (x << 8) | ((x * x) << 18); }
+XS_DEV bool row_on_one_xcd(uint32_t total, int nc, uint32_t y) {
+  return ((total >> 8) & 0x3FFu) == (uint32_t)nc * y && (total >> 18) == (uint32_t)nc * y * y;
 }
 
 // ---------------------------------------------------------------------------
-// The kernel.  Grid: rows x n_chunks workgroups of BLOCK lanes; chunk c of a
-// row covers slots [c*SPC, c*SPC + SPC).  Every wave reduces its own share of
-// the chunk and publishes it as one sub-record; the row's last workgroup to
-// arrive (an atomic ticket per row) finalizes the row with its first wave.
+// The kernel.  Grid: groups of n = 2^xcd_log2 rows x n_chunks workgroups of
+// BLOCK lanes (the row count rounded up to whole groups; workgroups past the
+// last row return at once); chunk c of a row covers slots [c*SPC, c*SPC +
+// SPC).  The hardware hands workgroup b of a launch to XCD b mod n (round
+// robin over the device's n XCDs, measured on every launch shape), so
+// workgroup (g*nc + c)*n + r takes chunk c of row g*n + r: all of a row's
+// workgroups run on one XCD.  Every wave reduces its own share of the chunk
+// and publishes it as one sub-record; the row's last workgroup to arrive (an
+// atomic ticket per row) finalizes the row with its first wave.
 
 template <bool HAS_MASK, bool WANT_LSE, bool HAS_CTL, bool ORD>
 __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) void sample_kernel(Args a, RowOrder<ORD> ro) {
@@ -3055,8 +3096,11 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
   __shared__ TailLds Tl;
   const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
   const int nc = a.n_chunks;
-  const int rb = blockIdx.x / nc;
-  const int chunk = blockIdx.x - rb * nc;
+  const int gc = (int)(blockIdx.x >> a.xcd_log2);  // (group, chunk) of the workgroup
+  const int grp = gc / nc;
+  const int chunk = gc - grp * nc;
+  const int rb = (grp << a.xcd_log2) | (int)(blockIdx.x & ((1u << a.xcd_log2) - 1u));
+  if (rb >= a.nrows) return;  // the last group's padding
   int row = rb;
   if constexpr (ORD) row = ro.v[rb];
   const int enc = (int)a.enc;
@@ -3506,7 +3550,7 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
       v = i == 8 ? hw8 : v;
       v = i == 9 ? hw9 : v;
       if (i >= SHDR) v = stg[i - SHDR];
-      st_agent(sub + (uint32_t)i * (uint32_t)nsp, v);
+      st_sub(sub + (uint32_t)i * (uint32_t)nsp, v);
     }
   }
 
@@ -3519,9 +3563,15 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
   drain();
   __syncthreads();
   if (tid == 0) {
-    const int t = __hip_atomic_fetch_add(&a.row_ticket[row * TSTRIDE], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    Lc.last = (t == nc - 1) ? 1 : 0;
-    if (t == nc - 1) {
+    // (xcd_test 2 flips the low bit of the XCD the odd chunks report: a row
+    // of several chunks then fails the placement check, a test hook)
+    const uint32_t x = xcc_id() ^ ((a.xcd_test == 2) ? (uint32_t)(chunk & 1) : 0u);
+    const uint32_t add = row_ticket_add(x);
+    const uint32_t t = (uint32_t)__hip_atomic_fetch_add(&a.row_ticket[row * TSTRIDE], (int32_t)add, __ATOMIC_RELAXED,
+                                                        __HIP_MEMORY_SCOPE_AGENT);
+    const bool lastw = (int)(t & 0xFFu) == nc - 1;
+    Lc.last = lastw ? (row_on_one_xcd(t + add, nc, x) ? 1 : 2) : 0;
+    if (lastw) {
       st_agent(&a.row_ticket[row * TSTRIDE], 0);
       st_agent(&a.row_ticket[row * TSTRIDE + 1], 0);  // held_row's running max key
     }
@@ -3529,17 +3579,29 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
   __syncthreads();
   if (!Lc.last) return;
   if (a.serial && serial_row<HAS_MASK, HAS_CTL>(a, cfg, row)) return;  // serial_kernel finalizes it
+
   // The first wave finalizes the row; held_row outputs then get the reference's
   // serial fold (held_fold); a verify block's rows then walk accept_drafts
   // (verify_walk), except a row with more candidates than the selection
   // holds: the whole-row kernels draw it and walk its block.  On a masked or
   // controlled launch a row whose token the exact sum does not settle is
   // summed serially by the same wave and finalized again (ser_fallback).
+  // A row whose workgroups did not all run on this XCD (Lc.last 2) has
+  // sub-records outside this L2: it is failed, not read, and its sequence's
+  // walk stops at it.
   if (wave != 0) return;
-  finalize_row<HAS_MASK, WANT_LSE, HAS_CTL>(a, cfg, row, rowrec, nsp, nc * NWAVE, rowp, mrow, Tl.fin);
-  if (HAS_MASK || HAS_CTL) ser_fallback<HAS_MASK, WANT_LSE, HAS_CTL>(a, cfg, row, rowrec, nsp, nc * NWAVE, rowp, mrow, Tl);
-  if (held) held_fold<1>(a, row, rowp, rowrec, nsp, nc * NWAVE, Tl.fin);
-  if (a.span > 0 && !deferred(cfg, Tl.fin)) verify_walk(a, row);
+  const bool placed = Lc.last == 1;
+  if (placed) {
+    finalize_row<HAS_MASK, WANT_LSE, HAS_CTL>(a, cfg, row, rowrec, nsp, nc * NWAVE, rowp, mrow, Tl.fin);
+    if (HAS_MASK || HAS_CTL) ser_fallback<HAS_MASK, WANT_LSE, HAS_CTL>(a, cfg, row, rowrec, nsp, nc * NWAVE, rowp, mrow, Tl);
+    if (held) held_fold<1>(a, row, rowp, rowrec, nsp, nc * NWAVE, Tl.fin);
+  } else if (lane == 0) {
+    st_agent(&a.token[row], -1);
+    st_agent(&a.status[row], XS_ROW_INTERNAL);
+    if (a.n_cand) a.n_cand[row] = 0;
+    if (cfg.big && a.big_state) a.big_state[row].state = 0;  // the whole-row kernels pass it by
+  }
+  if (a.span > 0 && (!placed || !deferred(cfg, Tl.fin))) verify_walk(a, row);
 }
 
 // ---------------------------------------------------------------------------
@@ -4203,6 +4265,11 @@ __global__ void fill_verify_kernel(const xs_verify_args a, int32_t st) {
 
 // Zeroes n ints (the arrival tickets of the no-allocation entry point; a
 // kernel rather than hipMemsetAsync, so a captured call records no memset node).
+// Each workgroup's XCD (xcd_placement).
+__global__ void xcc_probe_kernel(uint32_t* out) {
+  if (threadIdx.x == 0) out[blockIdx.x] = xcc_id();
+}
+
 __global__ void zero_kernel(int32_t* p, int64_t n) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] = 0;
@@ -4994,6 +5061,9 @@ struct xs_context {
   int32_t k_max;
   int32_t max_chunks;
   int32_t n_cu;         // compute units of the device
+  int32_t xcd;          // the device's XCDs, whose round-robin placement sample_kernel's grid
+                        // follows; 0: the placement was not confirmed, every call takes the split launch
+  int32_t xcd_test;     // test hook: 1 the split launch, 2 the placement check fails (odd chunks report another XCD)
   uint64_t* rec;
   int32_t* row_status;  // [max_rows] statuses of calls whose caller takes none (xs_argmax_probs)
   uint64_t* ctl_patch;  // [max_rows, ctl_cap] patch lists of controlled calls
@@ -5024,25 +5094,50 @@ static_assert(xs_host::SLOT == xs::SLOT && xs_host::SPC == xs::SPC, "the host ch
 
 xs_host_limits limits_of(const xs_context* ctx) { return xs_host_limits{ctx->max_rows, ctx->vocab, ctx->max_chunks}; }
 
+// The device's XCD count n when its placement is confirmed, else 0: a probe
+// launch of 64 n workgroups records each one's XCD, and n is kept when every
+// workgroup b ran on the XCD of workgroup b mod n (sample_kernel's grid puts
+// a row's workgroups n apart).  Kernels still check each row's placement.
+int xcd_placement(int device) {
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeNumberOfXccs, device) != hipSuccess || n < 1 || n > 16 ||
+      (n & (n - 1)) != 0)
+    return 0;
+  const int nb = 64 * n;
+  uint32_t* d = nullptr;
+  if (hipMalloc((void**)&d, nb * sizeof(uint32_t)) != hipSuccess) return 0;
+  hipLaunchKernelGGL(xs::xcc_probe_kernel, dim3((unsigned)nb), dim3(64), 0, nullptr, d);
+  std::vector<uint32_t> h((size_t)nb);
+  const bool ok = hipGetLastError() == hipSuccess &&
+                  hipMemcpy(h.data(), d, nb * sizeof(uint32_t), hipMemcpyDeviceToHost) == hipSuccess;
+  (void)hipFree(d);
+  if (!ok) return 0;
+  for (int b = 0; b < nb; b++)
+    if (h[(size_t)b] != h[(size_t)(b % n)]) return 0;
+  return n;
+}
+
 // One sample_kernel launch over rows x n_chunks workgroups (it finalizes the
 // rows itself), or, for a large batch, sample_kernel then finalize_kernel; a
 // call with sparse controls runs control_kernel (one workgroup per row) first,
 // one that can observe the serial denominator serial_kernel after them, and a
 // context sized for top_k >= 128 the whole-row kernels last.
 template <bool M, bool S, bool C>
-void launch2(xs_context* ctx, xs::Args& a, int64_t rows, dim3 g1, const int32_t* order) {
+void launch2(xs_context* ctx, xs::Args& a, int64_t rows, dim3 g1, dim3 gs, const int32_t* order) {
   // More workgroups than the GPU holds at once (4 per CU): the split launch,
   // unless the rows carry held_row statistics or a cost order -- their long
   // finalizers then overlap the later rows' streaming inside one launch (C5:
   // 75 us in one launch, 91 us split; C4: 57.2 us in one, 55.4 us split).
-  a.split = (g1.x > (unsigned)(4 * ctx->n_cu) && !S && !order) ? 1 : 0;
+  // A context whose XCD placement was not confirmed always splits: the
+  // launch boundary, not one XCD's L2, then orders the sub-records.
+  a.split = ((g1.x > (unsigned)(4 * ctx->n_cu) && !S && !order) || ctx->xcd == 0 || ctx->xcd_test == 1) ? 1 : 0;
   if (C) hipLaunchKernelGGL((xs::control_kernel<M>), dim3((unsigned)rows), dim3(xs::BLOCK), 0, ctx->stream, a);
   if (order) {
     xs::RowOrder<true> ro;
     for (int64_t i = 0; i < rows; i++) ro.v[i] = (uint16_t)order[i];
-    hipLaunchKernelGGL((xs::sample_kernel<M, S, C, true>), g1, dim3(xs::BLOCK), 0, ctx->stream, a, ro);
+    hipLaunchKernelGGL((xs::sample_kernel<M, S, C, true>), gs, dim3(xs::BLOCK), 0, ctx->stream, a, ro);
   } else {
-    hipLaunchKernelGGL((xs::sample_kernel<M, S, C, false>), g1, dim3(xs::BLOCK), 0, ctx->stream, a,
+    hipLaunchKernelGGL((xs::sample_kernel<M, S, C, false>), gs, dim3(xs::BLOCK), 0, ctx->stream, a,
                        xs::RowOrder<false>{});
   }
   if (a.split) hipLaunchKernelGGL((xs::finalize_kernel<M, S, C>), dim3((unsigned)rows), dim3(xs::BLOCK), 0, ctx->stream, a);
@@ -5073,7 +5168,13 @@ int launch(xs_context* ctx, xs::Args& a, int64_t rows, int span, bool mask, bool
   const bool ctl = a.controls != nullptr;
   const int64_t grid = rows * (int64_t)a.n_chunks;
   if (grid == 0) return XS_OK;
-  if (grid > 0x7FFFFFFF || span < 1) return XS_ERR_CAPACITY;
+  // sample_kernel's grid: whole groups of xcd rows (all workgroups of a row on one XCD)
+  const int nx = ctx->xcd > 0 ? ctx->xcd : 1;
+  a.xcd_log2 = __builtin_ctz((unsigned)nx);
+  a.nrows = (int32_t)rows;
+  a.xcd_test = ctx->xcd_test;
+  const int64_t gpad = (rows + nx - 1) / nx * nx * (int64_t)a.n_chunks;
+  if (gpad > 0x7FFFFFFF || span < 1) return XS_ERR_CAPACITY;
   if ((mask || ctl) && lse) return XS_ERR_ARG;
   a.patch = ctx->ctl_patch;
   a.ctl_keys = ctx->ctl_keys;
@@ -5100,12 +5201,12 @@ int launch(xs_context* ctx, xs::Args& a, int64_t rows, int span, bool mask, bool
   a.ser_sum = ctx->ser_sum;
   a.ser_e = ctx->ser_e;
   a.ser_ld = (int64_t)ctx->max_chunks * xs::SPC * xs::NWAVE;
-  const dim3 g1((unsigned)grid);
-  if (ctl && mask) launch2<true, false, true>(ctx, a, rows, g1, order);
-  else if (ctl) launch2<false, false, true>(ctx, a, rows, g1, order);
-  else if (mask) launch2<true, false, false>(ctx, a, rows, g1, order);
-  else if (lse) launch2<false, true, false>(ctx, a, rows, g1, order);
-  else launch2<false, false, false>(ctx, a, rows, g1, order);
+  const dim3 g1((unsigned)grid), gs((unsigned)gpad);
+  if (ctl && mask) launch2<true, false, true>(ctx, a, rows, g1, gs, order);
+  else if (ctl) launch2<false, false, true>(ctx, a, rows, g1, gs, order);
+  else if (mask) launch2<true, false, false>(ctx, a, rows, g1, gs, order);
+  else if (lse) launch2<false, true, false>(ctx, a, rows, g1, gs, order);
+  else launch2<false, false, false>(ctx, a, rows, g1, gs, order);
   return hipGetLastError() == hipSuccess ? XS_OK : XS_ERR_HIP;
 }
 
@@ -5136,6 +5237,7 @@ int xs_create_ex(int device, int64_t max_rows, int64_t vocab, int32_t k_max, int
   c->max_chunks = mc;
   if (hipDeviceGetAttribute(&c->n_cu, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || c->n_cu < 1)
     c->n_cu = 256;
+  c->xcd = xcd_placement(device);
   c->ctl_cap = ctl_max > xs::CTL_MAX ? ctl_max : xs::CTL_MAX;
   const int64_t nsp = ((int64_t)mc * xs::NWAVE + 63) / 64 * 64;  // sub-records per row, padded
   const int64_t units = max_rows * nsp;
@@ -5311,6 +5413,22 @@ int na_cus(int dev) {  // the device's compute units, asked once
   return na_cu[dev];
 }
 
+// The device's XCD count, asked once (no probe launch: this entry point may
+// run under graph capture; sample_kernel checks each row's placement), or 0
+// when the device does not report one: every call then takes the split launch.
+int na_xcd[NA_MAX_DEVICES];
+bool na_xcd_known[NA_MAX_DEVICES];
+int na_xcds(int dev) {
+  std::lock_guard<std::mutex> g(na_mu);
+  if (!na_xcd_known[dev]) {
+    int n = 0;
+    na_xcd[dev] = (hipDeviceGetAttribute(&n, hipDeviceAttributeNumberOfXccs, dev) == hipSuccess && n >= 1 && n <= 16 &&
+                   (n & (n - 1)) == 0) ? n : 0;
+    na_xcd_known[dev] = true;
+  }
+  return na_xcd[dev];
+}
+
 uint64_t* noalloc_scratch(int dev) {
   std::lock_guard<std::mutex> g(na_mu);
   if (!na_ptr[dev]) {
@@ -5339,6 +5457,7 @@ int xs_sample_noalloc(const xs_sample_args* in, void* hip_stream) {
   c.k_max = XS_K_MAX;
   c.max_chunks = (int32_t)xs::NA_CHUNKS;
   c.n_cu = na_cus(dev);
+  c.xcd = na_xcds(dev);
   c.rec = base + xs::NA_OFF_REC;
   c.ctl_patch = base + xs::NA_OFF_PATCH;
   c.ctl_cap = xs::CTL_MAX;
@@ -5429,6 +5548,13 @@ int xs_test_serial_fallback(xs_context* c, int32_t force, uint32_t* count) {
     if (hipMemcpy(count, c->ser_count, sizeof(uint32_t), hipMemcpyDeviceToHost) != hipSuccess) return XS_ERR_HIP;
   }
   c->ser_force = force != 0 ? 1 : 0;
+  return XS_OK;
+}
+
+int xs_test_xcd(xs_context* c, int32_t mode, int32_t* xcd) {
+  if (!c || mode < 0 || mode > 2) return XS_ERR_ARG;
+  if (xcd) *xcd = c->xcd;
+  c->xcd_test = mode;
   return XS_OK;
 }
 

@@ -49,7 +49,7 @@ ROW_STATUS_NAMES = {
     _lib.ROW_BAD_PARAM: "top_k exceeds the sampler context's k_max (create the context with a "
                         "larger k_max), or a control list holds more entries than the context's "
                         "ctl_max (XS_CTL_MAX unless the context was created with a larger one)",
-    _lib.ROW_INTERNAL: "internal error (reserved)",
+    _lib.ROW_INTERNAL: "the row's workgroups did not share one XCD (placement check); not sampled",
     _lib.ROW_ID_OOR: "a scored token id is outside the encodable ids",
 }
 

@@ -62,8 +62,8 @@ extern "C" {
  *                      the grid's placement expects (no reference
  *                      counterpart); the row was not sampled, its token is -1.
  *                      A context checks the placement when it is created and
- *                      otherwise takes the split launch, so this is not seen
- *                      in practice; xs_test_xcd forces it
+ *                      otherwise hands sub-records off through memory, so
+ *                      this is not seen in practice; xs_test_xcd forces it
  *   XS_ROW_ID_OOR      a scored id (score_ids) outside the encodable ids
  *                      (last_logprobs_for, generate.rs:1874-1879)           */
 #define XS_ROW_OK 0
@@ -378,13 +378,15 @@ int xs_test_exp(const float* x, float* y, int64_t n, void* hip_stream);
  * there, force == 0 restores the check. */
 int xs_test_serial_fallback(xs_context* ctx, int32_t force, uint32_t* count);
 
-/* Test hook (no reference counterpart): the XCD-local hand-off.  A row's
- * workgroups run on one XCD and hand their sub-records to the row's finalizer
- * through that XCD's L2; the row's arrival ticket proves the placement.  *xcd
- * (if not null) receives the context's XCD count (0: the placement was not
- * confirmed at creation, every call takes the split launch).  mode 0 is the
- * normal launch, 1 takes the split launch (the finalizers in a second kernel),
- * 2 makes every row of several chunks fail the placement check
+/* Test hook (no reference counterpart): the XCD-local hand-off.  In a call
+ * of at least 8 rows per XCD of the device, a row's workgroups run on
+ * one XCD and hand their sub-records to the row's finalizer through that
+ * XCD's L2; the row's arrival ticket proves the placement.  Smaller calls
+ * spread each row over the XCDs and hand off through memory.  *xcd (if not
+ * null) receives the context's XCD count (0: the placement was not confirmed
+ * at creation, every call hands off through memory).  mode 0 is the normal
+ * launch, 1 takes the split launch (the finalizers in a second kernel), 2
+ * makes every XCD-local row of several chunks fail the placement check
  * (XS_ROW_INTERNAL). */
 int xs_test_xcd(xs_context* ctx, int32_t mode, int32_t* xcd);
 

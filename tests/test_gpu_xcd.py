@@ -1,7 +1,8 @@
 """The XCD-local hand-off: every workgroup of a row runs on one XCD.
 
-sample_kernel's grid puts a row's chunks n workgroups apart (n the device's
-XCD count; the hardware deals workgroup b to XCD b mod n), so the chunk
+In a call of at least 8 rows per XCD, sample_kernel's grid puts a row's
+chunks n workgroups apart (n the device's XCD count; the hardware deals
+workgroup b to XCD b mod n), so the chunk
 workgroups hand their sub-records to the row's finalizer through that XCD's
 L2 (sc0 stores and loads) instead of through memory.  The row's arrival ticket
 proves the placement: it sums the workgroups' XCDs and their squares, and a
@@ -16,7 +17,10 @@ Checked here, through the hook xs_test_xcd:
   are and are not multiples of the XCD count;
 - a placement failure forced from the host (the odd chunks of each row
   report another XCD) fails every row of several chunks loudly, token -1,
-  and a verify block's sequences with it; the next call is normal again.
+  and a verify block's sequences with it; the next call is normal again;
+- a call of fewer than 8 rows per XCD spreads each row over the XCDs and
+  hands off through memory (one XCD would stream a lone row at its share of
+  the bandwidth), so the forced failure leaves it untouched.
 """
 import ctypes
 
@@ -81,14 +85,20 @@ def test_the_context_confirms_the_placement(ctx):
 
 
 def _cases():
-    c2, c3, c5 = workloads.c2_batch(), workloads.c3_masked(), workloads.c5_heterogeneous()
+    """Row counts of 64 and more hand off XCD-locally (71, 72 and 100 pad the
+    last group of 8); fewer spread each row over the XCDs."""
+    c2, c5 = workloads.c2_batch(rows=80), workloads.c5_heterogeneous()
+    c3, c3w = workloads.c3_masked(), workloads.c3_masked(seed=313, rows=72)
     return [
-        ("C2 64 rows with candidates", c2, None, dict(cand_k=20, stats=True)),
+        ("C2 64 rows with candidates", c2, 64, dict(cand_k=20, stats=True)),
+        ("C2 71 rows tokens only", c2, 71, {}),
         ("C2 13 rows tokens only", c2, 13, {}),
         ("C2 1 row", c2, 1, dict(cand_k=20)),
         ("C3 32 masked rows", c3, None, dict(allowed=dev(c3.mask.view(np.int32)), cand_k=20, stats=True)),
-        ("C3 27 masked rows tokens only", c3, 27, dict(allowed=dev(c3.mask[:27].view(np.int32)))),
+        ("C3 72 masked rows", c3w, None, dict(allowed=dev(c3w.mask.view(np.int32)), cand_k=20, stats=True)),
+        ("C3 70 masked rows tokens only", c3w, 70, dict(allowed=dev(c3w.mask[:70].view(np.int32)))),
         ("C5 256 rows with held_row statistics", c5, None, dict(n_top=20, stats=True)),
+        ("C5 100 rows with held_row statistics", c5, 100, dict(n_top=20)),
         ("C5 37 rows with held_row statistics", c5, 37, dict(n_top=20)),
     ]
 
@@ -138,6 +148,15 @@ def test_a_forced_placement_failure_fails_rows_loudly(ctx):
     assert (bad["n_cand"] == 0).all()
     again = draw(ctx, wl, cand_k=20)
     same_bits(good, again, "after the forced failure")
+    # fewer than 8 rows per XCD: each row spreads over the XCDs and hands off
+    # through memory, with no placement to check
+    for rows in (5, 40):
+        small = draw(ctx, wl, rows, cand_k=20)
+        set_mode(ctx, 2)
+        small2 = draw(ctx, wl, rows, cand_k=20)
+        set_mode(ctx, 0)
+        same_bits(small, small2, f"{rows} rows, spread over the XCDs")
+        assert (small["status"] == 0).all()
     # a verify block in one launch: every sequence stops at its first row,
     # with that row's status
     c4 = workloads.c4_verify(seqs=4)

@@ -505,8 +505,22 @@ XS_DEV int32_t ld_agent(const int32_t* p) { return __hip_atomic_load(const_cast<
 // proves the placement (row_ticket_add); a row whose workgroups did not share
 // the finalizer's XCD is failed, never read.  Kernels launched later read the
 // sub-records after the launch boundary has written the L2 back.
-XS_DEV void st_sub(uint64_t* p, uint64_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
-XS_DEV uint64_t ld_sub(const uint64_t* p) { return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP); }
+//
+// A launch of fewer than 8 rows per XCD spreads each row over the XCDs
+// instead (a lone row streamed through one XCD gets that XCD's share of the
+// bandwidth: C1 greedy took 9.3 us instead of 8.8) and instantiates the
+// kernel with LOC false: the hand-off then takes agent-scope sc1 stores and
+// loads, performed beyond the L2s.
+template <bool LOC>
+XS_DEV void st_sub(uint64_t* p, uint64_t v) {
+  if constexpr (LOC) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  else __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <bool LOC>
+XS_DEV uint64_t ld_sub(const uint64_t* p) {
+  if constexpr (LOC) return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  else return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // The XCD (XCC_ID hardware register, bits 3:0) the calling wave runs on.
 XS_DEV uint32_t xcc_id() { return (uint32_t)__builtin_amdgcn_s_getreg(20 | (3 << 11)) & 15u; }
@@ -844,7 +858,7 @@ struct ChunkCtl {
   float pull_val, force_val;
 };
 
-template <bool HAS_MASK, bool HAS_CTL>
+template <bool HAS_MASK, bool HAS_CTL, bool LOC>
 XS_DEV int wave_overflow(const float* rowp, const uint32_t* mrow, int s0, int ns, int enc,
                          uint64_t* sub, int nsp, int kp, uint32_t tk, const ChunkCtl& cc) {
   constexpr int H = SPC / 2;  // slots per round of loads
@@ -943,7 +957,7 @@ XS_DEV int wave_overflow(const float* rowp, const uint32_t* mrow, int s0, int ns
           const uint64_t b = __ballot(hit);
           if (b) {
             const int pos = n + lanes_below(b);
-            if (hit && pos < CAPW) st_sub(&sub[(int64_t)(SHDR + pos) * nsp], pack(fkey(x), (uint32_t)((s0 + h * H + u) * SLOT + 4 * tid + e)));
+            if (hit && pos < CAPW) st_sub<LOC>(&sub[(int64_t)(SHDR + pos) * nsp], pack(fkey(x), (uint32_t)((s0 + h * H + u) * SLOT + 4 * tid + e)));
             n += __popcll(b);
           }
         }
@@ -975,7 +989,7 @@ XS_DEV int wave_overflow(const float* rowp, const uint32_t* mrow, int s0, int ns
           for (int e = 0; e < 4; e++)
             if (t[e]) {
               if (pos < need && n + pos < CAPW)
-                st_sub(&sub[(int64_t)(SHDR + n + pos) * nsp], pack(eq, (uint32_t)((s0 + h * H + u) * SLOT + 4 * tid + e)));
+                st_sub<LOC>(&sub[(int64_t)(SHDR + n + pos) * nsp], pack(eq, (uint32_t)((s0 + h * H + u) * SLOT + 4 * tid + e)));
               pos++;
             }
           const int tot = (int)rdl((uint32_t)incl, 63);
@@ -1088,7 +1102,7 @@ XS_DEV double exp_f64(double x, TAB T) {
 // time, all 16 slots' loads in flight); wave 0 adds the partials of the
 // sub-records wholly before the argmax.  Then wave 0 writes row_lse and the
 // top-n log-probs.  Contains barriers: all waves of the workgroup call it.
-template <int NW>
+template <int NW, bool LOC>
 XS_DEV void held_fold(const Args& a, int row, const float* rowp, const uint64_t* rowrec, int nsp,
                       int nsub, FinLds& F) {
   HeldLds& H = F.held;
@@ -1109,10 +1123,10 @@ XS_DEV void held_fold(const Args& a, int row, const float* rowp, const uint64_t*
       const bool has = s < nsub;
       // (s < nsp: the words lie inside the row's record; loaded unguarded,
       // so that all go out at once, and dropped where !has)
-      const uint64_t h1 = ld_sub(&rowrec[1 * nsp + s]), h2 = ld_sub(&rowrec[2 * nsp + s]);
-      const uint64_t h3 = ld_sub(&rowrec[3 * nsp + s]), h4 = ld_sub(&rowrec[4 * nsp + s]);
-      const uint64_t h7 = ld_sub(&rowrec[7 * nsp + s]), h8 = ld_sub(&rowrec[8 * nsp + s]);
-      const uint64_t h9 = ld_sub(&rowrec[9 * nsp + s]);
+      const uint64_t h1 = ld_sub<LOC>(&rowrec[1 * nsp + s]), h2 = ld_sub<LOC>(&rowrec[2 * nsp + s]);
+      const uint64_t h3 = ld_sub<LOC>(&rowrec[3 * nsp + s]), h4 = ld_sub<LOC>(&rowrec[4 * nsp + s]);
+      const uint64_t h7 = ld_sub<LOC>(&rowrec[7 * nsp + s]), h8 = ld_sub<LOC>(&rowrec[8 * nsp + s]);
+      const uint64_t h9 = ld_sub<LOC>(&rowrec[9 * nsp + s]);
       const int c = s / NWAVE;
       const float mw = __uint_as_float((uint32_t)h3);
       const bool fold_data = ((h3 >> 32) & 8u) != 0;
@@ -1139,7 +1153,7 @@ XS_DEV void held_fold(const Args& a, int row, const float* rowp, const uint64_t*
         for (int j0 = 0; j0 < cnt; j0 += 8) {
           uint64_t e[8];  // (clamped inside the sub-record, not guarded: eight loads in flight)
 #pragma unroll
-          for (int u = 0; u < 8; u++) e[u] = ld_sub(&rowrec[(int64_t)(SHDR + min(j0 + u, CAPW - 1)) * nsp + s]);
+          for (int u = 0; u < 8; u++) e[u] = ld_sub<LOC>(&rowrec[(int64_t)(SHDR + min(j0 + u, CAPW - 1)) * nsp + s]);
 #pragma unroll
           for (int u = 0; u < 8; u++) {
             const float x = keyf(pk_key(e[u])) - m_v;
@@ -1268,6 +1282,7 @@ XS_DEV float at_lane(const float (&v)[R], int i) {  // element i of a list held 
 // sub-record whose entries past the preloaded EPRE may hold the answer, or
 // whose floor is unknown (+inf after an overflow), gives next_below(vL).  One
 // wave; E: sub-records 0..63's first EPRE entries, as load_heads read them.
+template <bool LOC>
 XS_DEV float below_selection(const uint64_t* rowrec, int nsp, int nsub, const uint64_t (&E)[EPRE], float vL) {
   const int lane = lane_id();
   float best = -INFINITY;
@@ -1275,11 +1290,11 @@ XS_DEV float below_selection(const uint64_t* rowrec, int nsp, int nsub, const ui
     const int s = g * 64 + lane;
     const bool live = s < nsub;
     const int sc = min(s, nsp - 1);  // (clamped, not guarded: the loads go out together)
-    const uint64_t h3 = ld_sub(&rowrec[3 * nsp + sc]), h4 = ld_sub(&rowrec[4 * nsp + sc]);
-    const uint64_t h7 = ld_sub(&rowrec[7 * nsp + sc]);
+    const uint64_t h3 = ld_sub<LOC>(&rowrec[3 * nsp + sc]), h4 = ld_sub<LOC>(&rowrec[4 * nsp + sc]);
+    const uint64_t h7 = ld_sub<LOC>(&rowrec[7 * nsp + sc]);
     uint64_t e[EPRE];
 #pragma unroll
-    for (int j = 0; j < EPRE; j++) e[j] = g == 0 ? E[j] : ld_sub(&rowrec[(SHDR + j) * nsp + sc]);
+    for (int j = 0; j < EPRE; j++) e[j] = g == 0 ? E[j] : ld_sub<LOC>(&rowrec[(SHDR + j) * nsp + sc]);
     const int cnt = live ? (int)min((uint32_t)h4, (uint32_t)CAPW) : 0;
     float mb = -INFINITY;
 #pragma unroll
@@ -1361,7 +1376,7 @@ XS_DEV bool draw_settled(const float (&c)[R], float tot, float x, int idx, int k
 // tie that needs the id-ordered row scan.  Returns false (having written
 // nothing) when the row is outside that case; the general finalizer then
 // does the row.  Same arithmetic, in the same order, as the general path.
-template <bool HAS_MASK, bool WANT_LSE>
+template <bool HAS_MASK, bool WANT_LSE, bool LOC>
 XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, int nsub, const uint64_t (&h)[NHW],
                      const uint64_t (&E)[EPRE], const uint64_t* rowrec, int nsp, const float* rowp,
                      FinLds& F, float S_ser) {
@@ -1451,7 +1466,7 @@ XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, int nsub, const uin
     uint64_t e[4];
 #pragma unroll
     for (int u = 0; u < 4; u++)  // (clamped inside the sub-record, not guarded: all four in flight)
-      e[u] = ld_sub(rowrec + (int64_t)(SHDR + min(j0 + u, CAPW - 1)) * nsp + lane);
+      e[u] = ld_sub<LOC>(rowrec + (int64_t)(SHDR + min(j0 + u, CAPW - 1)) * nsp + lane);
 #pragma unroll
     for (int u = 0; u < 4; u++) put(e[u], j0 + u < lim && e[u] >= floor_e);
     if (srt && j0 + 3 < lim && e[3] < floor_e) lim = j0;
@@ -1520,7 +1535,7 @@ XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, int nsub, const uin
       // a run of equal e across the top-k boundary: bounded below by the
       // row's actual next logit rather than next_below(vL)
       if (!cfg.full && nsel == kp && nsel > k && rdlf(ee, k - 1) == rdlf(ee, nsel - 1))
-        ebelow = exact_e(below_selection(rowrec, nsp, nsub, E, vL), cfg, m_s, T);
+        ebelow = exact_e(below_selection<LOC>(rowrec, nsp, nsub, E, vL), cfg, m_s, T);
       unsettled = !order_settled<1>(ea, nsel, kp, k, cfg.full, ebelow, S, cfg.dthr, want_cands);
     }
     // (p desc, id asc): p is non-increasing along the logit order, so only
@@ -1668,7 +1683,7 @@ XS_DEV bool fin_fast(const Args& a, const Cfg& cfg, int row, int nsub, const uin
 // controls, and probability ties at the top-k boundary.  Lane l handles
 // sub-records l + 64g; group 0's header words and first EPRE entries are the
 // ones finalize_row preloaded, the rest are read where they are used.
-template <bool HAS_MASK, bool WANT_LSE, bool HAS_CTL>
+template <bool HAS_MASK, bool WANT_LSE, bool HAS_CTL, bool LOC>
 XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* rowrec,
                         int nsp, int nsub, const float* rowp, const uint32_t* mrow, const CtlRow& cr,
                         const uint64_t (&h)[NHW], const uint64_t (&E)[EPRE], FinLds& F, float S_ser) {
@@ -1687,7 +1702,7 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
       for (int t = 1; t < NHW; t++) v = i == t ? h[t] : v;
       return has(0) ? v : 0ull;
     }
-    const uint64_t v = ld_sub(&rr[i * nsp + min(g * 64 + lane, nsp - 1)]);  // (clamped, not guarded)
+    const uint64_t v = ld_sub<LOC>(&rr[i * nsp + min(g * 64 + lane, nsp - 1)]);  // (clamped, not guarded)
     return has(g) ? v : 0ull;
   };
 
@@ -1797,7 +1812,7 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
       uint64_t e[4];
 #pragma unroll
       for (int u = 0; u < 4; u++)  // (clamped inside the sub-record, not guarded: all four in flight)
-        e[u] = ld_sub(rr + (int64_t)(SHDR + min(j + u, CAPW - 1)) * nsp + s);
+        e[u] = ld_sub<LOC>(rr + (int64_t)(SHDR + min(j + u, CAPW - 1)) * nsp + s);
 #pragma unroll
       for (int u = 0; u < 4; u++) put(e[u], j + u < lim && e[u] >= fl_e);
       if (srt && j + 3 < lim && e[3] < fl_e) lim = j;
@@ -1827,7 +1842,7 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
       for (int g = 0; g < GMAX; g++) {
         const int s = g * 64 + lane;
         const int n = has(g) ? (int)min((uint32_t)hdr(g, 4), (uint32_t)CAPW) : 0;
-        for (int j = 0; j < n; j++) c += ld_sub(rr + (int64_t)(SHDR + j) * nsp + s) >= cnd ? 1 : 0;
+        for (int j = 0; j < n; j++) c += ld_sub<LOC>(rr + (int64_t)(SHDR + j) * nsp + s) >= cnd ? 1 : 0;
       }
       if (wave_sumi(c) >= kp) ans = cnd;
     }
@@ -1909,7 +1924,7 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
       // a run of equal e across the top-k boundary: bounded below by the
       // row's actual next logit rather than next_below(vL)
       if (!cfg.full && nsel == kp && nsel > k && at_lane(ee, k - 1) == at_lane(ee, nsel - 1))
-        ebelow = exact_e(below_selection(rr, nsp, nsub, E, vL), cfg, m_s, T);
+        ebelow = exact_e(below_selection<LOC>(rr, nsp, nsub, E, vL), cfg, m_s, T);
       unsettled = !order_settled<2>(ee, nsel, kp, k, cfg.full, ebelow, S, cfg.dthr, want_cands);
     }
     bool bad = false;
@@ -2017,7 +2032,7 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
                 uint64_t e[4];
 #pragma unroll
                 for (int u = 0; u < 4; u++)  // (clamped inside the sub-record, not guarded)
-                  e[u] = ld_sub(rr + (int64_t)(SHDR + min(j + u, CAPW - 1)) * nsp + s);
+                  e[u] = ld_sub<LOC>(rr + (int64_t)(SHDR + min(j + u, CAPW - 1)) * nsp + s);
                 uint32_t hb = 0;  // bit u: entry j + u ties
 #pragma unroll
                 for (int u = 0; u < 4; u++) {
@@ -2404,15 +2419,15 @@ XS_DEV void fin_general(const Args& a, const Cfg cfg, int row, const uint64_t* r
 // sub-record `lane` per lane.  Every lane loads (its word lies inside the row's record: nsp >= 64),
 // and the lanes past nsub drop what they read: unguarded loads all go out at
 // once, where guarded ones were waited for in turn.
-template <bool WANT_LSE>
+template <bool WANT_LSE, bool LOC>
 XS_DEV void load_heads(const uint64_t* rowrec, int nsp, int nsub, uint64_t (&h)[NHW], uint64_t (&E)[EPRE]) {
   const int lane = lane_id();
   const bool live = lane < nsub;
 #pragma unroll
   for (int i = 0; i < NHW; i++)  // (word 2, the held_row partial, only when it is read)
-    h[i] = (i == 2 && !WANT_LSE) ? 0ull : ld_sub(&rowrec[(uint32_t)(i * nsp + lane)]);
+    h[i] = (i == 2 && !WANT_LSE) ? 0ull : ld_sub<LOC>(&rowrec[(uint32_t)(i * nsp + lane)]);
 #pragma unroll
-  for (int j = 0; j < EPRE; j++) E[j] = ld_sub(&rowrec[(uint32_t)((SHDR + j) * nsp + lane)]);
+  for (int j = 0; j < EPRE; j++) E[j] = ld_sub<LOC>(&rowrec[(uint32_t)((SHDR + j) * nsp + lane)]);
 #pragma unroll
   for (int i = 0; i < NHW; i++) h[i] = live ? h[i] : 0ull;
 #pragma unroll
@@ -2423,7 +2438,7 @@ XS_DEV void load_heads(const uint64_t* rowrec, int nsp, int nsub, uint64_t (&h)[
 // from the headers load_heads read.  For a speculative block the
 // row then takes its sequence's ticket, and the sequence's last finalized row
 // walks it (accept_drafts).
-template <bool HAS_MASK, bool WANT_LSE, bool HAS_CTL>
+template <bool HAS_MASK, bool WANT_LSE, bool HAS_CTL, bool LOC>
 XS_DEV void finalize_heads(const Args& a, const Cfg& cfg, int row, const uint64_t* rowrec, int nsp,
                            int nsub, const float* rowp, const uint32_t* mrow, FinLds& F,
                            const uint64_t (&h)[NHW], const uint64_t (&E)[EPRE], float S_ser = -1.0f) {
@@ -2431,17 +2446,17 @@ XS_DEV void finalize_heads(const Args& a, const Cfg& cfg, int row, const uint64_
   if (HAS_CTL) cr = a.ctl_row[row];
   if (lane_id() == 0) F.need_ser = 0;
   const bool done = !(HAS_CTL && cr.active) && nsub <= 64 && cfg.kp <= 64 && !cfg.bad && !cfg.big &&
-                    fin_fast<HAS_MASK, WANT_LSE>(a, cfg, row, nsub, h, E, rowrec, nsp, rowp, F, S_ser);
-  if (!done) fin_general<HAS_MASK, WANT_LSE, HAS_CTL>(a, cfg, row, rowrec, nsp, nsub, rowp, mrow, cr, h, E, F, S_ser);
+                    fin_fast<HAS_MASK, WANT_LSE, LOC>(a, cfg, row, nsub, h, E, rowrec, nsp, rowp, F, S_ser);
+  if (!done) fin_general<HAS_MASK, WANT_LSE, HAS_CTL, LOC>(a, cfg, row, rowrec, nsp, nsub, rowp, mrow, cr, h, E, F, S_ser);
 }
 
-template <bool HAS_MASK, bool WANT_LSE, bool HAS_CTL>
+template <bool HAS_MASK, bool WANT_LSE, bool HAS_CTL, bool LOC>
 XS_DEV void finalize_row(const Args& a, const Cfg& cfg, int row, const uint64_t* rowrec, int nsp,
                          int nsub, const float* rowp, const uint32_t* mrow, FinLds& F,
                          float S_ser = -1.0f) {
   uint64_t h[NHW], E[EPRE];
-  load_heads<WANT_LSE>(rowrec, nsp, nsub, h, E);
-  finalize_heads<HAS_MASK, WANT_LSE, HAS_CTL>(a, cfg, row, rowrec, nsp, nsub, rowp, mrow, F, h, E, S_ser);
+  load_heads<WANT_LSE, LOC>(rowrec, nsp, nsub, h, E);
+  finalize_heads<HAS_MASK, WANT_LSE, HAS_CTL, LOC>(a, cfg, row, rowrec, nsp, nsub, rowp, mrow, F, h, E, S_ser);
 }
 
 // The speculative walk: a finalized row of a verify block takes its sequence's
@@ -3049,7 +3064,7 @@ XS_DEV float ser_local(const Args& a, const Cfg& cfg, int row, float m_s, SerLoc
 // unsettled (F.need_ser), the wave sums the row's serial denominator
 // (ser_local) and finalizes the row again with it, which settles it by
 // construction.  Rows sent here are counted.
-template <bool HAS_MASK, bool WANT_LSE, bool HAS_CTL>
+template <bool HAS_MASK, bool WANT_LSE, bool HAS_CTL, bool LOC>
 XS_DEV void ser_fallback(const Args& a, const Cfg& cfg, int row, const uint64_t* rowrec, int nsp, int nsub,
                          const float* rowp, const uint32_t* mrow, TailLds& Tl) {
   wave_lds_sync();  // lane 0 wrote the verdict
@@ -3065,7 +3080,7 @@ XS_DEV void ser_fallback(const Args& a, const Cfg& cfg, int row, const uint64_t*
   const uint64_t* rr = rowrec;
   int np = __builtin_amdgcn_readfirstlane(nsp);
   asm volatile("" : "+s"(rr), "+s"(np));
-  finalize_row<HAS_MASK, WANT_LSE, HAS_CTL>(a, cfg, row, rr, np, nsub, rowp, mrow, Tl.fin, S_ser);
+  finalize_row<HAS_MASK, WANT_LSE, HAS_CTL, LOC>(a, cfg, row, rr, np, nsub, rowp, mrow, Tl.fin, S_ser);
 }
 
 // The row's arrival ticket counts its workgroups (bits 0-7; a row has at most
@@ -3080,27 +3095,35 @@ XS_DEV bool row_on_one_xcd(uint32_t total, int nc, uint32_t y) {
 }
 
 // ---------------------------------------------------------------------------
-// The kernel.  Grid: groups of n = 2^xcd_log2 rows x n_chunks workgroups of
-// BLOCK lanes (the row count rounded up to whole groups; workgroups past the
-// last row return at once); chunk c of a row covers slots [c*SPC, c*SPC +
-// SPC).  The hardware hands workgroup b of a launch to XCD b mod n (round
-// robin over the device's n XCDs, measured on every launch shape), so
-// workgroup (g*nc + c)*n + r takes chunk c of row g*n + r: all of a row's
-// workgroups run on one XCD.  Every wave reduces its own share of the chunk
-// and publishes it as one sub-record; the row's last workgroup to arrive (an
-// atomic ticket per row) finalizes the row with its first wave.
+// The kernel.  Grid (LOC, the XCD-local hand-off): groups of n = 2^xcd_log2
+// rows x n_chunks workgroups of BLOCK lanes (the row count rounded up to whole
+// groups; workgroups past the last row return at once); chunk c of a row
+// covers slots [c*SPC, c*SPC + SPC).  The hardware hands workgroup b of a
+// launch to XCD b mod n (round robin over the device's n XCDs, measured on
+// every launch shape), so workgroup (g*nc + c)*n + r takes chunk c of row
+// g*n + r: all of a row's workgroups run on one XCD.  Without LOC the grid is
+// row-major, rows x n_chunks, and a row's workgroups spread over the XCDs.
+// Every wave reduces its own share of the chunk and publishes it as one
+// sub-record; the row's last workgroup to arrive (an atomic ticket per row)
+// finalizes the row with its first wave.
 
-template <bool HAS_MASK, bool WANT_LSE, bool HAS_CTL, bool ORD>
+template <bool HAS_MASK, bool WANT_LSE, bool HAS_CTL, bool ORD, bool LOC>
 __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) void sample_kernel(Args a, RowOrder<ORD> ro) {
   __shared__ ChunkLds Lc;
   __shared__ TailLds Tl;
   const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
   const int nc = a.n_chunks;
-  const int gc = (int)(blockIdx.x >> a.xcd_log2);  // (group, chunk) of the workgroup
-  const int grp = gc / nc;
-  const int chunk = gc - grp * nc;
-  const int rb = (grp << a.xcd_log2) | (int)(blockIdx.x & ((1u << a.xcd_log2) - 1u));
-  if (rb >= a.nrows) return;  // the last group's padding
+  int rb, chunk;
+  if constexpr (LOC) {
+    const int gc = (int)(blockIdx.x >> a.xcd_log2);  // (group, chunk) of the workgroup
+    const int grp = gc / nc;
+    chunk = gc - grp * nc;
+    rb = (grp << a.xcd_log2) | (int)(blockIdx.x & ((1u << a.xcd_log2) - 1u));
+    if (rb >= a.nrows) return;  // the last group's padding
+  } else {  // row-major, no padding
+    rb = blockIdx.x / nc;
+    chunk = blockIdx.x - rb * nc;
+  }
   int row = rb;
   if constexpr (ORD) row = ro.v[rb];
   const int enc = (int)a.enc;
@@ -3510,7 +3533,7 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
     }
     if (cnt > CAPW) {  // the exact re-scan writes its entries straight to the sub-record
       const ChunkCtl cc{pl, pc0, phi, ctl_pull, ctl_force, ctl_pval, ctl_fval};
-      cnt = wave_overflow<HAS_MASK, HAS_CTL>(rowp, mrow, s0, ns, enc, sub, nsp, kp, tk, cc);
+      cnt = wave_overflow<HAS_MASK, HAS_CTL, LOC>(rowp, mrow, s0, ns, enc, sub, nsp, kp, tk, cc);
       ovf = true;
     }
   }
@@ -3550,7 +3573,7 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
       v = i == 8 ? hw8 : v;
       v = i == 9 ? hw9 : v;
       if (i >= SHDR) v = stg[i - SHDR];
-      st_sub(sub + (uint32_t)i * (uint32_t)nsp, v);
+      st_sub<LOC>(sub + (uint32_t)i * (uint32_t)nsp, v);
     }
   }
 
@@ -3565,12 +3588,12 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
   if (tid == 0) {
     // (xcd_test 2 flips the low bit of the XCD the odd chunks report: a row
     // of several chunks then fails the placement check, a test hook)
-    const uint32_t x = xcc_id() ^ ((a.xcd_test == 2) ? (uint32_t)(chunk & 1) : 0u);
-    const uint32_t add = row_ticket_add(x);
+    const uint32_t x = LOC ? xcc_id() ^ ((a.xcd_test == 2) ? (uint32_t)(chunk & 1) : 0u) : 0u;
+    const uint32_t add = LOC ? row_ticket_add(x) : 1u;
     const uint32_t t = (uint32_t)__hip_atomic_fetch_add(&a.row_ticket[row * TSTRIDE], (int32_t)add, __ATOMIC_RELAXED,
                                                         __HIP_MEMORY_SCOPE_AGENT);
     const bool lastw = (int)(t & 0xFFu) == nc - 1;
-    Lc.last = lastw ? (row_on_one_xcd(t + add, nc, x) ? 1 : 2) : 0;
+    Lc.last = lastw ? ((!LOC || row_on_one_xcd(t + add, nc, x)) ? 1 : 2) : 0;
     if (lastw) {
       st_agent(&a.row_ticket[row * TSTRIDE], 0);
       st_agent(&a.row_ticket[row * TSTRIDE + 1], 0);  // held_row's running max key
@@ -3590,11 +3613,11 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
   // sub-records outside this L2: it is failed, not read, and its sequence's
   // walk stops at it.
   if (wave != 0) return;
-  const bool placed = Lc.last == 1;
+  const bool placed = !LOC || Lc.last == 1;
   if (placed) {
-    finalize_row<HAS_MASK, WANT_LSE, HAS_CTL>(a, cfg, row, rowrec, nsp, nc * NWAVE, rowp, mrow, Tl.fin);
-    if (HAS_MASK || HAS_CTL) ser_fallback<HAS_MASK, WANT_LSE, HAS_CTL>(a, cfg, row, rowrec, nsp, nc * NWAVE, rowp, mrow, Tl);
-    if (held) held_fold<1>(a, row, rowp, rowrec, nsp, nc * NWAVE, Tl.fin);
+    finalize_row<HAS_MASK, WANT_LSE, HAS_CTL, LOC>(a, cfg, row, rowrec, nsp, nc * NWAVE, rowp, mrow, Tl.fin);
+    if (HAS_MASK || HAS_CTL) ser_fallback<HAS_MASK, WANT_LSE, HAS_CTL, LOC>(a, cfg, row, rowrec, nsp, nc * NWAVE, rowp, mrow, Tl);
+    if (held) held_fold<1, LOC>(a, row, rowp, rowrec, nsp, nc * NWAVE, Tl.fin);
   } else if (lane == 0) {
     st_agent(&a.token[row], -1);
     st_agent(&a.status[row], XS_ROW_INTERNAL);
@@ -3622,16 +3645,16 @@ __global__ __launch_bounds__(BLOCK) void finalize_kernel(Args a) {
   const uint64_t* const rowrec = a.rec + (int64_t)row * SRECW * nsp;
   // the row's headers first: their round trip overlaps the row's parameters
   uint64_t h[NHW], E[EPRE];
-  load_heads<WANT_LSE>(rowrec, nsp, nc * NWAVE, h, E);
+  load_heads<WANT_LSE, true>(rowrec, nsp, nc * NWAVE, h, E);
   const Cfg cfg = a.greedy_all ? greedy_cfg() : make_cfg(a.params[row], a.enc, a.n_top, a.k_max, a.ser_force);
   if (threadIdx.x == 0) st_agent(&a.row_ticket[row * TSTRIDE + 1], 0);  // held_row's running max key
   if (a.serial && serial_row<HAS_MASK, HAS_CTL>(a, cfg, row)) return;  // serial_kernel finalizes it
   const float* rowp = a.logits + (int64_t)row * a.ld;
   const uint32_t* mrow = HAS_MASK ? a.allowed + (int64_t)row * a.allowed_ld : nullptr;
   const bool held = WANT_LSE && (a.row_lse != nullptr || a.n_top > 0);
-  finalize_heads<HAS_MASK, WANT_LSE, HAS_CTL>(a, cfg, row, rowrec, nsp, nc * NWAVE, rowp, mrow, Tl.fin, h, E);
-  if (HAS_MASK || HAS_CTL) ser_fallback<HAS_MASK, WANT_LSE, HAS_CTL>(a, cfg, row, rowrec, nsp, nc * NWAVE, rowp, mrow, Tl);
-  if (held) held_fold<1>(a, row, rowp, rowrec, nsp, nc * NWAVE, Tl.fin);
+  finalize_heads<HAS_MASK, WANT_LSE, HAS_CTL, true>(a, cfg, row, rowrec, nsp, nc * NWAVE, rowp, mrow, Tl.fin, h, E);
+  if (HAS_MASK || HAS_CTL) ser_fallback<HAS_MASK, WANT_LSE, HAS_CTL, true>(a, cfg, row, rowrec, nsp, nc * NWAVE, rowp, mrow, Tl);
+  if (held) held_fold<1, true>(a, row, rowp, rowrec, nsp, nc * NWAVE, Tl.fin);
   if (a.span > 0 && !deferred(cfg, Tl.fin)) verify_walk(a, row);
 }
 
@@ -4056,7 +4079,7 @@ __global__ __launch_bounds__(BLOCK) void serial_kernel(Args a) {
     S_ser = __uint_as_float(sb);
   }
   if (wave != 0) return;
-  finalize_row<HAS_MASK, false, HAS_CTL>(a, cfg, row, rowrec, nsp, nsub, rowp, mrow, St.tl.fin, S_ser);
+  finalize_row<HAS_MASK, false, HAS_CTL, true>(a, cfg, row, rowrec, nsp, nsub, rowp, mrow, St.tl.fin, S_ser);
   if (a.span > 0 && !deferred(cfg, St.tl.fin)) verify_walk(a, row);
 }
 
@@ -5062,7 +5085,7 @@ struct xs_context {
   int32_t max_chunks;
   int32_t n_cu;         // compute units of the device
   int32_t xcd;          // the device's XCDs, whose round-robin placement sample_kernel's grid
-                        // follows; 0: the placement was not confirmed, every call takes the split launch
+                        // follows; 0: the placement was not confirmed, no call hands off XCD-locally
   int32_t xcd_test;     // test hook: 1 the split launch, 2 the placement check fails (odd chunks report another XCD)
   uint64_t* rec;
   int32_t* row_status;  // [max_rows] statuses of calls whose caller takes none (xs_argmax_probs)
@@ -5123,21 +5146,24 @@ int xcd_placement(int device) {
 // one that can observe the serial denominator serial_kernel after them, and a
 // context sized for top_k >= 128 the whole-row kernels last.
 template <bool M, bool S, bool C>
-void launch2(xs_context* ctx, xs::Args& a, int64_t rows, dim3 g1, dim3 gs, const int32_t* order) {
+void launch2(xs_context* ctx, xs::Args& a, int64_t rows, dim3 g1, dim3 gs, const int32_t* order, bool loc) {
   // More workgroups than the GPU holds at once (4 per CU): the split launch,
   // unless the rows carry held_row statistics or a cost order -- their long
   // finalizers then overlap the later rows' streaming inside one launch (C5:
   // 75 us in one launch, 91 us split; C4: 57.2 us in one, 55.4 us split).
-  // A context whose XCD placement was not confirmed always splits: the
-  // launch boundary, not one XCD's L2, then orders the sub-records.
-  a.split = ((g1.x > (unsigned)(4 * ctx->n_cu) && !S && !order) || ctx->xcd == 0 || ctx->xcd_test == 1) ? 1 : 0;
+  a.split = ((g1.x > (unsigned)(4 * ctx->n_cu) && !S && !order) || ctx->xcd_test == 1) ? 1 : 0;
   if (C) hipLaunchKernelGGL((xs::control_kernel<M>), dim3((unsigned)rows), dim3(xs::BLOCK), 0, ctx->stream, a);
-  if (order) {
+  // (a call of fewer rows than XCDs drops its row order: its rows all start
+  // at once, and outputs do not depend on the order)
+  if (order && loc) {
     xs::RowOrder<true> ro;
     for (int64_t i = 0; i < rows; i++) ro.v[i] = (uint16_t)order[i];
-    hipLaunchKernelGGL((xs::sample_kernel<M, S, C, true>), gs, dim3(xs::BLOCK), 0, ctx->stream, a, ro);
+    hipLaunchKernelGGL((xs::sample_kernel<M, S, C, true, true>), gs, dim3(xs::BLOCK), 0, ctx->stream, a, ro);
+  } else if (loc) {
+    hipLaunchKernelGGL((xs::sample_kernel<M, S, C, false, true>), gs, dim3(xs::BLOCK), 0, ctx->stream, a,
+                       xs::RowOrder<false>{});
   } else {
-    hipLaunchKernelGGL((xs::sample_kernel<M, S, C, false>), gs, dim3(xs::BLOCK), 0, ctx->stream, a,
+    hipLaunchKernelGGL((xs::sample_kernel<M, S, C, false, false>), gs, dim3(xs::BLOCK), 0, ctx->stream, a,
                        xs::RowOrder<false>{});
   }
   if (a.split) hipLaunchKernelGGL((xs::finalize_kernel<M, S, C>), dim3((unsigned)rows), dim3(xs::BLOCK), 0, ctx->stream, a);
@@ -5168,8 +5194,15 @@ int launch(xs_context* ctx, xs::Args& a, int64_t rows, int span, bool mask, bool
   const bool ctl = a.controls != nullptr;
   const int64_t grid = rows * (int64_t)a.n_chunks;
   if (grid == 0) return XS_OK;
-  // sample_kernel's grid: whole groups of xcd rows (all workgroups of a row on one XCD)
-  const int nx = ctx->xcd > 0 ? ctx->xcd : 1;
+  // sample_kernel's grid: whole groups of xcd rows, all workgroups of a row on
+  // one XCD (the XCD-local hand-off), when the context confirmed the placement
+  // and the call has at least 8 rows per XCD; otherwise row-major, each row
+  // spread over every XCD, handing off through memory.  (Measured: C2's 64
+  // rows 19.58 -> 19.12 us, C4 54.2 -> 49.2, C5 71.8 -> 67.4 with it; C3's 32
+  // masked rows 16.94 -> 17.45 and a lone row, through one XCD's share of
+  // the bandwidth, 8.86 -> 9.28 us greedy.)
+  const bool loc = ctx->xcd > 0 && rows >= 8 * (int64_t)ctx->xcd;
+  const int nx = loc ? ctx->xcd : 1;
   a.xcd_log2 = __builtin_ctz((unsigned)nx);
   a.nrows = (int32_t)rows;
   a.xcd_test = ctx->xcd_test;
@@ -5202,11 +5235,11 @@ int launch(xs_context* ctx, xs::Args& a, int64_t rows, int span, bool mask, bool
   a.ser_e = ctx->ser_e;
   a.ser_ld = (int64_t)ctx->max_chunks * xs::SPC * xs::NWAVE;
   const dim3 g1((unsigned)grid), gs((unsigned)gpad);
-  if (ctl && mask) launch2<true, false, true>(ctx, a, rows, g1, gs, order);
-  else if (ctl) launch2<false, false, true>(ctx, a, rows, g1, gs, order);
-  else if (mask) launch2<true, false, false>(ctx, a, rows, g1, gs, order);
-  else if (lse) launch2<false, true, false>(ctx, a, rows, g1, gs, order);
-  else launch2<false, false, false>(ctx, a, rows, g1, gs, order);
+  if (ctl && mask) launch2<true, false, true>(ctx, a, rows, g1, gs, order, loc);
+  else if (ctl) launch2<false, false, true>(ctx, a, rows, g1, gs, order, loc);
+  else if (mask) launch2<true, false, false>(ctx, a, rows, g1, gs, order, loc);
+  else if (lse) launch2<false, true, false>(ctx, a, rows, g1, gs, order, loc);
+  else launch2<false, false, false>(ctx, a, rows, g1, gs, order, loc);
   return hipGetLastError() == hipSuccess ? XS_OK : XS_ERR_HIP;
 }
 
@@ -5415,7 +5448,7 @@ int na_cus(int dev) {  // the device's compute units, asked once
 
 // The device's XCD count, asked once (no probe launch: this entry point may
 // run under graph capture; sample_kernel checks each row's placement), or 0
-// when the device does not report one: every call then takes the split launch.
+// when the device does not report one: no call then hands off XCD-locally.
 int na_xcd[NA_MAX_DEVICES];
 bool na_xcd_known[NA_MAX_DEVICES];
 int na_xcds(int dev) {

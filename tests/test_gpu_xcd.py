@@ -113,6 +113,17 @@ def test_split_launch_gives_identical_outputs(ctx):
         print(f"{tag}: identical in both launches; statuses {np.unique(a['status']).tolist()}")
         same_bits(a, b, tag)
         assert (a["status"] != 8).all(), tag
+    # controlled rows at top_p 1 with candidates: serial_kernel sums and
+    # finalizes them after sample_kernel's XCD-local launch
+    c3w = workloads.c3_masked(seed=323, rows=72)
+    c3w.top_p = np.full(72, 1.0)
+    kw = dict(allowed=dev(c3w.mask.view(np.int32)), cand_k=20, stats=True)
+    set_mode(ctx, 0)
+    a = draw(ctx, c3w, None, **kw)
+    set_mode(ctx, 1)
+    b = draw(ctx, c3w, None, **kw)
+    set_mode(ctx, 0)
+    same_bits(a, b, "C3 72 masked rows at top_p 1 (serial denominator)")
     # a verify block small enough for one launch (64 rows)
     c4 = workloads.c4_verify(seqs=4)
     got = []
@@ -121,6 +132,28 @@ def test_split_launch_gives_identical_outputs(ctx):
         got.append(verify(ctx, c4))
         set_mode(ctx, 0)
     same_bits(got[0], got[1], "C4 4 x 16 verify block")
+
+
+def test_whole_row_rows_in_an_xcd_local_call():
+    """64 rows at top_k 500 (the whole-row kernels draw them after the
+    finalizers defer them) give the same outputs handed off XCD-locally and
+    in the split launch."""
+    from xwen_amd import sampler as xsm
+    c = xsm.Context(max_rows=64, vocab=V, k_max=2**31 - 1)
+    c.bind_current_stream()
+    try:
+        wl = workloads.c2_batch(seed=212)
+        wl.top_k = np.full(64, 500)
+        got = []
+        for mode in (0, 1):
+            set_mode(c, mode)
+            got.append(draw(c, wl, None, cand_k=20, stats=True))
+        set_mode(c, 0)
+        same_bits(got[0], got[1], "64 rows at top_k 500")
+        assert (got[0]["status"] == 0).all()
+        assert (got[0]["n_cand"] == 500).all()
+    finally:
+        c.close()
 
 
 def verify(ctx, c4):

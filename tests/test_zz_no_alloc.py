@@ -49,12 +49,13 @@ def test_noalloc_matches_xs_sample_on_two_calls_in_a_row():
     ctx = xsm.Context(max_rows=64, vocab=V)
     ctx.bind_current_stream()
 
-    # first call: 48 rows of the batch-64 configuration at full width
-    wl = workloads.c2_batch(rows=48)
+    # first call: the batch-64 configuration at full width (64 rows: the
+    # XCD-local hand-off)
+    wl = workloads.c2_batch()
     lg = torch.as_tensor(wl.logits).cuda()
-    p = xsm.params_tensor(wl.temperature, wl.top_k, wl.top_p, 48, "cuda")
+    p = xsm.params_tensor(wl.temperature, wl.top_k, wl.top_p, 64, "cuda")
     u = torch.as_tensor(wl.u).cuda()
-    print("noalloc call 1: 48 x 248320", flush=True)
+    print("noalloc call 1: 64 x 248320", flush=True)
     got = xsm.sample_batch_noalloc(lg, p, u, cand_k=20, stats=True)
     want = xsm.sample_batch(ctx, lg, p, u, cand_k=20, stats=True)
     torch.cuda.synchronize()

@@ -3077,7 +3077,11 @@ XS_DEV void ser_fallback(const Args& a, const Cfg& cfg, int row, const uint64_t*
   // the compiler forms this finalize_row's addresses afresh instead of
   // keeping the first one's live across it (18 such registers spilled to
   // scratch in the masked and controlled kernels).
-  const uint64_t* rr = rowrec;
+  // (both made uniform first, so the scalar-register constraint always holds)
+  const uint64_t ra = reinterpret_cast<uint64_t>(rowrec);
+  const uint64_t* rr = reinterpret_cast<const uint64_t*>(
+      ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(ra >> 32)) << 32) |
+      (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)ra));
   int np = __builtin_amdgcn_readfirstlane(nsp);
   asm volatile("" : "+s"(rr), "+s"(np));
   finalize_row<HAS_MASK, WANT_LSE, HAS_CTL, LOC>(a, cfg, row, rr, np, nsub, rowp, mrow, Tl.fin, S_ser);

@@ -212,9 +212,11 @@ typedef struct {
    * Listing the rows with the costliest finalization first (top_k above 63,
    * held_row statistics, sparse controls) lets their long finalizers overlap
    * the other rows' streaming instead of ending the launch.  Outputs are the
-   * same in any order.  rows <= XS_ORDER_MAX; not a permutation is
-   * XS_ERR_ARG.  No counterpart in the reference, which samples one row at a
-   * time. */
+   * same in any order.  Not a permutation is XS_ERR_ARG; the order of a call
+   * of more than XS_ORDER_MAX rows is checked and not applied (its rows start
+   * in their natural order), and neither is that of a call of fewer than 8
+   * rows per XCD.  No counterpart in the reference, which samples one row at
+   * a time. */
   const int32_t* row_order;
   /* A bound on min(top_k, enc) for this call, or 0 for the context's k_max:
    * rows above it report XS_ROW_BAD_PARAM, and a bound of XS_K_MAX or less

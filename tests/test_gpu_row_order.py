@@ -81,15 +81,23 @@ def test_bad_orders_are_argument_errors(ctx):
     for order in ([0, 1, 2], list(range(9))):
         with pytest.raises(ValueError):
             xsm.sample_batch(ctx, lg, p, u, order=order)
-    # more rows than an order may list
+    # more rows than a launch's order table holds
     n = _lib.ORDER_MAX + 1
     big = xsm.Context(max_rows=n, vocab=1024)
     big.bind_current_stream()
     x = torch.zeros((n, 1024), dtype=torch.float32, device="cuda")
     pb = xsm.params_tensor(1.0, 20, 0.9, n, "cuda")
     ub = torch.zeros(n, dtype=torch.float32, device="cuda")
+    # past ORDER_MAX rows an order is checked, then not applied: the natural
+    # order's draws, and a non-permutation is still an error
+    want = xsm.sample_batch(big, x, pb, ub, cand_k=20)
+    got = xsm.sample_batch(big, x, pb, ub, cand_k=20, order=np.arange(n)[::-1].copy())
+    torch.cuda.synchronize()
+    assert torch.equal(got.token, want.token) and torch.equal(got.cand_id, want.cand_id)
+    bad = np.arange(n)
+    bad[5] = 4
     with pytest.raises(_lib.XsError):
-        xsm.sample_batch(big, x, pb, ub, order=np.arange(n))
+        xsm.sample_batch(big, x, pb, ub, order=bad)
     torch.cuda.synchronize()
     big.close()
 

@@ -100,7 +100,12 @@ def test_row_order_must_be_a_permutation(host):
     assert chk([3, 1, 0, 2]) == OK
     assert chk([3, 1, 1, 2]) == E and chk([0, 1, 2, 4]) == E and chk([0, -1, 2, 3]) == E
     assert chk(np.arange(_lib.ORDER_MAX), rows=_lib.ORDER_MAX) == OK
-    assert chk(np.arange(_lib.ORDER_MAX + 1), rows=_lib.ORDER_MAX + 1) == E
+    # past ORDER_MAX rows the order is checked, then not applied
+    big = np.arange(_lib.ORDER_MAX + 1)[::-1]
+    assert chk(big, rows=_lib.ORDER_MAX + 1) == OK
+    big = big.copy()
+    big[7] = big[8]
+    assert chk(big, rows=_lib.ORDER_MAX + 1) == E
 
 
 def test_verify_and_argmax_argument_checks(host):

@@ -64,9 +64,14 @@ int xs_host_check_sample(const xs_host_limits* lim, const xs_sample_args* in) {
   if (in->probs && in->probs_ld < in->enc) return XS_ERR_ARG;
   const bool lse = xs_host_wants_lse(in);
   if (lse && (in->allowed || in->controls)) return XS_ERR_ARG;
-  if (in->row_order) {  // a permutation of 0..rows-1
-    if (in->rows > XS_ORDER_MAX) return XS_ERR_ARG;
-    uint64_t seen[XS_ORDER_MAX / 64] = {};
+  if (in->row_order) {  // a permutation of 0..rows-1 (a longer one is checked, then not applied)
+    uint64_t small[XS_ORDER_MAX / 64] = {};
+    std::vector<uint64_t> large;
+    uint64_t* seen = small;
+    if (in->rows > XS_ORDER_MAX) {
+      large.assign((size_t)((in->rows + 63) / 64), 0ull);
+      seen = large.data();
+    }
     for (int64_t i = 0; i < in->rows; i++) {
       const int32_t r = in->row_order[i];
       if (r < 0 || r >= in->rows || ((seen[r >> 6] >> (r & 63)) & 1u)) return XS_ERR_ARG;

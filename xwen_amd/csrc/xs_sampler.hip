@@ -5425,7 +5425,9 @@ int sample_impl(xs_context* ctx, const xs_sample_args* in, bool clear_tickets) {
   // and a row whose token that sum does not settle is summed serially by its
   // finalizer (draw_settled, ser_local)
   const bool serial = in->cand_id || in->cand_w || in->soft_sum;
-  const int lrc = launch(ctx, a, in->rows, 1, in->allowed != nullptr, lse, serial, in->row_order);
+  // (the launch's arguments carry an order of at most XS_ORDER_MAX rows)
+  const int32_t* order = in->rows <= XS_ORDER_MAX ? in->row_order : nullptr;
+  const int lrc = launch(ctx, a, in->rows, 1, in->allowed != nullptr, lse, serial, order);
   if (lrc != XS_OK || !scores || in->rows == 0) return lrc;
   // the scoring reads, once every row's lse is written
   hipLaunchKernelGGL(xs::score_kernel, dim3((unsigned)(in->rows * a.n_chunks)), dim3(xs::BLOCK), 0, ctx->stream, a);

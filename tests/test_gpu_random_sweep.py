@@ -3,7 +3,9 @@ several scales, Student-t, tall peaks over a bulk, values quantized so that
 exact ties are common, all-negative ties, Gumbel), random T / top_k / top_p
 per row (greedy rows, K' across the fast and general finalizers), some with
 random allow-masks, at three row widths; every row held to the oracle by the
-same bar as the configured cases."""
+same bar as the configured cases.  Batches of 24 rows spread each row over
+the XCDs; batches of 72 (8 rows per XCD and more, a padded last group) take
+the XCD-local hand-off."""
 import numpy as np
 import pytest
 
@@ -25,10 +27,20 @@ def ctx():
     c.close()
 
 
-def _batch(b):
+@pytest.fixture(scope="module")
+def ctx72():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from xwen_amd import sampler as xsm
+    c = xsm.Context(max_rows=72, vocab=workloads.V)
+    c.bind_current_stream()
+    yield c
+    c.close()
+
+
+def _batch(b, rows=24):
     rng = np.random.default_rng(90_000 + b)
     v = int(rng.choice([4096, 65536, 248320]))
-    rows = 24
     kind = b % 6
     if kind == 0:
         x = rng.normal(0, rng.choice([0.5, 1, 3, 8]), (rows, v))
@@ -65,11 +77,17 @@ def test_random_batch(ctx, oracle, b):
     check_rows(oracle, x, T, K, P, U, d, mask=mask, label=label)
 
 
-def _control_batch(b):
+@pytest.mark.parametrize("b", range(6))
+def test_random_batch_xcd_local(ctx72, oracle, b):
+    x, T, K, P, U, mask, label = _batch(200 + b, rows=72)
+    d = run_sample(ctx72, x, T, K, P, U, mask=mask)
+    check_rows(oracle, x, T, K, P, U, d, mask=mask, label=label + " (72 rows)")
+
+
+def _control_batch(b, rows=24):
     from xwen_amd import sampler as xsm
     rng = np.random.default_rng(70_000 + b)
     v = int(rng.choice([4096, 65536, 248320]))
-    rows = 24
     x = rng.standard_t(3, (rows, v)) * 2 if b % 2 else rng.normal(0, 3, (rows, v))
     if b % 3 == 2:
         x = np.round(x * 2) / 2
@@ -106,6 +124,14 @@ def test_random_controls_batch(ctx, oracle, b):
     x, T, K, P, U, ctls, mask, label = _control_batch(b)
     d = run_sample(ctx, x, T, K, P, U, ctls=ctls, mask=mask)
     check_rows(oracle, x, T, K, P, U, d, ctls=ctls, mask=mask, label=label)
+
+
+@pytest.mark.parametrize("b", range(3))
+def test_random_controls_batch_xcd_local(ctx72, oracle, b):
+    """The same random controls over 72 rows (the XCD-local hand-off)."""
+    x, T, K, P, U, ctls, mask, label = _control_batch(100 + b, rows=72)
+    d = run_sample(ctx72, x, T, K, P, U, ctls=ctls, mask=mask)
+    check_rows(oracle, x, T, K, P, U, d, ctls=ctls, mask=mask, label=label + " (72 rows)")
 
 
 @pytest.mark.parametrize("b", range(8))

@@ -28,11 +28,11 @@ def ctx():
 
 
 @pytest.fixture(scope="module")
-def ctx72():
+def ctx_wide():
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
     from xwen_amd import sampler as xsm
-    c = xsm.Context(max_rows=72, vocab=workloads.V)
+    c = xsm.Context(max_rows=128, vocab=workloads.V)
     c.bind_current_stream()
     yield c
     c.close()
@@ -78,9 +78,9 @@ def test_random_batch(ctx, oracle, b):
 
 
 @pytest.mark.parametrize("b", range(6))
-def test_random_batch_xcd_local(ctx72, oracle, b):
+def test_random_batch_xcd_local(ctx_wide, oracle, b):
     x, T, K, P, U, mask, label = _batch(200 + b, rows=72)
-    d = run_sample(ctx72, x, T, K, P, U, mask=mask)
+    d = run_sample(ctx_wide, x, T, K, P, U, mask=mask)
     check_rows(oracle, x, T, K, P, U, d, mask=mask, label=label + " (72 rows)")
 
 
@@ -127,10 +127,10 @@ def test_random_controls_batch(ctx, oracle, b):
 
 
 @pytest.mark.parametrize("b", range(3))
-def test_random_controls_batch_xcd_local(ctx72, oracle, b):
+def test_random_controls_batch_xcd_local(ctx_wide, oracle, b):
     """The same random controls over 72 rows (the XCD-local hand-off)."""
     x, T, K, P, U, ctls, mask, label = _control_batch(100 + b, rows=72)
-    d = run_sample(ctx72, x, T, K, P, U, ctls=ctls, mask=mask)
+    d = run_sample(ctx_wide, x, T, K, P, U, ctls=ctls, mask=mask)
     check_rows(oracle, x, T, K, P, U, d, ctls=ctls, mask=mask, label=label + " (72 rows)")
 
 
@@ -140,9 +140,22 @@ def test_random_verify_block(ctx, oracle, b):
     the row's argmax, its sampled token or a random id, random budgets (0
     included) and EOG ids taken from the sampled tokens; the walk must equal
     accept_drafts (src/generate.rs:4020-4046) over the same row tokens."""
-    from xwen_amd import sampler as xsm
     rng = np.random.default_rng(50_000 + b)
-    seqs, span = int(rng.integers(1, 9)), int(rng.integers(1, 9))
+    _verify_block(ctx, oracle, rng, int(rng.integers(1, 9)), int(rng.integers(1, 9)), b)
+
+
+@pytest.mark.parametrize("b", range(4))
+def test_random_verify_block_xcd_local(ctx_wide, oracle, b):
+    """The same over blocks of 64-128 rows (spans 4-16), whose rows hand off
+    XCD-locally and whose sequences are walked by the last row's finalizer."""
+    rng = np.random.default_rng(51_000 + b)
+    span = int(rng.integers(4, 17))
+    seqs = int(rng.integers(-(-64 // span), 128 // span + 1))
+    _verify_block(ctx_wide, oracle, rng, seqs, span, b)
+
+
+def _verify_block(ctx, oracle, rng, seqs, span, b):
+    from xwen_amd import sampler as xsm
     rows, v = seqs * span, int(rng.choice([4096, 65536, 248320]))
     x = (rng.normal(0, 3, (rows, v)) if b % 2 else rng.standard_t(3, (rows, v)) * 2).astype(np.float32)
     T = rng.choice([0.0, 0.7, 1.0], rows)

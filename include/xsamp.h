@@ -193,9 +193,11 @@ typedef struct {
   int64_t cand_ld;       /* >= min(top_k, enc) of every row that writes candidates */
   float* soft_max;       /* [rows] max of the scaled, controlled row, or NULL */
   float* soft_sum;       /* [rows] softmax denominator used, or NULL */
-  /* held_row statistics over the raw logits (generate.rs:1905-1933), no
-   * allow-mask allowed with these: row_max, ln-sum-exp in f64, and the n_top
-   * highest logits (ties to the lower id) as log-probs v - lse. */
+  /* held_row statistics over the raw logits (generate.rs:1905-1933):
+   * row_max, ln-sum-exp in f64, and the n_top highest logits (ties to the
+   * lower id) as log-probs v - lse.  They ignore the allow-mask and the
+   * controls, as held_row reads the raw row; a call with either makes a
+   * second pass over its rows for them. */
   float* row_max;        /* [rows] or NULL */
   double* row_lse;       /* [rows] or NULL (NaN where held_row errors) */
   int32_t n_top;         /* 0..XS_TOP_MAX */
@@ -203,7 +205,7 @@ typedef struct {
   float* top_logprob;    /* [rows, top_ld] or NULL */
   int64_t top_ld;
   /* SampleControl's bans, biases, pull and force (see xs_row_control), or
-   * controls = NULL for none.  Not combinable with the held_row outputs. */
+   * controls = NULL for none. */
   const xs_row_control* controls; /* [rows] */
   const uint32_t* ctl_ids;        /* banned and bias ids of every row */
   const float* ctl_delta;         /* bias deltas, indexed as ctl_ids */
@@ -226,9 +228,9 @@ typedef struct {
    * largest min(top_k, enc) among them. */
   int32_t k_max;
   /* Scoring reads of the held row (generate.rs:1871-1899, batch.rs:1504-1521,
-   * :1628-1669), normalized by the same f64 lse as row_lse; the held_row
-   * outputs' rules apply (no allow-mask, no controls), and each may be asked
-   * for alone (lse is then computed without being written).  Not available
+   * :1628-1669), normalized by the same f64 lse as row_lse, over the raw row
+   * as the held_row outputs are; each may be asked for alone (lse is then
+   * computed without being written).  Not available
    * through xs_sample_noalloc (XS_ERR_ARG). */
   double* top_logprob64;          /* [rows, top_ld] the n_top log-probs in f64, or NULL */
   const int32_t* score_ids;       /* [rows, score_ld] ids to score, or NULL (last_logprobs_for) */

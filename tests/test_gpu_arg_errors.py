@@ -34,8 +34,6 @@ def setup():
         "mask": torch.full((ROWS, WIDTH // 32), -1, dtype=torch.int32, device="cuda"),
         "top": torch.empty((ROWS, 8), dtype=torch.int32, device="cuda"),
         "lp": torch.empty((ROWS, 8), dtype=torch.float32, device="cuda"),
-        "rmax": torch.empty(ROWS, dtype=torch.float32, device="cuda"),
-        "rlse": torch.empty(ROWS, dtype=torch.float64, device="cuda"),
         "prob": torch.empty(ROWS, dtype=torch.float32, device="cuda"),
     }
     yield ctx, t
@@ -90,10 +88,6 @@ def test_valid_call_then_every_broken_field(setup):
     assert broken(n_top=_lib.TOP_MAX + 1) == E
     assert broken(n_top=8, top_id=t["top"].data_ptr(), top_logprob=t["lp"].data_ptr(),
                   top_ld=4) == E                            # top_ld < n_top
-    # held_row statistics cannot be combined with an allow-mask
-    assert broken(row_max=t["rmax"].data_ptr(), row_lse=t["rlse"].data_ptr(),
-                  allowed=t["mask"].data_ptr(), allowed_words=WIDTH // 32,
-                  allowed_ld=WIDTH // 32) == E
     assert broken(allowed=t["mask"].data_ptr(), allowed_words=WIDTH // 32,
                   allowed_ld=WIDTH // 32 - 1) == E          # allowed_ld < allowed_words
 

@@ -65,8 +65,9 @@ def test_sample_argument_checks(host):
     assert chk(cand_id=DEV, cand_ld=0) == E
     assert chk(n_top=-1) == E and chk(n_top=_lib.TOP_MAX + 1) == E
     assert chk(top_id=DEV, n_top=20, top_ld=19) == E
-    assert chk(row_lse=DEV, allowed=DEV, allowed_words=7760, allowed_ld=7760) == E
-    assert chk(row_max=DEV, controls=DEV) == E
+    # held_row outputs over the raw row beside a masked or controlled draw
+    assert chk(row_lse=DEV, allowed=DEV, allowed_words=7760, allowed_ld=7760) == OK
+    assert chk(row_max=DEV, controls=DEV) == OK
     narrow = Limits(8, 300_000, 15)                               # 15 chunks < 16 needed
     assert host.xs_host_check_sample(C.byref(narrow), C.byref(_sample())) == CAP
 
@@ -87,8 +88,9 @@ def test_scoring_argument_checks(host):
     assert chk(class_masks=DEV, n_class=2, class_ld=7760) == E
     assert chk(class_masks=DEV, class_mass=DEV, n_class=_lib.CLASS_MAX + 1, class_ld=7760) == E
     assert chk(probs=DEV, probs_ld=248_320) == OK and chk(probs=DEV, probs_ld=248_319) == E
-    assert chk(probs=DEV, probs_ld=248_320, allowed=DEV, allowed_words=7760, allowed_ld=7760) == E
-    assert chk(score_ids=DEV, score_logprob=DEV, n_score=1, score_ld=1, controls=DEV) == E
+    # the scoring reads of the raw row beside a masked or controlled draw
+    assert chk(probs=DEV, probs_ld=248_320, allowed=DEV, allowed_words=7760, allowed_ld=7760) == OK
+    assert chk(score_ids=DEV, score_logprob=DEV, n_score=1, score_ld=1, controls=DEV) == OK
     assert chk(top_logprob64=DEV, n_top=20, top_ld=19) == E
 
 

@@ -62,8 +62,6 @@ int xs_host_check_sample(const xs_host_limits* lim, const xs_sample_args* in) {
   if (in->class_masks && (in->n_class < 0 || in->n_class > XS_CLASS_MAX || in->class_ld < (in->enc + 31) / 32))
     return XS_ERR_ARG;
   if (in->probs && in->probs_ld < in->enc) return XS_ERR_ARG;
-  const bool lse = xs_host_wants_lse(in);
-  if (lse && (in->allowed || in->controls)) return XS_ERR_ARG;
   if (in->row_order) {  // a permutation of 0..rows-1 (a longer one is checked, then not applied)
     uint64_t small[XS_ORDER_MAX / 64] = {};
     std::vector<uint64_t> large;

@@ -344,12 +344,15 @@ XS_DEV Cfg make_cfg(const xs_row_params& p, int64_t enc, int n_top, int k_max, i
   return c;
 }
 
-XS_DEV Cfg greedy_cfg() {
+// Every row greedy at T 1 (argmax_probs, and the held_row launch of a call
+// that also masks or controls its rows): the streaming selection keeps the
+// argmax and, when asked, the n_top highest logits.
+XS_DEV Cfg greedy_cfg(int n_top, int64_t enc) {
   Cfg c;
   c.inv = 1.0f;
   c.top_p = 1.0f;
   c.k = 0;
-  c.kp = 1;
+  c.kp = n_top > 0 ? (int)min((int64_t)n_top, enc) : 1;
   c.greedy = true;
   c.scale = c.full = c.bad = c.big = c.force = false;
   c.dthr = 0.0f;
@@ -3153,7 +3156,7 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
   }
   // The row's parameters are read only now, so that round trip overlaps the
   // loads instead of delaying them.
-  const Cfg cfg = a.greedy_all ? greedy_cfg() : make_cfg(a.params[row], a.enc, a.n_top, a.k_max, a.ser_force);
+  const Cfg cfg = a.greedy_all ? greedy_cfg(a.n_top, a.enc) : make_cfg(a.params[row], a.enc, a.n_top, a.k_max, a.ser_force);
   const bool stoch = !cfg.greedy && !cfg.bad;
   const int kp = cfg.kp;
   // Sparse controls: the chunk's patches (final values written by
@@ -3650,7 +3653,7 @@ __global__ __launch_bounds__(BLOCK) void finalize_kernel(Args a) {
   // the row's headers first: their round trip overlaps the row's parameters
   uint64_t h[NHW], E[EPRE];
   load_heads<WANT_LSE, true>(rowrec, nsp, nc * NWAVE, h, E);
-  const Cfg cfg = a.greedy_all ? greedy_cfg() : make_cfg(a.params[row], a.enc, a.n_top, a.k_max, a.ser_force);
+  const Cfg cfg = a.greedy_all ? greedy_cfg(a.n_top, a.enc) : make_cfg(a.params[row], a.enc, a.n_top, a.k_max, a.ser_force);
   if (threadIdx.x == 0) st_agent(&a.row_ticket[row * TSTRIDE + 1], 0);  // held_row's running max key
   if (a.serial && serial_row<HAS_MASK, HAS_CTL>(a, cfg, row)) return;  // serial_kernel finalizes it
   const float* rowp = a.logits + (int64_t)row * a.ld;
@@ -4425,7 +4428,7 @@ XS_DEV void count_digit(uint32_t* cnt, uint32_t d, bool valid) {
 // The row's whole-row state for the kernels below: null when the call does not
 // draw the row on this path.
 XS_DEV const BigRow* big_live(const Args& a, int row, Cfg& cfg) {
-  cfg = a.greedy_all ? greedy_cfg() : make_cfg(a.params[row], a.enc, a.n_top, a.k_max, a.ser_force);
+  cfg = a.greedy_all ? greedy_cfg(a.n_top, a.enc) : make_cfg(a.params[row], a.enc, a.n_top, a.k_max, a.ser_force);
   if (!cfg.big || cfg.bad) return nullptr;  // (then big_state[row] is not this call's)
   const BigRow* br = a.big_state + row;
   return br->state ? br : nullptr;
@@ -5424,12 +5427,52 @@ int sample_impl(xs_context* ctx, const xs_sample_args* in, bool clear_tickets) {
   // rows at top_p >= 1; every other controlled row draws with the exact sum,
   // and a row whose token that sum does not settle is summed serially by its
   // finalizer (draw_settled, ser_local)
-  const bool serial = in->cand_id || in->cand_w || in->soft_sum;
+  bool serial = in->cand_id || in->cand_w || in->soft_sum;
   // (the launch's arguments carry an order of at most XS_ORDER_MAX rows)
   const int32_t* order = in->rows <= XS_ORDER_MAX ? in->row_order : nullptr;
-  const int lrc = launch(ctx, a, in->rows, 1, in->allowed != nullptr, lse, serial, order);
+  const bool masked = in->allowed != nullptr || in->controls != nullptr;
+  if (lse && masked) {
+    // held_row reads the raw row (generate.rs:1905-1933), whatever mask or
+    // controls the draw takes: the masked draw runs without the held_row
+    // outputs, then a second pass over the raw rows, every row greedy at T 1,
+    // writes them (its tokens and statuses land in row_status, unread)
+    xs::Args d = a;
+    d.row_max = nullptr;
+    d.row_lse = nullptr;
+    d.n_top = 0;
+    d.top_id = nullptr;
+    d.top_logprob = nullptr;
+    d.top_logprob64 = nullptr;
+    d.n_score = 0;
+    d.score_ids = nullptr;
+    d.n_class = 0;
+    d.class_masks = nullptr;
+    d.probs = nullptr;
+    const int drc = launch(ctx, d, in->rows, 1, in->allowed != nullptr, false, serial, order);
+    if (drc != XS_OK) return drc;
+    a.params = nullptr;
+    a.uniforms = nullptr;
+    a.allowed = nullptr;
+    a.controls = nullptr;
+    a.ctl_ids = nullptr;
+    a.ctl_delta = nullptr;
+    a.token = ctx->row_status;
+    a.status = ctx->row_status;
+    a.cand_id = nullptr;
+    a.cand_w = nullptr;
+    a.n_cand = nullptr;
+    a.soft_max = nullptr;
+    a.soft_sum = nullptr;
+    a.greedy_all = 1;
+    order = nullptr;
+    serial = false;
+  }
+  const int lrc = launch(ctx, a, in->rows, 1, a.allowed != nullptr, lse, serial, order);
   if (lrc != XS_OK || !scores || in->rows == 0) return lrc;
-  // the scoring reads, once every row's lse is written
+  // the scoring reads, once every row's lse is written (an id out of range
+  // fails the caller's row)
+  a.token = in->token;
+  a.status = in->status;
   hipLaunchKernelGGL(xs::score_kernel, dim3((unsigned)(in->rows * a.n_chunks)), dim3(xs::BLOCK), 0, ctx->stream, a);
   return hipGetLastError() == hipSuccess ? XS_OK : XS_ERR_HIP;
 }

@@ -3,8 +3,12 @@
 held_row (src/generate.rs:1905-1933) reads the raw logit row; the allow-mask
 and SampleControl (src/sampler.rs:85-121) shape only the draw.  A call that
 asks for both gets the masked draw and the raw row's statistics: bit for bit
-what the same call without the held outputs draws, and what a call without
-mask or controls reports for the held outputs; both are also held to the
+what the same call without the held outputs draws, and the row_max and
+top ids a call without mask or controls reports.  The f64 log-sums (row_lse,
+the log-probs) agree with that call's to the held_row bar: held_row's serial
+fold is emulated by partial sums whose grouping follows the finalizer a row's
+draw takes, so their last bits may differ between the two calls (both stay
+within the bar of the reference's fold).  Everything is also held to the
 oracle.  Row counts of 24 (each row spread over the XCDs) and 72 (the
 XCD-local hand-off) are covered."""
 import numpy as np
@@ -12,12 +16,11 @@ import pytest
 
 from tests import workloads
 from tests.test_gpu_random_sweep import _batch, _control_batch
-from tests.test_gpu_sampler import check_held_row, check_rows, dev
+from tests.test_gpu_sampler import PROB_RTOL, check_held_row, check_rows, dev
 
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
 
-HELD = ("row_max", "row_lse", "top_id", "top_logprob", "top_logprob64")
 SCORES = ("score_logprob", "class_mass", "probs")
 
 
@@ -55,6 +58,20 @@ def same_bits(a, b, keys, tag):
         np.testing.assert_array_equal(x, y, err_msg=f"{tag}: {k}")
 
 
+def close_held(a, b, tag, extra=()):
+    """row_max and the top ids bit for bit; the f64 log-sums and what they
+    normalize (log-probs, scores, class masses, probabilities) within the
+    held_row bar: 1e-5 relative with a floor of eight f64 ulps of lse."""
+    same_bits(a, b, ("row_max", "top_id"), tag)
+    lse = b["row_lse"].astype(np.float64)
+    floor = 8 * np.spacing(np.abs(lse))
+    for k in ("row_lse", "top_logprob", "top_logprob64") + tuple(extra):
+        x, y = a[k].astype(np.float64), b[k].astype(np.float64)
+        fl = floor.reshape((-1,) + (1,) * (x.ndim - 1))
+        bad = ~((np.abs(x - y) <= PROB_RTOL * np.abs(y) + fl) | (np.isnan(x) & np.isnan(y)))
+        assert not bad.any(), (tag, k, np.argwhere(bad)[:5].tolist())
+
+
 def _cases():
     out = []
     for b, rows in ((3, 24), (7, 72)):
@@ -74,7 +91,7 @@ def test_held_row_beside_a_masked_draw(ctx, oracle, case):
     draw = call(ctx, x, T, K, P, U, mask=mask, ctls=ctls, cand_k=20, stats=True)
     raw = call(ctx, x, T, K, P, U, n_top=n_top)
     same_bits(both, draw, [k for k in draw], tag + " (the draw)")
-    same_bits(both, raw, HELD, tag + " (held_row over the raw row)")
+    close_held(both, raw, tag + " (held_row over the raw row)")
     check_rows(oracle, x, T, K, P, U, both, mask=mask, ctls=ctls, label=tag)
     for r in range(x.shape[0]):
         check_held_row(oracle, x[r], both, r, n_top, label=tag)
@@ -101,7 +118,7 @@ def test_scoring_reads_beside_a_masked_draw(ctx):
     keep = np.arange(rows) != 5
     for k in draw:
         np.testing.assert_array_equal(both[k][keep], draw[k][keep], err_msg=k)
-    same_bits(both, raw, HELD + SCORES, tag + " scoring reads")
+    close_held(both, raw, tag + " scoring reads", extra=SCORES)
     assert np.isnan(both["score_logprob"][5, 2])
 
 

@@ -5215,6 +5215,8 @@ int launch(xs_context* ctx, xs::Args& a, int64_t rows, int span, bool mask, bool
   a.xcd_test = ctx->xcd_test;
   const int64_t gpad = (rows + nx - 1) / nx * nx * (int64_t)a.n_chunks;
   if (gpad > 0x7FFFFFFF || span < 1) return XS_ERR_CAPACITY;
+  // (no instantiation streams a masked or controlled row with held_row's
+  // statistics: sample_impl splits such a call into two launches)
   if ((mask || ctl) && lse) return XS_ERR_ARG;
   a.patch = ctx->ctl_patch;
   a.ctl_keys = ctx->ctl_keys;

@@ -475,6 +475,11 @@ struct Args {
   // count, or 1), nrows of them; xcd_test 2 makes the rows of several chunks
   // fail their placement check (a test hook)
   int32_t xcd_log2, nrows, xcd_test;
+  // held_fold's re-reads are shared by the finalizing workgroup's four waves
+  // (1) or left to its first wave (0): shared when the launch's workgroups
+  // fit on the device at once, so that the waves that wait for the first
+  // wave's finalization hold no slot another workgroup needs
+  int32_t fold_shared;
   uint64_t* ser_sum;  // [rows, ser_ld, 2]: segment summaries
   uint64_t* ser_e;    // [rows, SER_NB, SEG / 2]: kept segments' terms, two f32 per word
   int64_t ser_ld;     // segments per row of ser_sum
@@ -1101,13 +1106,14 @@ XS_DEV double exp_f64(double x, TAB T) {
   return v * __longlong_as_double((long long)((uint64_t)(e + 1023) << 52));
 }
 
-// The workgroup's four waves share the re-reads (one sub-record each at a
-// time, all 16 slots' loads in flight); wave 0 adds the partials of the
-// sub-records wholly before the argmax.  Then wave 0 writes row_lse and the
-// top-n log-probs.  Contains barriers: all waves of the workgroup call it.
-template <int NW, bool LOC>
+// The workgroup's first nw waves (1, or all four) share the re-reads (one
+// sub-record each at a time, all 16 slots' loads in flight); wave 0 adds the
+// partials of the sub-records wholly before the argmax.  Then wave 0 writes
+// row_lse and the top-n log-probs.  With nw > 1 it contains a barrier: all
+// waves of the workgroup call it.
+template <bool LOC>
 XS_DEV void held_fold(const Args& a, int row, const float* rowp, const uint64_t* rowrec, int nsp,
-                      int nsub, FinLds& F) {
+                      int nsub, FinLds& F, int nw) {
   HeldLds& H = F.held;
   const int lane = lane_id(), wave = wave_id();
   const int enc = (int)a.enc;
@@ -1168,7 +1174,7 @@ XS_DEV void held_fold(const Args& a, int row, const float* rowp, const uint64_t*
       while (m) {  // one sub-record's elements: wave w of chunk cc
         const int sr = g * 64 + (int)__builtin_ctzll(m);
         m &= m - 1ull;
-        if ((nth++ % NW) != wave) continue;
+        if ((nth++ % nw) != wave) continue;
         const int cc = sr / NWAVE, w = sr % NWAVE;
         float4 v[SPC];
 #pragma unroll
@@ -1210,14 +1216,13 @@ XS_DEV void held_fold(const Args& a, int row, const float* rowp, const uint64_t*
     H.pre[wave] = pre;
     H.post[wave] = post;
   }
-  if (NW > 1) __syncthreads();
+  if (nw > 1) __syncthreads();
   if (wave != 0) return;
   double D = R_d;
   if (fold) {
     double p4 = 0.0;
     long long q4 = 0;
-#pragma unroll
-    for (int w = 0; w < NW; w++) {
+    for (int w = 0; w < nw; w++) {
       p4 += H.pre[w];
       q4 += H.post[w];
     }
@@ -3618,18 +3623,46 @@ __global__ __launch_bounds__(BLOCK) __attribute__((amdgpu_waves_per_eu(4, 8))) v
   // summed serially by the same wave and finalized again (ser_fallback).
   // A row whose workgroups did not all run on this XCD (Lc.last 2) has
   // sub-records outside this L2: it is failed, not read, and its sequence's
-  // walk stops at it.
-  if (wave != 0) return;
+  // walk stops at it.  In a launch whose workgroups fit on the device at
+  // once, held_fold's re-reads (a whole row, on a row whose fold leaves every
+  // term above 2^-53) are shared by the four waves: the other three wait at
+  // one barrier for the first wave's finalization (whose code holds no
+  // barrier) and leave after the fold.
+  if constexpr (!WANT_LSE) {  // (the first wave alone)
+    if (wave != 0) return;
+    const bool placed = !LOC || Lc.last == 1;
+    if (placed) {
+      finalize_row<HAS_MASK, WANT_LSE, HAS_CTL, LOC>(a, cfg, row, rowrec, nsp, nc * NWAVE, rowp, mrow, Tl.fin);
+      if (HAS_MASK || HAS_CTL) ser_fallback<HAS_MASK, WANT_LSE, HAS_CTL, LOC>(a, cfg, row, rowrec, nsp, nc * NWAVE, rowp, mrow, Tl);
+    } else if (lane == 0) {
+      st_agent(&a.token[row], -1);
+      st_agent(&a.status[row], XS_ROW_INTERNAL);
+      if (a.n_cand) a.n_cand[row] = 0;
+      if (cfg.big && a.big_state) a.big_state[row].state = 0;  // the whole-row kernels pass it by
+    }
+    if (a.span > 0 && (!placed || !deferred(cfg, Tl.fin))) verify_walk(a, row);
+    return;
+  }
   const bool placed = !LOC || Lc.last == 1;
-  if (placed) {
-    finalize_row<HAS_MASK, WANT_LSE, HAS_CTL, LOC>(a, cfg, row, rowrec, nsp, nc * NWAVE, rowp, mrow, Tl.fin);
-    if (HAS_MASK || HAS_CTL) ser_fallback<HAS_MASK, WANT_LSE, HAS_CTL, LOC>(a, cfg, row, rowrec, nsp, nc * NWAVE, rowp, mrow, Tl);
-    if (held) held_fold<1, LOC>(a, row, rowp, rowrec, nsp, nc * NWAVE, Tl.fin);
-  } else if (lane == 0) {
-    st_agent(&a.token[row], -1);
-    st_agent(&a.status[row], XS_ROW_INTERNAL);
-    if (a.n_cand) a.n_cand[row] = 0;
-    if (cfg.big && a.big_state) a.big_state[row].state = 0;  // the whole-row kernels pass it by
+  const bool shared = held && placed && a.fold_shared;  // (uniform)
+  if (wave != 0 && !shared) return;
+  if (wave == 0) {
+    if (placed) {
+      finalize_row<HAS_MASK, WANT_LSE, HAS_CTL, LOC>(a, cfg, row, rowrec, nsp, nc * NWAVE, rowp, mrow, Tl.fin);
+      if (HAS_MASK || HAS_CTL) ser_fallback<HAS_MASK, WANT_LSE, HAS_CTL, LOC>(a, cfg, row, rowrec, nsp, nc * NWAVE, rowp, mrow, Tl);
+    } else if (lane == 0) {
+      st_agent(&a.token[row], -1);
+      st_agent(&a.status[row], XS_ROW_INTERNAL);
+      if (a.n_cand) a.n_cand[row] = 0;
+      if (cfg.big && a.big_state) a.big_state[row].state = 0;  // the whole-row kernels pass it by
+    }
+  }
+  if constexpr (WANT_LSE) {
+    if (held && placed) {
+      if (shared) __syncthreads();  // the first wave's finalization is in LDS
+      held_fold<LOC>(a, row, rowp, rowrec, nsp, nc * NWAVE, Tl.fin, shared ? NWAVE : 1);
+      if (wave != 0) return;
+    }
   }
   if (a.span > 0 && (!placed || !deferred(cfg, Tl.fin))) verify_walk(a, row);
 }
@@ -3646,22 +3679,30 @@ template <bool HAS_MASK, bool WANT_LSE, bool HAS_CTL>
 __global__ __launch_bounds__(BLOCK) void finalize_kernel(Args a) {
   __shared__ TailLds Tl;
   const int row = blockIdx.x;
-  if (wave_id() != 0) return;  // one wave finalizes the row
   const int nc = a.n_chunks;
   const int nsp = ((nc * NWAVE + 63) >> 6) << 6;
   const uint64_t* const rowrec = a.rec + (int64_t)row * SRECW * nsp;
+  const bool held = WANT_LSE && (a.row_lse != nullptr || a.n_top > 0);
+  const bool shared = held && a.fold_shared;  // as sample_kernel's finalizer
+  const int wave = wave_id();
+  if (wave != 0 && !shared) return;  // one wave finalizes the row; all four may share held_fold
   // the row's headers first: their round trip overlaps the row's parameters
   uint64_t h[NHW], E[EPRE];
-  load_heads<WANT_LSE, true>(rowrec, nsp, nc * NWAVE, h, E);
+  if (wave == 0) load_heads<WANT_LSE, true>(rowrec, nsp, nc * NWAVE, h, E);
   const Cfg cfg = a.greedy_all ? greedy_cfg(a.n_top, a.enc) : make_cfg(a.params[row], a.enc, a.n_top, a.k_max, a.ser_force);
   if (threadIdx.x == 0) st_agent(&a.row_ticket[row * TSTRIDE + 1], 0);  // held_row's running max key
   if (a.serial && serial_row<HAS_MASK, HAS_CTL>(a, cfg, row)) return;  // serial_kernel finalizes it
   const float* rowp = a.logits + (int64_t)row * a.ld;
   const uint32_t* mrow = HAS_MASK ? a.allowed + (int64_t)row * a.allowed_ld : nullptr;
-  const bool held = WANT_LSE && (a.row_lse != nullptr || a.n_top > 0);
-  finalize_heads<HAS_MASK, WANT_LSE, HAS_CTL, true>(a, cfg, row, rowrec, nsp, nc * NWAVE, rowp, mrow, Tl.fin, h, E);
-  if (HAS_MASK || HAS_CTL) ser_fallback<HAS_MASK, WANT_LSE, HAS_CTL, true>(a, cfg, row, rowrec, nsp, nc * NWAVE, rowp, mrow, Tl);
-  if (held) held_fold<1, true>(a, row, rowp, rowrec, nsp, nc * NWAVE, Tl.fin);
+  if (wave == 0) {
+    finalize_heads<HAS_MASK, WANT_LSE, HAS_CTL, true>(a, cfg, row, rowrec, nsp, nc * NWAVE, rowp, mrow, Tl.fin, h, E);
+    if (HAS_MASK || HAS_CTL) ser_fallback<HAS_MASK, WANT_LSE, HAS_CTL, true>(a, cfg, row, rowrec, nsp, nc * NWAVE, rowp, mrow, Tl);
+  }
+  if (held) {
+    if (shared) __syncthreads();  // the first wave's finalization is in LDS
+    held_fold<true>(a, row, rowp, rowrec, nsp, nc * NWAVE, Tl.fin, shared ? NWAVE : 1);
+    if (wave != 0) return;
+  }
   if (a.span > 0 && !deferred(cfg, Tl.fin)) verify_walk(a, row);
 }
 
@@ -5214,6 +5255,7 @@ int launch(xs_context* ctx, xs::Args& a, int64_t rows, int span, bool mask, bool
   a.nrows = (int32_t)rows;
   a.xcd_test = ctx->xcd_test;
   const int64_t gpad = (rows + nx - 1) / nx * nx * (int64_t)a.n_chunks;
+  a.fold_shared = gpad <= 4 * (int64_t)ctx->n_cu ? 1 : 0;  // (alike for a split launch of the same call)
   if (gpad > 0x7FFFFFFF || span < 1) return XS_ERR_CAPACITY;
   // (no instantiation streams a masked or controlled row with held_row's
   // statistics: sample_impl splits such a call into two launches)
